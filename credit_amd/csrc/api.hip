@@ -1,0 +1,243 @@
+// Host plumbing of libcredit_hip.so: errors, argument checks, device
+// properties, the workspace cache and the watchdog query.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "api_internal.hpp"
+
+namespace credit {
+
+namespace {
+thread_local char g_last_error[512] = "";
+
+struct Workspace {
+  char* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::vector<Workspace> g_ws;  // indexed by device
+
+std::mutex g_props_mutex;
+std::vector<DeviceProps> g_props;
+}  // namespace
+
+int set_error(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int hip_failure(hipError_t err, const char* what) {
+  return set_error(CREDIT_ERR_HIP, "%s failed: %s (%d)", what,
+                   hipGetErrorString(err), static_cast<int>(err));
+}
+
+int check_ptr(const void* p, const char* name) {
+  if (p == nullptr) return set_error(CREDIT_ERR_NULL_POINTER, "%s is NULL", name);
+  return CREDIT_OK;
+}
+
+int check_aligned(const void* p, size_t align, const char* name) {
+  if (reinterpret_cast<uintptr_t>(p) % align != 0)
+    return set_error(CREDIT_ERR_ALIGNMENT, "%s is not %zu-byte aligned", name,
+                     align);
+  return CREDIT_OK;
+}
+
+int check_shape(int64_t rows, int64_t cols, int64_t max_cols) {
+  if (rows < 0 || cols < 1)
+    return set_error(CREDIT_ERR_BAD_SHAPE,
+                     "shape (%lld, %lld): need rows >= 0 and cols >= 1",
+                     static_cast<long long>(rows), static_cast<long long>(cols));
+  if (cols > max_cols)
+    return set_error(CREDIT_ERR_BAD_SHAPE, "cols %lld exceeds the maximum %lld",
+                     static_cast<long long>(cols),
+                     static_cast<long long>(max_cols));
+  if (rows > (int64_t{1} << 31) - 1)
+    return set_error(CREDIT_ERR_BAD_SHAPE, "rows %lld exceeds 2^31-1",
+                     static_cast<long long>(rows));
+  return CREDIT_OK;
+}
+
+int check_cfg(const credit_cfg* cfg) {
+  if (cfg == nullptr) return CREDIT_OK;
+  if (cfg->variant < CREDIT_VARIANT_AUTO || cfg->variant > CREDIT_VARIANT_SPLIT)
+    return set_error(CREDIT_ERR_BAD_CONFIG, "unknown variant %d", cfg->variant);
+  if (cfg->split < 0 || cfg->split > 64)
+    return set_error(CREDIT_ERR_BAD_CONFIG, "split %d outside [0, 64]",
+                     cfg->split);
+  if (cfg->workspace != nullptr &&
+      reinterpret_cast<uintptr_t>(cfg->workspace) % 256 != 0)
+    return set_error(CREDIT_ERR_WORKSPACE, "workspace is not 256-byte aligned");
+  return CREDIT_OK;
+}
+
+int current_device_props(const DeviceProps** out) {
+  int dev = 0;
+  CREDIT_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_props_mutex);
+  if (static_cast<int>(g_props.size()) <= dev) g_props.resize(dev + 1);
+  DeviceProps& p = g_props[dev];
+  if (p.device != dev) {
+    hipDeviceProp_t prop;
+    CREDIT_HIP(hipGetDeviceProperties(&prop, dev));
+    p.cu_count = prop.multiProcessorCount;
+    p.max_lds_per_block = static_cast<int>(prop.sharedMemPerBlock);
+    p.lds_per_cu = static_cast<int>(prop.maxSharedMemoryPerMultiProcessor);
+    p.clock_khz = prop.clockRate;
+    p.cooperative = prop.cooperativeLaunch;
+    p.l2_bytes = prop.l2CacheSize;
+    // gfx950 (MI355X) carries 32 CUs per XCD; the XCD count is what the
+    // blockIdx -> XCD round-robin mapping needs.
+    p.xcd_count = p.cu_count >= 32 ? p.cu_count / 32 : 1;
+    p.device = dev;
+  }
+  *out = &p;
+  return CREDIT_OK;
+}
+
+int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base) {
+  const size_t need = kWorkspaceHeader + bytes;
+  if (cfg != nullptr && cfg->workspace != nullptr) {
+    if (cfg->workspace_bytes < need)
+      return set_error(CREDIT_ERR_WORKSPACE,
+                       "workspace of %zu bytes is smaller than the %zu needed",
+                       cfg->workspace_bytes, need);
+    *base = static_cast<char*>(cfg->workspace);
+    return CREDIT_OK;
+  }
+  int dev = 0;
+  CREDIT_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  if (static_cast<int>(g_ws.size()) <= dev) g_ws.resize(dev + 1);
+  Workspace& ws = g_ws[dev];
+  if (ws.bytes < need) {
+    if (ws.ptr != nullptr) {
+      // Earlier calls may still use the old buffer.
+      CREDIT_HIP(hipDeviceSynchronize());
+      CREDIT_HIP(hipFree(ws.ptr));
+      ws.ptr = nullptr;
+      ws.bytes = 0;
+    }
+    size_t grow = align_up(need < (size_t{1} << 20) ? (size_t{1} << 20) : need,
+                           size_t{1} << 20);
+    void* p = nullptr;
+    CREDIT_HIP(hipMalloc(&p, grow));
+    CREDIT_HIP(hipMemset(p, 0, grow));
+    CREDIT_HIP(hipDeviceSynchronize());
+    ws.ptr = static_cast<char*>(p);
+    ws.bytes = grow;
+  }
+  *base = ws.ptr;
+  return CREDIT_OK;
+}
+
+int cu_count_or_default() {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  const DeviceProps* p = nullptr;
+  if (current_device_props(&p) != CREDIT_OK) return 256;
+  return p->cu_count;
+}
+
+int check_launch(const char* kernel) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return hip_failure(err, kernel);
+  return CREDIT_OK;
+}
+
+}  // namespace credit
+
+using namespace credit;
+
+extern "C" {
+
+const char* credit_version(void) { return "credit-hip 0.1.0 gfx950"; }
+
+const char* credit_last_error(void) { return g_last_error; }
+
+const char* credit_status_string(int status) {
+  switch (status) {
+    case CREDIT_OK: return "CREDIT_OK";
+    case CREDIT_ERR_NULL_POINTER: return "CREDIT_ERR_NULL_POINTER";
+    case CREDIT_ERR_BAD_SHAPE: return "CREDIT_ERR_BAD_SHAPE";
+    case CREDIT_ERR_ALIGNMENT: return "CREDIT_ERR_ALIGNMENT";
+    case CREDIT_ERR_UNSUPPORTED: return "CREDIT_ERR_UNSUPPORTED";
+    case CREDIT_ERR_WORKSPACE: return "CREDIT_ERR_WORKSPACE";
+    case CREDIT_ERR_HIP: return "CREDIT_ERR_HIP";
+    case CREDIT_ERR_WATCHDOG: return "CREDIT_ERR_WATCHDOG";
+    case CREDIT_ERR_BAD_CONFIG: return "CREDIT_ERR_BAD_CONFIG";
+    default: return "CREDIT_ERR_UNKNOWN";
+  }
+}
+
+int credit_query_device(int32_t device, credit_device_info* info) {
+  CREDIT_TRY(check_ptr(info, "info"));
+  if (device < 0) return set_error(CREDIT_ERR_BAD_CONFIG, "device %d < 0", device);
+  int count = 0;
+  CREDIT_HIP(hipGetDeviceCount(&count));
+  if (device >= count)
+    return set_error(CREDIT_ERR_BAD_CONFIG, "device %d of %d", device, count);
+  hipDeviceProp_t prop;
+  CREDIT_HIP(hipGetDeviceProperties(&prop, device));
+  memset(info, 0, sizeof(*info));
+  snprintf(info->name, sizeof(info->name), "%s", prop.name);
+  snprintf(info->arch, sizeof(info->arch), "%s", prop.gcnArchName);
+  info->device = device;
+  info->cu_count = prop.multiProcessorCount;
+  info->xcd_count = prop.multiProcessorCount >= 32 ? prop.multiProcessorCount / 32 : 1;
+  info->wave_size = prop.warpSize;
+  info->max_threads_per_block = prop.maxThreadsPerBlock;
+  info->cooperative_launch = prop.cooperativeLaunch;
+  info->lds_bytes_per_block = static_cast<int64_t>(prop.sharedMemPerBlock);
+  info->lds_bytes_per_cu =
+      static_cast<int64_t>(prop.maxSharedMemoryPerMultiProcessor);
+  info->l2_bytes = prop.l2CacheSize;
+  info->hbm_bytes = static_cast<int64_t>(prop.totalGlobalMem);
+  info->clock_khz = prop.clockRate;
+  info->mem_clock_khz = prop.memoryClockRate;
+  info->mem_bus_width_bits = prop.memoryBusWidth;
+  return CREDIT_OK;
+}
+
+size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
+                              int32_t variant, int32_t split) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const int cus = cu_count_or_default();
+  size_t body = 0;
+  switch (op) {
+    case CREDIT_OP_ROW_SUM_MAX:
+      body = row_sum_max_workspace(rows, cols, variant, split, cus);
+      break;
+    default:
+      body = 0;
+  }
+  return body == 0 ? 0 : kWorkspaceHeader + body;
+}
+
+int credit_check_watchdog(const credit_cfg* cfg) {
+  CREDIT_TRY(check_cfg(cfg));
+  char* base = nullptr;
+  CREDIT_TRY(acquire_workspace(cfg, 0, &base));
+  uint32_t flag = 0;
+  CREDIT_HIP(hipStreamSynchronize(cfg_stream(cfg)));
+  CREDIT_HIP(hipMemcpy(&flag, base, sizeof(flag), hipMemcpyDeviceToHost));
+  if (flag != 0) {
+    const uint32_t zero = 0;
+    CREDIT_HIP(hipMemcpy(base, &zero, sizeof(zero), hipMemcpyHostToDevice));
+    return set_error(CREDIT_ERR_WATCHDOG,
+                     "a split-row barrier exceeded its spin limit");
+  }
+  return CREDIT_OK;
+}
+
+}  // extern "C"

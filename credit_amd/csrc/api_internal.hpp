@@ -1,0 +1,80 @@
+// Host-side plumbing shared by every C-ABI entry point: status codes and the
+// thread-local error text, argument checks that run before anything touches
+// the GPU, the per-device workspace cache and device-property cache.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/credit.h"
+
+namespace credit {
+
+int set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_failure(hipError_t err, const char* what);
+
+#define CREDIT_HIP(expr)                                       \
+  do {                                                         \
+    hipError_t credit_err__ = (expr);                          \
+    if (credit_err__ != hipSuccess)                            \
+      return ::credit::hip_failure(credit_err__, #expr);       \
+  } while (0)
+
+#define CREDIT_TRY(expr)                 \
+  do {                                   \
+    int credit_status__ = (expr);        \
+    if (credit_status__ != CREDIT_OK)    \
+      return credit_status__;            \
+  } while (0)
+
+struct DeviceProps {
+  int device = -1;
+  int cu_count = 0;
+  int xcd_count = 0;
+  int max_lds_per_block = 0;
+  int lds_per_cu = 0;
+  int clock_khz = 0;
+  int cooperative = 0;
+  long long l2_bytes = 0;
+};
+
+// Cached hipGetDeviceProperties for the current device.
+int current_device_props(const DeviceProps** out);
+
+// Argument checks.  Every one returns CREDIT_OK or a negative status after
+// recording a message; none of them calls into HIP.
+int check_ptr(const void* p, const char* name);
+int check_aligned(const void* p, size_t align, const char* name);
+int check_shape(int64_t rows, int64_t cols, int64_t max_cols);
+int check_cfg(const credit_cfg* cfg);
+
+inline hipStream_t cfg_stream(const credit_cfg* cfg) {
+  return cfg ? static_cast<hipStream_t>(cfg->stream) : nullptr;
+}
+inline int cfg_variant(const credit_cfg* cfg) {
+  return cfg ? cfg->variant : CREDIT_VARIANT_AUTO;
+}
+inline int cfg_split(const credit_cfg* cfg) { return cfg ? cfg->split : 0; }
+
+// Workspace: a zero-filled device buffer whose first 256 bytes hold the
+// watchdog word the split-row barrier raises.  Uses the caller's buffer when
+// cfg->workspace is set (it must be at least `bytes` long, 256-byte aligned,
+// and zero-filled before its first use), otherwise a per-device buffer the
+// library keeps for the life of the process.
+constexpr size_t kWorkspaceHeader = 256;
+int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base);
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Launch helpers that turn a launch failure into a status.
+int check_launch(const char* kernel);
+
+// Workspace sizes of the individual operations (bytes after the header).
+size_t row_sum_max_workspace(int64_t rows, int64_t cols, int variant, int split,
+                             int cu_count);
+
+// CU count of the current device, or 256 (MI355X) when none is visible.
+int cu_count_or_default();
+
+}  // namespace credit

@@ -1,0 +1,214 @@
+// C2: LayerNorm forward, bf16 in/out with fp32 statistics.
+//
+// y = (x - mean) * rstd * gamma + beta,  mean = sum(x)/N,
+// var = sum((x - mean)^2)/N (two-pass, the form of dsmem_eval/workloads.py:54-56),
+// rstd = 1/sqrt(var + eps).  The reference only has the backward kernel; its
+// statistics pass is src/workloads/layernorm_backward.cu:286-295.
+//
+// Variants:
+//  - STAGED: one workgroup per row, the row held in VGPRs as packed bf16
+//            (VPT dwordx4 per lane), both statistics passes and the output
+//            pass run from registers: one HBM read of x, one write of y.
+//  - READ  : one workgroup per row streaming the row three times (sum, sum of
+//            squared deviations, output), for shapes the staged layout does
+//            not cover (cols not a multiple of 8, misaligned rows, very wide
+//            rows).
+// Algorithmic traffic per row: 2*cols (x) + 2*cols (y) + 8 (mean, rstd) bytes,
+// plus 4*cols once for gamma and beta.
+#include "api_internal.hpp"
+#include "common.hpp"
+
+namespace credit {
+namespace {
+
+__device__ __forceinline__ float sum8(u32x4 v) {
+  return ((bf16_lo(v.x) + bf16_hi(v.x)) + (bf16_lo(v.y) + bf16_hi(v.y))) +
+         ((bf16_lo(v.z) + bf16_hi(v.z)) + (bf16_lo(v.w) + bf16_hi(v.w)));
+}
+
+__device__ __forceinline__ float sqdev8(u32x4 v, float mu) {
+  float a = bf16_lo(v.x) - mu, b = bf16_hi(v.x) - mu;
+  float c = bf16_lo(v.y) - mu, d = bf16_hi(v.y) - mu;
+  float e = bf16_lo(v.z) - mu, f = bf16_hi(v.z) - mu;
+  float g = bf16_lo(v.w) - mu, h = bf16_hi(v.w) - mu;
+  return ((a * a + b * b) + (c * c + d * d)) + ((e * e + f * f) + (g * g + h * h));
+}
+
+__device__ __forceinline__ uint32_t norm2(uint32_t xv, uint32_t gv, uint32_t bv,
+                                          float mu, float rs) {
+  const float lo = (bf16_lo(xv) - mu) * rs * bf16_lo(gv) + bf16_lo(bv);
+  const float hi = (bf16_hi(xv) - mu) * rs * bf16_hi(gv) + bf16_hi(bv);
+  return pack_bf16x2(lo, hi);
+}
+
+__device__ __forceinline__ u32x4 norm8(u32x4 xv, u32x4 gv, u32x4 bv, float mu,
+                                       float rs) {
+  return u32x4{norm2(xv.x, gv.x, bv.x, mu, rs), norm2(xv.y, gv.y, bv.y, mu, rs),
+               norm2(xv.z, gv.z, bv.z, mu, rs), norm2(xv.w, gv.w, bv.w, mu, rs)};
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void layernorm_fwd_staged_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
+    const uint16_t* __restrict__ beta, uint16_t* __restrict__ y,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int cols,
+    float eps) {
+  constexpr int NW = THREADS / kWave;
+  __shared__ double red0[NW];
+  __shared__ double red1[NW];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nvec = cols >> 3;
+  const u32x4* xr = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(row) * cols);
+  u32x4 v[VPT];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int idx = tid + k * THREADS;
+    v[k] = idx < nvec ? load_nt(xr + idx) : u32x4{0, 0, 0, 0};
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) s += sum8(v[k]);
+  const double total = block_reduce_sum_f64<NW>(static_cast<double>(s), red0);
+  const float mu = static_cast<float>(total / cols);
+  float q = 0.0f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int idx = tid + k * THREADS;
+    if (idx < nvec) q += sqdev8(v[k], mu);
+  }
+  const double sq = block_reduce_sum_f64<NW>(static_cast<double>(q), red1);
+  // Deviations were taken from the fp32-rounded mean; the exact two-pass
+  // variance about the true mean differs by (mu - total/N)^2, which the
+  // correction term removes.
+  const double dmu = static_cast<double>(mu) - total / cols;
+  const double var = sq / cols - dmu * dmu;
+  const float rs = static_cast<float>(1.0 / __builtin_sqrt((var > 0.0 ? var : 0.0) + eps));
+  const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
+  const u32x4* br = reinterpret_cast<const u32x4*>(beta);
+  u32x4* yr = reinterpret_cast<u32x4*>(y + static_cast<size_t>(row) * cols);
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int idx = tid + k * THREADS;
+    if (idx < nvec) store_nt(yr + idx, norm8(v[k], gr[idx], br[idx], mu, rs));
+  }
+  if (tid == 0) {
+    mean_out[row] = static_cast<float>(total / cols);
+    rstd_out[row] = rs;
+  }
+}
+
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void layernorm_fwd_read_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
+    const uint16_t* __restrict__ beta, uint16_t* __restrict__ y,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int cols,
+    float eps) {
+  constexpr int NW = THREADS / kWave;
+  __shared__ double red0[NW];
+  __shared__ double red1[NW];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint16_t* xr = x + static_cast<size_t>(row) * cols;
+  double s = 0.0;
+  for (int c = tid; c < cols; c += THREADS) s += bf16_to_f32(xr[c]);
+  const double total = block_reduce_sum_f64<NW>(s, red0);
+  const double mean = total / cols;
+  double q = 0.0;
+  for (int c = tid; c < cols; c += THREADS) {
+    const double d = bf16_to_f32(xr[c]) - mean;
+    q += d * d;
+  }
+  const double var = block_reduce_sum_f64<NW>(q, red1) / cols;
+  const float rs = static_cast<float>(1.0 / __builtin_sqrt(var + eps));
+  const float mu = static_cast<float>(mean);
+  uint16_t* yr = y + static_cast<size_t>(row) * cols;
+  for (int c = tid; c < cols; c += THREADS) {
+    const float v = (bf16_to_f32(xr[c]) - mu) * rs * bf16_to_f32(gamma[c]) +
+                    bf16_to_f32(beta[c]);
+    yr[c] = f32_to_bf16(v);
+  }
+  if (tid == 0) {
+    mean_out[row] = mu;
+    rstd_out[row] = rs;
+  }
+}
+
+using StagedFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*,
+                          uint16_t*, float*, float*, int, float);
+
+struct StagedPick {
+  StagedFn fn;
+  int threads;
+  int max_vec;  // threads * VPT
+};
+
+// Row widths the register-staged kernel covers, smallest footprint first.
+// VPT stays at 8 (eight dwordx4 loads in flight per lane) wherever the row
+// allows, and rises to 16 only for rows wider than 1024*8 vectors.
+const StagedPick kStaged[] = {
+    {layernorm_fwd_staged_kernel<64, 4>, 64, 256},
+    {layernorm_fwd_staged_kernel<128, 4>, 128, 512},
+    {layernorm_fwd_staged_kernel<256, 4>, 256, 1024},
+    {layernorm_fwd_staged_kernel<256, 8>, 256, 2048},
+    {layernorm_fwd_staged_kernel<512, 8>, 512, 4096},
+    {layernorm_fwd_staged_kernel<1024, 8>, 1024, 8192},
+    {layernorm_fwd_staged_kernel<1024, 16>, 1024, 16384},
+};
+
+}  // namespace
+}  // namespace credit
+
+using namespace credit;
+
+extern "C" int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamma,
+                                         const uint16_t* beta, uint16_t* y,
+                                         float* mean, float* rstd, int64_t rows,
+                                         int64_t cols, float eps,
+                                         const credit_cfg* cfg) {
+  CREDIT_TRY(check_ptr(x, "x"));
+  CREDIT_TRY(check_ptr(gamma, "gamma"));
+  CREDIT_TRY(check_ptr(beta, "beta"));
+  CREDIT_TRY(check_ptr(y, "y"));
+  CREDIT_TRY(check_ptr(mean, "mean"));
+  CREDIT_TRY(check_ptr(rstd, "rstd"));
+  CREDIT_TRY(check_shape(rows, cols, int64_t{1} << 30));
+  CREDIT_TRY(check_aligned(x, 2, "x"));
+  CREDIT_TRY(check_cfg(cfg));
+  if (!(eps >= 0.0f))
+    return set_error(CREDIT_ERR_BAD_CONFIG, "eps must be >= 0");
+  if (rows == 0) return CREDIT_OK;
+  int variant = cfg_variant(cfg);
+  if (variant == CREDIT_VARIANT_SPLIT)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "layernorm_fwd: split-row variant not built");
+  hipStream_t stream = cfg_stream(cfg);
+  const int c = static_cast<int>(cols);
+  const bool vec_ok = (cols % 8 == 0) &&
+                      reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(gamma) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(beta) % 16 == 0;
+  const int64_t nvec = cols / 8;
+  const StagedPick* pick = nullptr;
+  if (vec_ok) {
+    for (const StagedPick& p : kStaged) {
+      if (nvec <= p.max_vec) {
+        pick = &p;
+        break;
+      }
+    }
+  }
+  if (variant == CREDIT_VARIANT_STAGED && pick == nullptr)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "layernorm_fwd staged variant needs cols %% 8 == 0, "
+                     "16-byte aligned buffers and cols <= 131072");
+  if (variant == CREDIT_VARIANT_READ || pick == nullptr) {
+    layernorm_fwd_read_kernel<256><<<dim3(static_cast<unsigned>(rows)), dim3(256), 0,
+                                     stream>>>(x, gamma, beta, y, mean, rstd, c, eps);
+    return check_launch("layernorm_fwd_read_kernel");
+  }
+  hipLaunchKernelGGL(pick->fn, dim3(static_cast<unsigned>(rows)), dim3(pick->threads),
+                     0, stream, x, gamma, beta, y, mean, rstd, c, eps);
+  return check_launch("layernorm_fwd_staged_kernel");
+}

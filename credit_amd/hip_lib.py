@@ -1,0 +1,299 @@
+"""ctypes binding of libcredit_hip.so, the gfx950 wide-row kernels.
+
+This is the in-process operator boundary.  It mirrors the reference's
+Triton launcher table (dsmem_eval/triton_kernels.py:300-414):
+``HIP_LAUNCHERS[name](inputs, outputs, ...)`` writes the outputs in place and
+``allocate_outputs(name, inputs)`` gives their shapes and dtypes.  The
+reference's CUDA kernels sat behind a subprocess + stdout protocol
+(dsmem_eval/runner.py:280-310); here they are direct calls on the caller's
+current HIP stream.
+
+The library is loaded from the package directory (built by
+``credit_amd/csrc/Makefile``).  There is no fallback: a missing library or a
+non-zero status raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Callable
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libcredit_hip.so"
+
+# Status codes (include/credit.h).
+CREDIT_OK = 0
+STATUS_NAMES = {
+    0: "CREDIT_OK",
+    -1: "CREDIT_ERR_NULL_POINTER",
+    -2: "CREDIT_ERR_BAD_SHAPE",
+    -3: "CREDIT_ERR_ALIGNMENT",
+    -4: "CREDIT_ERR_UNSUPPORTED",
+    -5: "CREDIT_ERR_WORKSPACE",
+    -6: "CREDIT_ERR_HIP",
+    -7: "CREDIT_ERR_WATCHDOG",
+    -8: "CREDIT_ERR_BAD_CONFIG",
+}
+
+VARIANTS = {"auto": 0, "read": 1, "staged": 2, "split": 3}
+VARIANT_NAMES = {v: k for k, v in VARIANTS.items()}
+
+OPS = {
+    "row_sum_max": 1,
+    "layernorm_fwd": 2,
+    "layernorm_backward": 3,
+    "rmsnorm_fwd": 4,
+    "rmsnorm_bwd": 5,
+    "softmax_fwd": 6,
+    "softmax_bwd": 7,
+    "softmax_logits_backward": 8,
+    "ffn": 9,
+}
+
+
+class CreditError(RuntimeError):
+    """A non-zero status from libcredit_hip.so."""
+
+    def __init__(self, status: int, function: str, message: str):
+        self.status = status
+        self.function = function
+        super().__init__(f"{function}: {STATUS_NAMES.get(status, status)}: {message}")
+
+
+class CreditCfg(ctypes.Structure):
+    _fields_ = [
+        ("stream", ctypes.c_void_p),
+        ("variant", ctypes.c_int32),
+        ("split", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 128),
+        ("arch", ctypes.c_char * 64),
+        ("device", ctypes.c_int32),
+        ("cu_count", ctypes.c_int32),
+        ("xcd_count", ctypes.c_int32),
+        ("wave_size", ctypes.c_int32),
+        ("max_threads_per_block", ctypes.c_int32),
+        ("cooperative_launch", ctypes.c_int32),
+        ("lds_bytes_per_block", ctypes.c_int64),
+        ("lds_bytes_per_cu", ctypes.c_int64),
+        ("l2_bytes", ctypes.c_int64),
+        ("hbm_bytes", ctypes.c_int64),
+        ("clock_khz", ctypes.c_int32),
+        ("mem_clock_khz", ctypes.c_int32),
+        ("mem_bus_width_bits", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_CFG = ctypes.POINTER(CreditCfg)
+
+# name -> argument types (return type is int unless listed in _RESTYPES).
+SIGNATURES: dict[str, list] = {
+    "credit_version": [],
+    "credit_last_error": [],
+    "credit_status_string": [ctypes.c_int],
+    "credit_query_device": [ctypes.c_int32, ctypes.POINTER(DeviceInfo)],
+    "credit_workspace_bytes": [ctypes.c_int32, _I64, _I64, ctypes.c_int32, ctypes.c_int32],
+    "credit_check_watchdog": [_CFG],
+    "credit_row_sum_max_f32": [_P, _P, _P, _I64, _I64, _CFG],
+    "credit_layernorm_fwd_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _CFG],
+}
+_RESTYPES = {
+    "credit_version": ctypes.c_char_p,
+    "credit_last_error": ctypes.c_char_p,
+    "credit_status_string": ctypes.c_char_p,
+    "credit_workspace_bytes": ctypes.c_size_t,
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Load libcredit_hip.so once and declare every entry point's signature.
+
+    torch is imported first so that the HIP runtime torch already mapped is
+    the one the library binds to (both carry the soname libamdhip64.so.7).
+    """
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    lib_path = Path(path) if path is not None else LIB_PATH
+    if not lib_path.is_file():
+        raise FileNotFoundError(
+            f"{lib_path} is missing; build it with `make -C credit_amd/csrc` "
+            "or `python -c 'import __graft_entry__ as g; g.build()'`"
+        )
+    lib = ctypes.CDLL(str(lib_path), mode=ctypes.RTLD_GLOBAL)
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = _RESTYPES.get(name, ctypes.c_int)
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load_library().credit_last_error().decode()
+
+
+def check(status: int, function: str) -> None:
+    if status != CREDIT_OK:
+        raise CreditError(status, function, last_error())
+
+
+def query_device(device: int = 0) -> dict:
+    info = DeviceInfo()
+    check(load_library().credit_query_device(device, ctypes.byref(info)), "credit_query_device")
+    out = {name: getattr(info, name) for name, _ in DeviceInfo._fields_ if name != "reserved"}
+    out["name"] = info.name.decode()
+    out["arch"] = info.arch.decode()
+    return out
+
+
+def make_cfg(
+    variant: str | int = "auto",
+    split: int = 0,
+    stream: int | None = None,
+    workspace: torch.Tensor | None = None,
+) -> CreditCfg:
+    """Build a credit_cfg for the current torch stream (or `stream`)."""
+    if isinstance(variant, str):
+        if variant not in VARIANTS:
+            raise ValueError(f"unknown variant {variant!r}; expected one of {sorted(VARIANTS)}")
+        variant = VARIANTS[variant]
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream if torch.cuda.is_available() else 0
+    cfg = CreditCfg()
+    cfg.stream = stream or None
+    cfg.variant = int(variant)
+    cfg.split = int(split)
+    if workspace is not None:
+        cfg.workspace = workspace.data_ptr()
+        cfg.workspace_bytes = workspace.numel() * workspace.element_size()
+    return cfg
+
+
+def workspace_bytes(op: str, rows: int, cols: int, variant: str = "auto", split: int = 0) -> int:
+    return int(load_library().credit_workspace_bytes(OPS[op], rows, cols, VARIANTS[variant], split))
+
+
+def check_watchdog(cfg: CreditCfg | None = None) -> None:
+    cfg = cfg if cfg is not None else make_cfg()
+    check(load_library().credit_check_watchdog(ctypes.byref(cfg)), "credit_check_watchdog")
+
+
+def _ptr(t: torch.Tensor, name: str, dtype: torch.dtype) -> int:
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: tensor must be on a GPU, got {t.device}")
+    return t.data_ptr()
+
+
+def _rows_cols(x: torch.Tensor) -> tuple[int, int]:
+    if x.dim() != 2:
+        raise ValueError(f"expected a 2-D tensor, got shape {tuple(x.shape)}")
+    return int(x.shape[0]), int(x.shape[1])
+
+
+# --------------------------------------------------------------- operators --
+
+
+def row_sum_max(x: torch.Tensor, out_sum: torch.Tensor, out_max: torch.Tensor, cfg: CreditCfg) -> None:
+    rows, cols = _rows_cols(x)
+    check(
+        load_library().credit_row_sum_max_f32(
+            _ptr(x, "x", torch.float32),
+            _ptr(out_sum, "sum", torch.float32),
+            _ptr(out_max, "max", torch.float32),
+            rows,
+            cols,
+            ctypes.byref(cfg),
+        ),
+        "credit_row_sum_max_f32",
+    )
+
+
+def layernorm_fwd(
+    x: torch.Tensor,
+    gamma: torch.Tensor,
+    beta: torch.Tensor,
+    y: torch.Tensor,
+    mean: torch.Tensor,
+    rstd: torch.Tensor,
+    eps: float,
+    cfg: CreditCfg,
+) -> None:
+    rows, cols = _rows_cols(x)
+    check(
+        load_library().credit_layernorm_fwd_bf16(
+            _ptr(x, "x", torch.bfloat16),
+            _ptr(gamma, "gamma", torch.bfloat16),
+            _ptr(beta, "beta", torch.bfloat16),
+            _ptr(y, "y", torch.bfloat16),
+            _ptr(mean, "mean", torch.float32),
+            _ptr(rstd, "rstd", torch.float32),
+            rows,
+            cols,
+            float(eps),
+            ctypes.byref(cfg),
+        ),
+        "credit_layernorm_fwd_bf16",
+    )
+
+
+# ------------------------------------------------- reference-shaped table --
+
+
+@dataclass(frozen=True)
+class LaunchConfig:
+    """Knobs a launcher takes: the variant and split factor replace the
+    reference's (block_size, num_warps) Triton pair and cluster size P."""
+
+    variant: str = "auto"
+    split: int = 0
+
+
+def launch_row_sum_max(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    (x,) = inputs
+    s, m = outputs
+    row_sum_max(x, s, m, make_cfg(config.variant, config.split))
+
+
+def launch_layernorm_fwd(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    x, gamma, beta = inputs
+    y, mean, rstd = outputs
+    layernorm_fwd(x, gamma, beta, y, mean, rstd, 1.0e-5, make_cfg(config.variant, config.split))
+
+
+HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
+    "row_sum_max": launch_row_sum_max,
+    "layernorm_fwd": launch_layernorm_fwd,
+}
+
+
+def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch.Tensor, ...]:
+    """Output buffers of a launcher, as dsmem_eval/triton_kernels.py:403-414."""
+    x = inputs[0]
+    rows = x.shape[0]
+    f32 = dict(device=x.device, dtype=torch.float32)
+    if name == "row_sum_max":
+        return torch.empty(rows, **f32), torch.empty(rows, **f32)
+    if name == "layernorm_fwd":
+        return torch.empty_like(x), torch.empty(rows, **f32), torch.empty(rows, **f32)
+    raise KeyError(name)

@@ -1,0 +1,293 @@
+"""Workload registry: shapes, seeded inputs, traffic and tolerances.
+
+Mirrors the reference's ``WorkloadSpec`` registry
+(dsmem_eval/workloads.py:16-37,157-212) for the MI355X build.  Two families:
+
+* the BASELINE configurations C1-C5 (row sum/max, LayerNorm forward,
+  RMSNorm forward/backward, online softmax forward/backward, norm-fused
+  FFN), which have no reference kernel; and
+* the reference's own wide-row workloads (LayerNorm backward,
+  softmax-logits backward, ...), with the input ranges, eps and tolerances of
+  dsmem_eval/workloads.py.
+
+Inputs come from a seeded CPU ``torch.Generator`` (CPU and ROCm generator
+streams differ, so generating on the CPU and copying keeps the GPU run, the
+oracle and the CPU baseline on identical data).  The reference seeds a CUDA
+generator with 1234 + cols (dsmem_eval/runner.py:358); the BASELINE
+configurations use seed 0.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Callable
+
+import torch
+
+TensorTuple = tuple[torch.Tensor, ...]
+
+
+@dataclass(frozen=True)
+class WorkloadSpec:
+    name: str
+    label: str
+    category: str
+    rows: int
+    cols: int
+    input_factory: Callable[[int, int, torch.Generator], TensorTuple]
+    output_names: tuple[str, ...]
+    # Algorithmic (compulsory) HBM bytes of one call at (rows, cols): every
+    # input read once, every output written once.  The roofline numerator.
+    algorithmic_bytes: Callable[[int, int], int]
+    # Per-output (atol, rtol); None means bit-exact.
+    tolerances: tuple[tuple[float, float] | None, ...]
+    seed: int = 0
+    # Cost-model metadata (dsmem_eval/workload_metadata.py:6-35): bytes per
+    # element of the no-staging variant, the re-read share staging removes,
+    # bytes staged on chip per element, partials exchanged per stage.
+    modeled_bytes_per_element: float = 0.0
+    reread_bytes_per_element: float = 0.0
+    staged_bytes_per_element: int = 0
+    reductions_per_stage: tuple[int, ...] = field(default_factory=tuple)
+
+    @property
+    def barrier_count(self) -> int:
+        """One arrival barrier per reduction stage (the reference counts two
+        cluster.sync per stage, dsmem_eval/workloads.py:31-33)."""
+        return len(self.reductions_per_stage)
+
+    @property
+    def partial_count(self) -> int:
+        return sum(self.reductions_per_stage)
+
+    def make_inputs(self, rows: int | None = None, cols: int | None = None, seed: int | None = None,
+                    device: str | torch.device = "cpu") -> TensorTuple:
+        g = torch.Generator(device="cpu")
+        g.manual_seed(self.seed if seed is None else seed)
+        tensors = self.input_factory(rows or self.rows, cols or self.cols, g)
+        if torch.device(device).type == "cpu":
+            return tensors
+        return tuple(t.to(device) for t in tensors)
+
+
+# ----------------------------------------------------------- factories ----
+
+
+def _uniform(shape, low, high, g):
+    return torch.empty(shape, dtype=torch.float32).uniform_(low, high, generator=g)
+
+
+def _normal(shape, mean, std, g, dtype=torch.float32):
+    t = torch.randn(shape, generator=g, dtype=torch.float32)
+    if std != 1.0:
+        t.mul_(std)
+    if mean != 0.0:
+        t.add_(mean)
+    return t.to(dtype)
+
+
+def make_row_sum_max_inputs(rows, cols, g):
+    return (_uniform((rows, cols), -1.0, 1.0, g),)
+
+
+def make_layernorm_fwd_inputs(rows, cols, g):
+    return (
+        _normal((rows, cols), 0.0, 1.0, g, torch.bfloat16),
+        _normal((cols,), 1.0, 0.02, g, torch.bfloat16),
+        _normal((cols,), 0.0, 0.02, g, torch.bfloat16),
+    )
+
+
+def make_rmsnorm_inputs(rows, cols, g):
+    return (
+        _normal((rows, cols), 0.0, 1.0, g, torch.bfloat16),
+        _normal((cols,), 1.0, 0.02, g, torch.bfloat16),
+        _normal((rows, cols), 0.0, 1.0, g, torch.bfloat16),
+    )
+
+
+def make_softmax_inputs(rows, cols, g):
+    """x ~ N(0, std 4) with 1% of entries set to +20; dy ~ N(0, 1).
+    Draw order: x, dy, then the mask."""
+    x = _normal((rows, cols), 0.0, 4.0, g)
+    dy = _normal((rows, cols), 0.0, 1.0, g)
+    mask = torch.rand((rows, cols), generator=g) < 0.01
+    x[mask] = 20.0
+    return x, dy
+
+
+def make_ffn_inputs(rows, cols, g, ffn_dim: int = 28672):
+    d = cols
+    return (
+        _normal((rows, d), 0.0, 1.0, g, torch.bfloat16),
+        _normal((d, ffn_dim), 0.0, 1.0 / math.sqrt(d), g, torch.bfloat16),
+        _normal((ffn_dim, d), 0.0, 1.0 / math.sqrt(ffn_dim), g, torch.bfloat16),
+    )
+
+
+# Reference workloads: input ranges of dsmem_eval/workloads.py:45-50,115-119.
+
+
+def make_layernorm_backward_inputs(rows, cols, g):
+    return (
+        _uniform((rows, cols), -1.0, 1.0, g),
+        _uniform((rows, cols), -1.0, 1.0, g),
+        _uniform((cols,), 0.75, 1.25, g),
+    )
+
+
+def make_softmax_logits_inputs(rows, cols, g):
+    return (
+        _uniform((rows, cols), -4.0, 4.0, g),
+        _uniform((rows, cols), -1.0, 1.0, g),
+    )
+
+
+# -------------------------------------------------------------- registry --
+
+FP32_TOL = (1.0e-6, 1.0e-5)
+BF16_TOL = (1.0e-2, 1.0e-2)
+
+WORKLOADS: dict[str, WorkloadSpec] = {
+    "row_sum_max": WorkloadSpec(
+        name="row_sum_max",
+        label="Row-wise sum + max",
+        category="reduction",
+        rows=1024,
+        cols=65536,
+        input_factory=make_row_sum_max_inputs,
+        output_names=("sum", "max"),
+        algorithmic_bytes=lambda r, c: 4 * r * c + 8 * r,
+        tolerances=(FP32_TOL, None),
+        modeled_bytes_per_element=4.0,
+        reread_bytes_per_element=0.0,
+        staged_bytes_per_element=0,
+        reductions_per_stage=(2,),
+    ),
+    "layernorm_fwd": WorkloadSpec(
+        name="layernorm_fwd",
+        label="LayerNorm forward (bf16)",
+        category="normalization",
+        rows=2048,
+        cols=32768,
+        input_factory=make_layernorm_fwd_inputs,
+        output_names=("y", "mean", "rstd"),
+        algorithmic_bytes=lambda r, c: 2 * r * c + 2 * r * c + 4 * c + 8 * r,
+        tolerances=(BF16_TOL, FP32_TOL, FP32_TOL),
+        modeled_bytes_per_element=8.0,  # read x twice (stats, output) + write y
+        reread_bytes_per_element=4.0,   # the second and third reads of x
+        staged_bytes_per_element=2,
+        reductions_per_stage=(1, 1),
+    ),
+    "rmsnorm_fwd": WorkloadSpec(
+        name="rmsnorm_fwd",
+        label="RMSNorm forward (bf16)",
+        category="normalization",
+        rows=1024,
+        cols=131072,
+        input_factory=make_rmsnorm_inputs,
+        output_names=("y", "rstd"),
+        algorithmic_bytes=lambda r, c: 2 * r * c + 2 * c + 2 * r * c + 4 * r,
+        tolerances=(BF16_TOL, FP32_TOL),
+        modeled_bytes_per_element=6.0,
+        reread_bytes_per_element=2.0,
+        staged_bytes_per_element=2,
+        reductions_per_stage=(1,),
+    ),
+    "rmsnorm_bwd": WorkloadSpec(
+        name="rmsnorm_bwd",
+        label="RMSNorm backward (bf16, fp32 dweight)",
+        category="normalization",
+        rows=1024,
+        cols=131072,
+        input_factory=make_rmsnorm_inputs,
+        output_names=("dx", "dweight"),
+        algorithmic_bytes=lambda r, c: 2 * r * c * 2 + 2 * c + 4 * r + 2 * r * c + 4 * c,
+        tolerances=(BF16_TOL, FP32_TOL),
+        modeled_bytes_per_element=10.0,
+        reread_bytes_per_element=4.0,
+        staged_bytes_per_element=4,
+        reductions_per_stage=(1,),
+    ),
+    "softmax_fwd": WorkloadSpec(
+        name="softmax_fwd",
+        label="Online softmax forward (fp32)",
+        category="softmax",
+        rows=512,
+        cols=262144,
+        input_factory=make_softmax_inputs,
+        output_names=("p", "max", "lse"),
+        algorithmic_bytes=lambda r, c: 4 * r * c * 2 + 8 * r,
+        tolerances=(FP32_TOL, None, FP32_TOL),
+        modeled_bytes_per_element=12.0,
+        reread_bytes_per_element=4.0,
+        staged_bytes_per_element=4,
+        reductions_per_stage=(2,),
+    ),
+    "softmax_bwd": WorkloadSpec(
+        name="softmax_bwd",
+        label="Softmax backward (fp32)",
+        category="softmax",
+        rows=512,
+        cols=262144,
+        input_factory=make_softmax_inputs,
+        output_names=("dx",),
+        algorithmic_bytes=lambda r, c: 4 * r * c * 3,
+        tolerances=(FP32_TOL,),
+        modeled_bytes_per_element=20.0,
+        reread_bytes_per_element=8.0,
+        staged_bytes_per_element=8,
+        reductions_per_stage=(1,),
+    ),
+    "ffn": WorkloadSpec(
+        name="ffn",
+        label="Norm-fused FFN (bf16 MFMA)",
+        category="gemm",
+        rows=4096,
+        cols=8192,
+        input_factory=make_ffn_inputs,
+        output_names=("out",),
+        algorithmic_bytes=lambda r, c: 2 * (r * c * 2 + 2 * c * 28672),
+        tolerances=(BF16_TOL,),
+    ),
+    # Reference workloads (dsmem_eval/workloads.py:157-212).
+    "layernorm_backward": WorkloadSpec(
+        name="layernorm_backward",
+        label="LayerNorm backward",
+        category="normalization",
+        rows=2048,
+        cols=65536,
+        input_factory=make_layernorm_backward_inputs,
+        output_names=("dx",),
+        algorithmic_bytes=lambda r, c: 4 * r * c * 3 + 4 * c,
+        tolerances=((2.0e-2, 2.0e-2),),
+        seed=1234,
+        modeled_bytes_per_element=32.0,
+        reread_bytes_per_element=12.0,
+        staged_bytes_per_element=4,
+        reductions_per_stage=(2, 2),
+    ),
+    "softmax_logits_backward": WorkloadSpec(
+        name="softmax_logits_backward",
+        label="Softmax-logits backward",
+        category="softmax",
+        rows=4096,
+        cols=65536,
+        input_factory=make_softmax_logits_inputs,
+        output_names=("dx",),
+        algorithmic_bytes=lambda r, c: 4 * r * c * 3,
+        tolerances=((3.0e-3, 3.0e-3),),
+        seed=1234,
+        modeled_bytes_per_element=28.0,
+        reread_bytes_per_element=16.0,
+        staged_bytes_per_element=8,
+        reductions_per_stage=(1, 1, 1),
+    ),
+}
+
+# FFN flop count of one call: two GEMMs, 2*M*d*f each.
+FFN_DIM = 28672
+
+
+def ffn_flops(rows: int, d: int, f: int = FFN_DIM) -> int:
+    return 2 * rows * d * f * 2

@@ -1,0 +1,154 @@
+/*
+ * credit.h -- C-ABI of libcredit_hip.so, the MI355X (gfx950) wide-row kernels.
+ *
+ * In the reference (zhengxiongli08/CREDIT) the native code sits behind a
+ * process boundary: dsmem_eval/runner.py:280-310 spawns one CUDA executable
+ * per workload (`build/<workload> --csv --rows R --n-values ... --cluster-size P`)
+ * and parses its `RESULT,...` stdout line (src/workloads/layernorm_backward.cu:
+ * 730-765, parsed at dsmem_eval/runner.py:258-277); the in-process operator
+ * form of the same workloads is the Triton launcher table
+ * `launcher(inputs, outputs, block_size, num_warps)` of
+ * dsmem_eval/triton_kernels.py:300-400.  This library replaces both with
+ * in-process calls: plain device pointers and sizes, no torch types.
+ *
+ * Contract shared by every compute entry point:
+ *  - Ownership: the caller owns every buffer.  Pointers are device pointers,
+ *    borrowed for the duration of the (asynchronous) call.
+ *  - Layout: row-major, contiguous, rows x cols.  bf16 tensors are passed as
+ *    uint16_t bit patterns.  Vectorised paths need 16-byte aligned rows; other
+ *    shapes take a scalar path, they are never rejected for alignment alone.
+ *  - Errors: every function returns 0 (CREDIT_OK) or a negative CREDIT_ERR_*
+ *    code; credit_last_error() gives the message (thread-local).  Nothing
+ *    exits or throws across the ABI.  Arguments are validated on the host
+ *    before any HIP call, so a bad call never reaches the GPU.
+ *  - Streams: work is enqueued on cfg->stream (a hipStream_t; NULL means the
+ *    null stream).  cfg itself may be NULL (= all defaults).
+ *  - Workspace: split-row variants exchange partial results through a device
+ *    scratch buffer.  With cfg->workspace == NULL the library uses a cached
+ *    per-device buffer; otherwise cfg->workspace must hold at least
+ *    credit_workspace_bytes(...) bytes, be 256-byte aligned and be
+ *    zero-filled before its first use.  Every call that completes leaves it
+ *    in that state again, so it needs no clearing between calls.  Calls that
+ *    share one workspace must not run concurrently.
+ */
+#ifndef CREDIT_H_
+#define CREDIT_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ status ---- */
+#define CREDIT_OK 0
+#define CREDIT_ERR_NULL_POINTER (-1)
+#define CREDIT_ERR_BAD_SHAPE (-2)
+#define CREDIT_ERR_ALIGNMENT (-3)
+#define CREDIT_ERR_UNSUPPORTED (-4)
+#define CREDIT_ERR_WORKSPACE (-5)
+#define CREDIT_ERR_HIP (-6)
+#define CREDIT_ERR_WATCHDOG (-7)
+#define CREDIT_ERR_BAD_CONFIG (-8)
+
+/* ----------------------------------------------------------- variants ---
+ * The reference times three kernel variants per workload
+ * (src/workloads/layernorm_backward.cu:470-593): block_read (one CTA per row,
+ * re-reading HBM on every pass), block_smem (one CTA per row, row staged on
+ * chip) and cluster_smem (row split over a P-CTA cluster, partials exchanged
+ * through DSMEM).  Their gfx950 counterparts: */
+#define CREDIT_VARIANT_AUTO 0     /* library picks                          */
+#define CREDIT_VARIANT_READ 1     /* one workgroup per row, streams HBM     */
+#define CREDIT_VARIANT_STAGED 2   /* one workgroup per row, row in VGPRs/LDS */
+#define CREDIT_VARIANT_SPLIT 3    /* P workgroups per row, L2 exchange      */
+
+typedef struct credit_cfg {
+  void* stream;           /* hipStream_t or NULL                            */
+  int32_t variant;        /* CREDIT_VARIANT_*                               */
+  int32_t split;          /* P for CREDIT_VARIANT_SPLIT; 0 = library choice */
+  void* workspace;        /* optional caller scratch, see contract above    */
+  size_t workspace_bytes; /* its size                                       */
+} credit_cfg;
+
+/* Operation ids for credit_workspace_bytes(). */
+#define CREDIT_OP_ROW_SUM_MAX 1
+#define CREDIT_OP_LAYERNORM_FWD 2
+#define CREDIT_OP_LAYERNORM_BWD 3
+#define CREDIT_OP_RMSNORM_FWD 4
+#define CREDIT_OP_RMSNORM_BWD 5
+#define CREDIT_OP_SOFTMAX_FWD 6
+#define CREDIT_OP_SOFTMAX_BWD 7
+#define CREDIT_OP_SOFTMAX_LOGITS_BWD 8
+#define CREDIT_OP_FFN 9
+
+/* ------------------------------------------------------------ library --- */
+
+/* Library version string, e.g. "credit-hip 0.1.0 gfx950". */
+const char* credit_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* credit_last_error(void);
+
+/* Static name of a status code. */
+const char* credit_status_string(int status);
+
+/* Replaces query_device_info (src/workloads/layernorm_backward.cu:440-468),
+ * which reported opt-in shared memory and cluster support. */
+typedef struct credit_device_info {
+  char name[128];
+  char arch[64];
+  int32_t device;
+  int32_t cu_count;
+  int32_t xcd_count;
+  int32_t wave_size;
+  int32_t max_threads_per_block;
+  int32_t cooperative_launch;
+  int64_t lds_bytes_per_block;
+  int64_t lds_bytes_per_cu;
+  int64_t l2_bytes;
+  int64_t hbm_bytes;
+  int32_t clock_khz;
+  int32_t mem_clock_khz;
+  int32_t mem_bus_width_bits;
+  int32_t reserved;
+} credit_device_info;
+int credit_query_device(int32_t device, credit_device_info* info);
+
+/* Bytes of workspace a call needs (0 when the chosen variant needs none).
+ * The reference has no counterpart: its DSMEM exchange lives in the
+ * cluster's shared memory (cost_model.py:47-52 sizes that). */
+size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
+                              int32_t variant, int32_t split);
+
+/* Waits for cfg->stream, then reports CREDIT_ERR_WATCHDOG (and clears the
+ * flag) if a split-row barrier of an earlier call on this workspace gave up
+ * waiting.  The reference's cluster.sync() cannot time out; this is the
+ * host-visible form of the bounded spin that replaces it. */
+int credit_check_watchdog(const credit_cfg* cfg);
+
+/* ------------------------------------------------ C1: row sum and max ---
+ * sum[r] = sum_j x[r, j] (accumulated in fp64, rounded once to fp32) and
+ * max[r] = max_j x[r, j] (NaN-propagating, bit-exact with torch.amax).
+ * Generalises the max-abs row reduction of
+ * src/workloads/rowwise_quant.cu:260-363 (launched per runner.py:280-310);
+ * the reference has no standalone sum/max workload.  cols >= 1. */
+int credit_row_sum_max_f32(const float* x, float* sum, float* max,
+                           int64_t rows, int64_t cols, const credit_cfg* cfg);
+
+/* --------------------------------------------- C2: LayerNorm forward -----
+ * y = (x - mean) * rstd * gamma + beta over each row, bf16 in/out, fp32
+ * statistics (two-pass: mean, then mean of squared deviations).  No
+ * forward kernel exists in the reference; its statistics follow
+ * src/workloads/layernorm_backward.cu:286-295 and the eps of
+ * dsmem_eval/workloads.py:55. */
+int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamma,
+                              const uint16_t* beta, uint16_t* y, float* mean,
+                              float* rstd, int64_t rows, int64_t cols,
+                              float eps, const credit_cfg* cfg);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CREDIT_H_ */

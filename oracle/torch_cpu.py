@@ -1,0 +1,84 @@
+"""The reference's PyTorch path run on CPU tensors (test infrastructure only).
+
+Used as bench.py's ``cpu_baseline`` leg: the workloads as the reference's
+eager PyTorch functions compute them (dsmem_eval/workloads.py:53-154 style:
+fp32 arithmetic, library reductions), on the host cores of the GPU box.  For
+the BASELINE configurations without a reference function the restatement
+uses the library routines BASELINE.md names (torch.sum/amax, LayerNorm on
+x.float(), F.rms_norm, torch.softmax/logsumexp, GELU-tanh FFN).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def row_sum_max(x):
+    return torch.sum(x, dim=-1), torch.amax(x, dim=-1)
+
+
+def layernorm_fwd(x, gamma, beta, eps=1.0e-5):
+    xf = x.float()
+    var, mean = torch.var_mean(xf, dim=-1, unbiased=False, keepdim=True)
+    rstd = torch.rsqrt(var + eps)
+    y = ((xf - mean) * rstd * gamma.float() + beta.float()).to(x.dtype)
+    return y, mean.squeeze(-1), rstd.squeeze(-1)
+
+
+def rmsnorm_fwd(x, w, eps=1.0e-6):
+    xf = x.float()
+    rstd = torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (xf * rstd * w.float()).to(x.dtype), rstd.squeeze(-1)
+
+
+def rmsnorm_bwd(x, w, dy, rstd):
+    xf, dyf = x.float(), dy.float()
+    r = rstd.unsqueeze(-1)
+    g = dyf * w.float()
+    xhat = xf * r
+    c = (g * xhat).mean(dim=-1, keepdim=True)
+    return (r * (g - xhat * c)).to(x.dtype), (dyf * xhat).sum(dim=0)
+
+
+def softmax_fwd(x):
+    m = torch.amax(x, dim=-1)
+    lse = torch.logsumexp(x, dim=-1)
+    return torch.softmax(x, dim=-1), m, lse
+
+
+def softmax_bwd(p, dy):
+    return p * (dy - (p * dy).sum(dim=-1, keepdim=True))
+
+
+def layernorm_backward(x, dy, gamma):
+    mean = x.mean(dim=-1, keepdim=True)
+    xmu = x - mean
+    inv_std = torch.rsqrt((xmu * xmu).mean(dim=-1, keepdim=True) + 1.0e-5)
+    xhat = xmu * inv_std
+    dyg = dy * gamma
+    return (dyg - dyg.mean(dim=-1, keepdim=True) - xhat * (dyg * xhat).mean(dim=-1, keepdim=True)) * inv_std
+
+
+def softmax_logits_backward(logits, dy):
+    p = torch.softmax(logits, dim=-1)
+    return p * (dy - (p * dy).sum(dim=-1, keepdim=True))
+
+
+def ffn(x, w1, w2, eps=1.0e-6):
+    a = F.rms_norm(x.float(), (x.shape[-1],), None, eps).to(x.dtype)
+    h = F.gelu(a @ w1, approximate="tanh")
+    return (x.float() + (h @ w2).float()).to(x.dtype)
+
+
+# name -> (function, which BASELINE inputs it takes)
+FUNCTIONS = {
+    "row_sum_max": row_sum_max,
+    "layernorm_fwd": layernorm_fwd,
+    "rmsnorm_fwd": lambda x, w, dy: rmsnorm_fwd(x, w),
+    "rmsnorm_bwd": lambda x, w, dy: rmsnorm_bwd(x, w, dy, rmsnorm_fwd(x, w)[1]),
+    "softmax_fwd": lambda x, dy: softmax_fwd(x),
+    "softmax_bwd": lambda x, dy: softmax_bwd(torch.softmax(x, dim=-1), dy),
+    "layernorm_backward": layernorm_backward,
+    "softmax_logits_backward": softmax_logits_backward,
+    "ffn": ffn,
+}
