@@ -103,7 +103,7 @@ int current_device_props(const DeviceProps** out) {
 }
 
 int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base) {
-  const size_t need = kWorkspaceHeader + bytes;
+  const size_t need = kScratchOffset + bytes;
   if (cfg != nullptr && cfg->workspace != nullptr) {
     if (cfg->workspace_bytes < need)
       return set_error(CREDIT_ERR_WORKSPACE,
@@ -221,7 +221,7 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
     default:
       body = 0;
   }
-  return body == 0 ? 0 : kWorkspaceHeader + body;
+  return body == 0 ? 0 : kScratchOffset + body;
 }
 
 int credit_check_watchdog(const credit_cfg* cfg) {

@@ -57,13 +57,29 @@ inline int cfg_variant(const credit_cfg* cfg) {
 }
 inline int cfg_split(const credit_cfg* cfg) { return cfg ? cfg->split : 0; }
 
-// Workspace: a zero-filled device buffer whose first 256 bytes hold the
-// watchdog word the split-row barrier raises.  Uses the caller's buffer when
-// cfg->workspace is set (it must be at least `bytes` long, 256-byte aligned,
-// and zero-filled before its first use), otherwise a per-device buffer the
-// library keeps for the life of the process.
+// Workspace layout, identical for every operation:
+//   [0, 256)                 header: the watchdog word the split-row
+//                            barrier raises
+//   [256, 256 + 64 KiB)      counter area: 16384 uint32 arrival counters /
+//                            barrier words.  Only the arrival protocols write
+//                            here and each returns its counters to zero, so
+//                            the area stays zero between calls whatever
+//                            shapes the calls have.
+//   [kScratchOffset, ...)    op-specific partials; always written before
+//                            they are read, so stale contents are harmless.
+// Uses the caller's buffer when cfg->workspace is set (at least
+// kScratchOffset + `bytes` long, 256-byte aligned, zero-filled before its
+// first use), otherwise a per-device buffer the library keeps for the life
+// of the process.
 constexpr size_t kWorkspaceHeader = 256;
+constexpr int kCounterSlots = 16384;
+constexpr size_t kScratchOffset = kWorkspaceHeader + size_t{4} * kCounterSlots;
 int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base);
+inline uint32_t* ws_watchdog(char* base) { return reinterpret_cast<uint32_t*>(base); }
+inline uint32_t* ws_counters(char* base) {
+  return reinterpret_cast<uint32_t*>(base + kWorkspaceHeader);
+}
+inline char* ws_scratch(char* base) { return base + kScratchOffset; }
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 

@@ -170,52 +170,159 @@ __device__ __forceinline__ void store_nt(u32x4* p, u32x4 v) {
   __builtin_nontemporal_store(v, p);
 }
 
+// ------------------------------------- cross-workgroup exchange (L2/MALL) --
+// CDNA4 has no distributed shared memory; workgroups exchange partials
+// through device memory.  The L2 of each XCD is not coherent with the other
+// seven, and the compiler's agent-scope acquire/release fences are whole-L2
+// maintenance operations (buffer_wbl2 / buffer_inv), far too costly to issue
+// once per workgroup.  The exchange therefore never relies on fences:
+//  - partials are published with device-scope relaxed atomic stores
+//    (global_store ... sc1: written through to the coherent level);
+//  - publish_wait() is an explicit s_waitcnt vmcnt(0): every store of this
+//    wave has been acknowledged before the arrival atomic issues;
+//  - arrival counters are device-scope atomics, performed at the coherent
+//    level for every XCD;
+//  - waiting and reading partials use device-scope relaxed atomic loads
+//    (global_load ... sc1: never served by a stale L2 line), and a wave
+//    cannot issue a load that depends on the loop exit before the spin load
+//    has returned.
+__device__ __forceinline__ void publish_wait() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ void publish(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish(double* p, double v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float fetch(const float* p) {
+  return __builtin_bit_cast(
+      float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ double fetch(const double* p) {
+  return __builtin_bit_cast(
+      double, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ uint32_t arrive(uint32_t* counter) {
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void counter_reset(uint32_t* counter) {
+  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t counter_read(const uint32_t* counter) {
+  return __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // --------------------------------------------- split-row group barrier ----
-// P workgroups that share one row meet here.  `count` returns to zero after
-// every barrier and `gen` only ever increases, so the pair needs no reset
-// between launches (a zero-filled workspace stays valid forever).  The
-// partial-sum slots the group exchanges are double-buffered by the caller on
-// the row parity: a workgroup cannot write the slots of row k+2 before every
-// member of its group has arrived at row k+1, i.e. finished reading row k.
+// P workgroups ("members") that share a row form a group.  A persistent
+// cooperative grid gives every group a sequence of rows; for the k-th row a
+// member publishes its partial, arrives on the group's counter of parity
+// k & 1, and later waits until all P members have arrived.
 //
+//  - Within a launch each parity counter only grows, by P per use, so the
+//    k-th use of a parity completes at count == P * (uses + 1): a member can
+//    only arrive at row k+2 after waiting for row k, so arrivals of
+//    different rows never mix on one counter.
+//  - The arrival is a returning atomic whose result is not needed until the
+//    wait, so its latency overlaps whatever the member does in between.
+//  - After a member's last wait, member 0 returns both counters to zero; a
+//    waiter that reads a value at or below its own arrival index knows the
+//    reset happened, which only follows completion.  A zero-filled counter
+//    area therefore stays valid across launches of any shape.
+//  - Partial slots are indexed by k % 4: a member cannot publish row k+4
+//    before every member has arrived at row k+2, which each does only after
+//    it has finished reading row k's slots.
+//  - The two counters of a group sit in different 128-byte lines and
+//    waiters poll with s_sleep backoff, so polling does not queue behind the
+//    arrivals.
 // Co-residency of the P members is guaranteed by the cooperative launch the
-// host uses for every kernel that calls this.  The spin is still bounded: on
+// host uses for every kernel that waits here.  The spin is still bounded: on
 // expiry it raises `*watchdog` and returns, so a broken launch produces a
 // reported error instead of a hung GPU.
-struct GroupBarrier {
-  uint32_t* count;
-  uint32_t* gen;
+constexpr int kGroupCounterStride = 64;  // uint32 slots per group (2 x 128 B)
+constexpr int kMaxGroups = 16384 / kGroupCounterStride;
+constexpr uint32_t kSpinLimit = 1u << 21;  // several seconds of s_sleep spins
+
+struct GroupSync {
+  uint32_t* count0;  // parity-0 counter
+  uint32_t* count1;  // parity-1 counter (different cache line)
+  uint32_t members;
+  uint32_t uses[2];
+  uint32_t old[2];
 };
 
-constexpr uint32_t kSpinLimit = 1u << 22;  // ~0.3 s of s_sleep 1 spins
+__device__ __forceinline__ GroupSync group_sync_init(uint32_t* counter_area, int group,
+                                                     int members) {
+  GroupSync s;
+  s.count0 = counter_area + group * kGroupCounterStride;
+  s.count1 = s.count0 + kGroupCounterStride / 2;
+  s.members = static_cast<uint32_t>(members);
+  s.uses[0] = s.uses[1] = 0;
+  s.old[0] = s.old[1] = 0;
+  return s;
+}
 
-__device__ __forceinline__ void group_barrier(GroupBarrier b, uint32_t members,
-                                              uint32_t* watchdog) {
-  __syncthreads();  // every thread's slot writes precede the arrival
+// Called by every thread after this member's partial stores; only thread 0
+// touches the counter.
+__device__ __forceinline__ void group_arrive(GroupSync& s, int k) {
+  publish_wait();
+  __syncthreads();
+  if (threadIdx.x == 0) s.old[k & 1] = arrive((k & 1) ? s.count1 : s.count0);
+}
+
+__device__ __forceinline__ void group_wait(GroupSync& s, int k, uint32_t* watchdog) {
+  const int p = k & 1;
   if (threadIdx.x == 0) {
-    const uint32_t my_gen =
-        __hip_atomic_load(b.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t old = __hip_atomic_fetch_add(
-        b.count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == members - 1) {
-      __hip_atomic_store(b.count, 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(b.gen, 1u, __ATOMIC_RELEASE,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      uint32_t spins = 0;
-      while (__hip_atomic_load(b.gen, __ATOMIC_ACQUIRE,
-                               __HIP_MEMORY_SCOPE_AGENT) == my_gen) {
-        __builtin_amdgcn_s_sleep(1);
-        if (++spins > kSpinLimit) {
-          __hip_atomic_store(watchdog, 1u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
+    const uint32_t target = s.members * (s.uses[p] + 1);
+    const uint32_t mine = s.old[p];
+    const uint32_t* c = p ? s.count1 : s.count0;
+    uint32_t spins = 0;
+    for (;;) {
+      const uint32_t v = counter_read(c);
+      if (v >= target || v <= mine) break;
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
       }
     }
   }
+  s.uses[p] += 1;
   __syncthreads();
+}
+
+// After the member's last wait: member 0 returns the counters to zero.
+__device__ __forceinline__ void group_finish(GroupSync& s, int member) {
+  if (member == 0 && threadIdx.x == 0) {
+    counter_reset(s.count0);
+    counter_reset(s.count1);
+  }
+}
+
+// Block -> (group, member) for a persistent split grid of groups x members
+// workgroups.  Workgroups are dispatched to the 8 XCDs round-robin, so
+// ids congruent mod 8 share an XCD: member m of group g is workgroup
+// (g / 8) * 8 * members + m * 8 + g % 8 whenever the group count is a
+// multiple of 8, and the group's exchange then stays on one XCD.
+__device__ __forceinline__ void split_coords(int members, int groups, int* group, int* member) {
+  const int b = blockIdx.x;
+  if ((groups & 7) == 0) {
+    const int tile = b / (8 * members);
+    const int within = b - tile * 8 * members;
+    *group = tile * 8 + (within & 7);
+    *member = within >> 3;
+  } else {
+    *group = b / members;
+    *member = b - *group * members;
+  }
 }
 
 // e^x through the hardware base-2 exponential (v_exp_f32).  The product

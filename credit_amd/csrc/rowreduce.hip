@@ -9,8 +9,8 @@
 //            in flight per lane; sum in fp64, max with v_maximum3_f32.
 //  - SPLIT : P workgroups per row each reduce a 1/P slice and deposit a
 //            partial in the workspace; the last to arrive (device-scope
-//            acq_rel counter) folds the P partials in slice order and resets
-//            the counter.  No workgroup ever waits on another, so the split
+//            counter) folds the P partials in slice order and resets the
+//            counter.  No workgroup ever waits on another, so the split
 //            needs no co-residency guarantee and stays deterministic.
 // Algorithmic traffic per row: 4*cols bytes read + 8 bytes written.
 #include "api_internal.hpp"
@@ -111,11 +111,10 @@ __global__ __launch_bounds__(THREADS) void row_sum_max_split_kernel(
   __shared__ int is_last;
   if (threadIdx.x == 0) {
     const size_t slot = static_cast<size_t>(row) * split + slice;
-    part_sum[slot] = r.s;
-    part_max[slot] = r.m;
-    const uint32_t old = __hip_atomic_fetch_add(
-        arrivals + row, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = old == static_cast<uint32_t>(split - 1);
+    publish(part_sum + slot, r.s);
+    publish(part_max + slot, r.m);
+    publish_wait();
+    is_last = arrive(arrivals + row) == static_cast<uint32_t>(split - 1);
   }
   __syncthreads();
   if (is_last && threadIdx.x == 0) {
@@ -123,27 +122,28 @@ __global__ __launch_bounds__(THREADS) void row_sum_max_split_kernel(
     double s = 0.0;
     float m = -__builtin_inff();
     for (int k = 0; k < split; ++k) {
-      s += part_sum[base + k];
-      m = fmax_nan(m, part_max[base + k]);
+      s += fetch(part_sum + base + k);
+      m = fmax_nan(m, fetch(part_max + base + k));
     }
     sum_out[row] = static_cast<float>(s);
     max_out[row] = m;
-    __hip_atomic_store(arrivals + row, 0u, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    counter_reset(arrivals + row);
   }
 }
 
 struct SplitLayout {
-  size_t part_sum_off, part_max_off, arrivals_off, bytes;
+  size_t part_sum_off, part_max_off, bytes;
 };
 
+// Partials for one launch of at most kCounterSlots rows (the arrival
+// counters live in the workspace's counter area, one per row of a launch).
 SplitLayout split_layout(int64_t rows, int split) {
   SplitLayout l;
-  const size_t slots = static_cast<size_t>(rows) * split;
+  const int64_t launch_rows = rows < kCounterSlots ? rows : kCounterSlots;
+  const size_t slots = static_cast<size_t>(launch_rows) * split;
   l.part_sum_off = 0;
   l.part_max_off = align_up(slots * sizeof(double), 256);
-  l.arrivals_off = l.part_max_off + align_up(slots * sizeof(float), 256);
-  l.bytes = l.arrivals_off + align_up(static_cast<size_t>(rows) * 4, 256);
+  l.bytes = l.part_max_off + align_up(slots * sizeof(float), 256);
   return l;
 }
 
@@ -222,15 +222,15 @@ extern "C" int credit_row_sum_max_f32(const float* x, float* sum, float* max,
   const SplitLayout l = split_layout(rows, split);
   char* ws = nullptr;
   CREDIT_TRY(acquire_workspace(cfg, l.bytes, &ws));
-  char* base = ws + kWorkspaceHeader;
-  const int64_t grid = rows * split;
-  if (grid > (int64_t{1} << 31) - 1)
-    return set_error(CREDIT_ERR_BAD_SHAPE, "rows*split exceeds the grid limit");
-  row_sum_max_split_kernel<kRowThreads>
-      <<<dim3(static_cast<unsigned>(grid)), dim3(kRowThreads), 0, stream>>>(
-          x, sum, max, c, split, chunk,
-          reinterpret_cast<double*>(base + l.part_sum_off),
-          reinterpret_cast<float*>(base + l.part_max_off),
-          reinterpret_cast<uint32_t*>(base + l.arrivals_off));
-  return check_launch("row_sum_max_split_kernel");
+  char* scratch = ws_scratch(ws);
+  for (int64_t r0 = 0; r0 < rows; r0 += kCounterSlots) {
+    const int64_t n = rows - r0 < kCounterSlots ? rows - r0 : kCounterSlots;
+    row_sum_max_split_kernel<kRowThreads>
+        <<<dim3(static_cast<unsigned>(n * split)), dim3(kRowThreads), 0, stream>>>(
+            x + r0 * cols, sum + r0, max + r0, c, split, chunk,
+            reinterpret_cast<double*>(scratch + l.part_sum_off),
+            reinterpret_cast<float*>(scratch + l.part_max_off), ws_counters(ws));
+    CREDIT_TRY(check_launch("row_sum_max_split_kernel"));
+  }
+  return CREDIT_OK;
 }

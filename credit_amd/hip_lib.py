@@ -109,6 +109,11 @@ SIGNATURES: dict[str, list] = {
     "credit_check_watchdog": [_CFG],
     "credit_row_sum_max_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_layernorm_fwd_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _CFG],
+    "credit_microbench": [ctypes.c_int32, _I64, ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
+                          ctypes.c_int32],
+    "credit_control_overhead": [_I64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
+                                ctypes.POINTER(ctypes.c_double)],
 }
 _RESTYPES = {
     "credit_version": ctypes.c_char_p,
@@ -209,6 +214,38 @@ def _rows_cols(x: torch.Tensor) -> tuple[int, int]:
     if x.dim() != 2:
         raise ValueError(f"expected a 2-D tensor, got shape {tuple(x.shape)}")
     return int(x.shape[0]), int(x.shape[1])
+
+
+MICROBENCH = {
+    "hbm_read": 1,
+    "hbm_write": 2,
+    "hbm_copy": 3,
+    "clock": 4,
+    "latency": 5,
+    "lds_read": 6,
+    "lds_write": 7,
+    "exchange_roundtrip": 8,
+}
+
+
+def microbench(name: str, nbytes: int = 0, iters: int = 0, n_results: int = 16) -> list[float]:
+    """Run one gfx950 calibration microbenchmark (include/credit.h)."""
+    out = (ctypes.c_double * n_results)()
+    check(load_library().credit_microbench(MICROBENCH[name], nbytes, iters, out, n_results),
+          "credit_microbench")
+    return list(out)
+
+
+def control_overhead(rows: int, split: int, barriers: int, warmup: int = 3, iters: int = 20,
+                     xcd_local: bool = True) -> tuple[float, float]:
+    """(plain_ms, split_ms): cooperative grid with `barriers` arrival barriers
+    per group against a plain launch (replaces build/cluster_control)."""
+    plain = ctypes.c_double()
+    split_ms = ctypes.c_double()
+    check(load_library().credit_control_overhead(rows, split, barriers, warmup, iters, int(xcd_local),
+                                                 ctypes.byref(plain), ctypes.byref(split_ms)),
+          "credit_control_overhead")
+    return plain.value, split_ms.value
 
 
 # --------------------------------------------------------------- operators --

@@ -147,6 +147,45 @@ int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamma,
                               float* rstd, int64_t rows, int64_t cols,
                               float eps, const credit_cfg* cfg);
 
+/* ------------------------------------------- calibration (gfx950) -------
+ * Replaces the reference's build/primitive_benchmark executable
+ * (src/primitive_benchmark.cu:605-993, its stdout parsed by
+ * dsmem_eval/profile.py:27-103).  Allocates its own buffers and runs on the
+ * null stream of the current device.  results[] layout per benchmark:
+ *   HBM_READ/WRITE/COPY : [0] best GB/s, [1..] GB/s of each kernel shape
+ *                         tried (bytes = buffer size, default 1 GiB,
+ *                         three rotating buffer sets)
+ *   CLOCK               : [0] shader clock in MHz (s_memtime vs the 100 MHz
+ *                         s_memrealtime)
+ *   LATENCY             : [0..3] cycles per dependent load with working sets
+ *                         of 16 KiB, 2 MiB, 64 MiB and 1 GiB (L1, L2, MALL,
+ *                         HBM); iters = chain steps
+ *   LDS_READ/WRITE      : [0] bytes per cycle per CU (one workgroup per CU)
+ *   EXCHANGE_ROUNDTRIP  : [0] cycles per device-scope atomic round trip
+ *                         between two workgroups on one XCD, [1] on two
+ *                         XCDs (iters = rounds); the gfx950 stand-in for
+ *                         the reference's DSMEM latency/visibility tests */
+#define CREDIT_MB_HBM_READ 1
+#define CREDIT_MB_HBM_WRITE 2
+#define CREDIT_MB_HBM_COPY 3
+#define CREDIT_MB_CLOCK 4
+#define CREDIT_MB_LATENCY 5
+#define CREDIT_MB_LDS_READ 6
+#define CREDIT_MB_LDS_WRITE 7
+#define CREDIT_MB_EXCHANGE_ROUNDTRIP 8
+int credit_microbench(int32_t which, int64_t bytes, int32_t iters, double* results,
+                      int32_t n_results);
+
+/* Replaces build/cluster_control (src/cluster_control.cu:114-180, read at
+ * dsmem_eval/runner.py:313-347): time of a cooperative grid whose groups of
+ * `split` workgroups meet at `barriers` arrival barriers, against a plain
+ * launch of the same grid that does nothing.  The grid covers min(rows,
+ * co-resident capacity / split) groups.  xcd_local != 0 places a group's
+ * members on one XCD (workgroup ids congruent mod 8). */
+int credit_control_overhead(int64_t rows, int32_t split, int32_t barriers, int32_t warmup,
+                            int32_t iters, int32_t xcd_local, double* plain_ms,
+                            double* split_ms);
+
 #ifdef __cplusplus
 }
 #endif
