@@ -1,0 +1,184 @@
+"""gfx950 calibration: run the microbenchmarks and build a DeviceProfile.
+
+The reference runs ``build/primitive_benchmark`` in a subprocess and parses
+its human-readable stdout with regular expressions
+(dsmem_eval/profile.py:27-103, dsmem_eval/runner.py:248-255), then folds the
+numbers into a ``DeviceProfile`` (dsmem_eval/profile.py:106-126).  Here the
+microbenchmarks are calls into ``libcredit_hip.so`` (``credit_microbench``,
+``credit_control_overhead``) and the profile is built from their results
+directly.  ``format_profile_text`` / ``parse_profile_text`` keep a text form
+with one ``Key: value unit`` line per measurement, so a saved calibration can
+be re-read without a GPU, as the reference re-reads ``primitive_stdout.txt``.
+
+CDNA4 has no distributed shared memory.  The reference's DSMEM figures
+(cluster sync latency, DSMEM store throughput, store-visibility round trip;
+src/primitive_benchmark.cu:236-566) are replaced by the costs of the
+split-row exchange this library uses: device-scope atomic round trips
+between two workgroups on one XCD and on two XCDs, and the time of a
+P-member arrival barrier inside a cooperative grid.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import re
+import sys
+from dataclasses import asdict
+from typing import Any
+
+from . import hip_lib
+from .cost_model import DeviceProfile
+
+FLOAT = r"([0-9]+(?:\.[0-9]+)?(?:[eE][-+]?[0-9]+)?)"
+
+# (key in the parsed dict, text label, unit) -- the text protocol.
+TEXT_KEYS: tuple[tuple[str, str, str], ...] = (
+    ("clock_ghz", "Clock frequency", "GHz"),
+    ("cu_count", "CU count", ""),
+    ("xcd_count", "XCD count", ""),
+    ("lds_bytes_per_cu", "LDS per CU", "bytes"),
+    ("max_lds_bytes_per_block", "LDS per workgroup", "bytes"),
+    ("l2_capacity_bytes", "L2 capacity", "bytes"),
+    ("l1_latency_cycles", "L1 read latency", "cycles"),
+    ("l2_latency_cycles", "L2 read latency", "cycles"),
+    ("mall_latency_cycles", "MALL read latency", "cycles"),
+    ("hbm_latency_cycles", "HBM read latency", "cycles"),
+    ("hbm_read_gbps", "HBM read bandwidth", "GB/s"),
+    ("hbm_write_gbps", "HBM write bandwidth", "GB/s"),
+    ("hbm_copy_gbps", "HBM copy bandwidth", "GB/s"),
+    ("lds_read_bytes_per_cycle_cu", "LDS read throughput", "B/cycle/CU"),
+    ("lds_write_bytes_per_cycle_cu", "LDS write throughput", "B/cycle/CU"),
+    ("exchange_roundtrip_cycles_xcd", "Exchange round trip same XCD", "cycles"),
+    ("exchange_roundtrip_cycles_cross", "Exchange round trip cross XCD", "cycles"),
+)
+
+
+def run_microbenchmarks(hbm_bytes: int = 1 << 30, iters: int = 20) -> dict[str, Any]:
+    """Run every gfx950 microbenchmark once on device 0 (the current device)."""
+    info = hip_lib.query_device(0)
+    clock_mhz = hip_lib.microbench("clock")[0]
+    lat = hip_lib.microbench("latency", 0, 20000, 4)
+    read = hip_lib.microbench("hbm_read", hbm_bytes, iters)
+    write = hip_lib.microbench("hbm_write", hbm_bytes, iters)
+    copy = hip_lib.microbench("hbm_copy", hbm_bytes, iters)
+    lds_r = hip_lib.microbench("lds_read", 0, 4096)[0]
+    lds_w = hip_lib.microbench("lds_write", 0, 4096)[0]
+    rt = hip_lib.microbench("exchange_roundtrip", 0, 2000, 2)
+    return {
+        "name": info["name"],
+        "arch": info["arch"],
+        "clock_ghz": clock_mhz / 1000.0,
+        "cu_count": info["cu_count"],
+        "xcd_count": info["xcd_count"],
+        "lds_bytes_per_cu": info["lds_bytes_per_cu"],
+        "max_lds_bytes_per_block": info["lds_bytes_per_block"],
+        "l2_capacity_bytes": info["l2_bytes"],
+        "l1_latency_cycles": lat[0],
+        "l2_latency_cycles": lat[1],
+        "mall_latency_cycles": lat[2],
+        "hbm_latency_cycles": lat[3],
+        "hbm_read_gbps": read[0],
+        "hbm_write_gbps": write[0],
+        "hbm_copy_gbps": copy[0],
+        "hbm_read_shapes_gbps": [v for v in read[1:] if v > 0],
+        "hbm_copy_shapes_gbps": [v for v in copy[1:] if v > 0],
+        "lds_read_bytes_per_cycle_cu": lds_r,
+        "lds_write_bytes_per_cycle_cu": lds_w,
+        "exchange_roundtrip_cycles_xcd": rt[0],
+        "exchange_roundtrip_cycles_cross": rt[1],
+    }
+
+
+def run_control_sweep(rows: int = 1024, splits=(2, 4, 8, 16), barriers=(1, 2, 3),
+                      warmup: int = 3, iters: int = 20) -> list[dict[str, Any]]:
+    """credit_control_overhead over (P, barriers) for both group placements.
+    Replaces the per-shape build/cluster_control runs of
+    dsmem_eval/runner.py:313-347."""
+    out = []
+    for p in splits:
+        for b in barriers:
+            for xcd_local in (True, False):
+                plain, split = hip_lib.control_overhead(rows, p, b, warmup, iters, xcd_local)
+                out.append({"rows": rows, "split": p, "barriers": b, "xcd_local": xcd_local,
+                            "plain_ms": plain, "split_ms": split,
+                            "overhead_ms": max(split - plain, 0.0)})
+    return out
+
+
+def format_profile_text(parsed: dict[str, Any]) -> str:
+    lines = [f"GPU Model: {parsed['name']}"]
+    for key, label, unit in TEXT_KEYS:
+        value = parsed[key]
+        text = f"{value:.6g}" if isinstance(value, float) else str(value)
+        lines.append(f"{label}: {text} {unit}".rstrip())
+    return "\n".join(lines) + "\n"
+
+
+def parse_profile_text(text: str) -> dict[str, Any]:
+    """Inverse of format_profile_text (the role of
+    dsmem_eval/profile.py:27-103).  Raises if a key is missing."""
+    m = re.search(r"^GPU Model:\s*(.+)$", text, flags=re.MULTILINE)
+    if m is None:
+        raise RuntimeError("calibration text does not name the GPU model")
+    parsed: dict[str, Any] = {"name": m.group(1).strip()}
+    for key, label, _unit in TEXT_KEYS:
+        m = re.search(rf"^{re.escape(label)}:\s*{FLOAT}", text, flags=re.MULTILINE)
+        if m is None:
+            raise RuntimeError(f"calibration text does not report {label}")
+        v = float(m.group(1))
+        parsed[key] = int(v) if key in ("cu_count", "xcd_count", "lds_bytes_per_cu",
+                                        "max_lds_bytes_per_block", "l2_capacity_bytes") else v
+    return parsed
+
+
+def make_device_profile(parsed: dict[str, Any]) -> DeviceProfile:
+    """Fold the measurements into the cost model's DeviceProfile
+    (dsmem_eval/profile.py:106-126 does this for the DSMEM fields)."""
+    return DeviceProfile(
+        name=str(parsed["name"]),
+        cu_count=int(parsed["cu_count"]),
+        xcd_count=int(parsed["xcd_count"]),
+        clock_ghz=float(parsed["clock_ghz"]),
+        hbm_read_gbps=float(parsed["hbm_read_gbps"]),
+        hbm_copy_gbps=float(parsed["hbm_copy_gbps"]),
+        l2_capacity_bytes=int(parsed["l2_capacity_bytes"]),
+        lds_bytes_per_cu=int(parsed["lds_bytes_per_cu"]),
+        max_lds_bytes_per_block=int(parsed["max_lds_bytes_per_block"]),
+        lds_read_bytes_per_cycle_cu=float(parsed["lds_read_bytes_per_cycle_cu"]),
+        lds_write_bytes_per_cycle_cu=float(parsed["lds_write_bytes_per_cycle_cu"]),
+        exchange_roundtrip_cycles=float(parsed["exchange_roundtrip_cycles_xcd"]),
+        hbm_latency_cycles=float(parsed["hbm_latency_cycles"]),
+    )
+
+
+def profile_as_dict(profile: DeviceProfile) -> dict[str, Any]:
+    return asdict(profile)
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="gfx950 calibration microbenchmarks")
+    ap.add_argument("--hbm-bytes", type=int, default=1 << 30)
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--control", action="store_true", help="also sweep the barrier overhead")
+    ap.add_argument("--json", help="write the measurements (and control sweep) here")
+    args = ap.parse_args(argv)
+    import torch  # noqa: F401  (loads the HIP runtime torch uses before the library)
+
+    parsed = run_microbenchmarks(args.hbm_bytes, args.iters)
+    sys.stdout.write(format_profile_text(parsed))
+    result: dict[str, Any] = {"measurements": parsed,
+                              "cost_model_profile": profile_as_dict(make_device_profile(parsed))}
+    if args.control:
+        result["control"] = run_control_sweep()
+        for row in result["control"]:
+            print("CONTROL,{rows},{split},{barriers},{xcd_local:d},{plain_ms:.6f},{split_ms:.6f},"
+                  "{overhead_ms:.6f}".format(**row))
+    if args.json:
+        with open(args.json, "w", encoding="utf-8") as fh:
+            json.dump(result, fh, indent=2)
+    sys.stdout.flush()
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
