@@ -46,11 +46,39 @@ def parse_args(argv=None):
 # ----------------------------------------------------------- GPU timing ---
 
 
+def prepare_inputs(name, cpu_inputs, hip_lib, torch, dev):
+    """Launcher inputs on the GPU.  The backward passes take what their
+    forward produced (rstd, p); it is computed here by this library's own
+    forward kernels, outside the timed region."""
+    ins = tuple(t.to(dev) for t in cpu_inputs)
+    if name == "rmsnorm_fwd":
+        return ins[:2]
+    if name == "rmsnorm_bwd":
+        x, w, dy = ins
+        y, rstd = hip_lib.allocate_outputs("rmsnorm_fwd", (x, w))
+        hip_lib.HIP_LAUNCHERS["rmsnorm_fwd"]((x, w), (y, rstd))
+        del y
+        return x, w, dy, rstd
+    if name == "softmax_fwd":
+        return ins[:1]
+    if name == "ffn":
+        x, w1, w2 = ins  # BASELINE layout: W1 [d, f], W2 [f, d]
+        return x, hip_lib.linear_layout(w1), hip_lib.linear_layout(w2)
+    if name == "softmax_bwd":
+        x, dy = ins
+        p, m, lse = hip_lib.allocate_outputs("softmax_fwd", (x,))
+        hip_lib.HIP_LAUNCHERS["softmax_fwd"]((x,), (p, m, lse))
+        del x, m, lse
+        return p, dy
+    return ins
+
+
 def build_case(name, spec, hip_lib, torch, dev, nsets):
     """Inputs (resident), rotating output sets and a launch(set_index, variant, split)."""
     cpu_inputs = spec.make_inputs()
-    inputs = [tuple(t.to(dev) for t in cpu_inputs) for _ in range(nsets)]
+    inputs = [prepare_inputs(name, cpu_inputs, hip_lib, torch, dev) for _ in range(nsets)]
     outputs = [hip_lib.allocate_outputs(name, ins) for ins in inputs]
+    torch.cuda.synchronize()
     launcher = hip_lib.HIP_LAUNCHERS[name]
 
     def launch(i, variant="auto", split=0):
@@ -184,6 +212,11 @@ def measure(name, args, hip_lib, torch, dev, with_cpu):
 VARIANT_SWEEP = {
     "row_sum_max": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
     "layernorm_fwd": [("read", 0), ("staged", 0)],
+    "rmsnorm_fwd": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
+    "rmsnorm_bwd": [("read", 0), ("split", 8), ("split", 16)],
+    "softmax_fwd": [("read", 0), ("split", 4), ("split", 8), ("split", 16)],
+    "softmax_bwd": [("read", 0), ("split", 8), ("split", 16)],
+    "softmax_logits_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
 }
 
 
@@ -227,7 +260,7 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if args.workload in ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd", "ffn") else "fp32",
+        "dtype": "bf16" if args.workload in ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd", "ffn") else "f32",
         "data": "synthetic (seeded CPU generator, BASELINE distributions)",
         "config": {"workload": args.workload, "rows": head["rows"], "cols": head["cols"],
                    "device": info["name"], "arch": info["arch"], "cus": info["cu_count"],

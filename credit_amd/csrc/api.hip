@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "api_internal.hpp"
+#include "common.hpp"
 
 namespace credit {
 
@@ -138,6 +139,24 @@ int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base) {
   return CREDIT_OK;
 }
 
+__global__ void fill_f32_kernel(float* __restrict__ p, float v, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
+                            int k_values, size_t extra_bytes, SplitWorkspace* out) {
+  const size_t slot_bytes =
+      align_up(split_slot_bytes(groups, members, k_values), 256);
+  char* base = nullptr;
+  CREDIT_TRY(acquire_workspace(cfg, slot_bytes + extra_bytes, &base));
+  out->counters = ws_counters(base);
+  out->watchdog = ws_watchdog(base);
+  out->slots = reinterpret_cast<double*>(ws_scratch(base));
+  out->extra = ws_scratch(base) + slot_bytes;
+  return CREDIT_OK;
+}
+
 int cu_count_or_default() {
   int count = 0;
   if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
@@ -218,6 +237,20 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
     case CREDIT_OP_ROW_SUM_MAX:
       body = row_sum_max_workspace(rows, cols, variant, split, cus);
       break;
+    case CREDIT_OP_RMSNORM_FWD:
+      body = rmsnorm_fwd_workspace(rows, cols, variant, split);
+      break;
+    case CREDIT_OP_RMSNORM_BWD:
+      body = rmsnorm_bwd_workspace(rows, cols, variant, split, cus);
+      break;
+    case CREDIT_OP_FFN:  // cols = the FFN hidden width f
+      body = ffn_workspace(rows, cols);
+      break;
+    case CREDIT_OP_SOFTMAX_FWD:
+    case CREDIT_OP_SOFTMAX_BWD:
+    case CREDIT_OP_SOFTMAX_LOGITS_BWD:
+      body = softmax_workspace(op, rows, cols, variant, split);
+      break;
     default:
       body = 0;
   }
@@ -232,8 +265,10 @@ int credit_check_watchdog(const credit_cfg* cfg) {
   CREDIT_HIP(hipStreamSynchronize(cfg_stream(cfg)));
   CREDIT_HIP(hipMemcpy(&flag, base, sizeof(flag), hipMemcpyDeviceToHost));
   if (flag != 0) {
-    const uint32_t zero = 0;
-    CREDIT_HIP(hipMemcpy(base, &zero, sizeof(zero), hipMemcpyHostToDevice));
+    // A barrier that gave up leaves its counters mid-protocol: return the
+    // whole header and counter area to the zero state.
+    CREDIT_HIP(hipMemset(base, 0, kScratchOffset));
+    CREDIT_HIP(hipDeviceSynchronize());
     return set_error(CREDIT_ERR_WATCHDOG,
                      "a split-row barrier exceeded its spin limit");
   }

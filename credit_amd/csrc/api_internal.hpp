@@ -45,6 +45,11 @@ int current_device_props(const DeviceProps** out);
 // Argument checks.  Every one returns CREDIT_OK or a negative status after
 // recording a message; none of them calls into HIP.
 int check_ptr(const void* p, const char* name);
+// A buffer indexed by row: NULL is accepted when there are no rows (torch
+// hands out NULL data pointers for empty tensors).
+inline int check_row_ptr(const void* p, const char* name, int64_t rows) {
+  return rows == 0 ? CREDIT_OK : check_ptr(p, name);
+}
 int check_aligned(const void* p, size_t align, const char* name);
 int check_shape(int64_t rows, int64_t cols, int64_t max_cols);
 int check_cfg(const credit_cfg* cfg);
@@ -60,11 +65,15 @@ inline int cfg_split(const credit_cfg* cfg) { return cfg ? cfg->split : 0; }
 // Workspace layout, identical for every operation:
 //   [0, 256)                 header: the watchdog word the split-row
 //                            barrier raises
-//   [256, 256 + 64 KiB)      counter area: 16384 uint32 arrival counters /
-//                            barrier words.  Only the arrival protocols write
-//                            here and each returns its counters to zero, so
-//                            the area stays zero between calls whatever
-//                            shapes the calls have.
+//   [256, 256 + 1 MiB)       counter area: 262144 uint32 slots.  The first
+//                            kDispensers lines are the ticket dispensers of
+//                            split launches; group arrival counters follow
+//                            from slot kGroupCounterBase, one 64-byte line
+//                            each.  Only
+//                            the arrival protocols write here and each
+//                            returns its counters to zero, so the area
+//                            stays zero between calls whatever shapes the
+//                            calls have.
 //   [kScratchOffset, ...)    op-specific partials; always written before
 //                            they are read, so stale contents are harmless.
 // Uses the caller's buffer when cfg->workspace is set (at least
@@ -72,9 +81,42 @@ inline int cfg_split(const credit_cfg* cfg) { return cfg ? cfg->split : 0; }
 // first use), otherwise a per-device buffer the library keeps for the life
 // of the process.
 constexpr size_t kWorkspaceHeader = 256;
-constexpr int kCounterSlots = 16384;
+constexpr int kCounterSlots = 262144;
 constexpr size_t kScratchOffset = kWorkspaceHeader + size_t{4} * kCounterSlots;
+constexpr int kDispensers = 8;           // ticket dispensers, one per blockIdx % 8
+constexpr int kDispenserStride = 16;     // one 64-byte line each
+constexpr int kGroupCounterBase = kDispensers * kDispenserStride;  // first group counter
+constexpr int kGroupCounterStride = 16;  // one 64-byte line per group counter
+constexpr int kMaxGroupsPerLaunch =
+    (kCounterSlots - kGroupCounterBase) / kGroupCounterStride / kDispensers * kDispensers;
+constexpr int kSlotRing = 4;             // stages a group's partial slots rotate over
+// Groups of a split launch are padded to a multiple of kDispensers (the
+// padding groups exit at once).
+inline int64_t padded_groups(int64_t groups) {
+  return (groups + kDispensers - 1) / kDispensers * kDispensers;
+}
+// Bytes of partial slots a split launch of `groups` groups needs.
+inline size_t split_slot_bytes(int64_t groups, int members, int k_values) {
+  return static_cast<size_t>(groups) * kSlotRing * k_values * members * sizeof(double);
+}
 int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base);
+
+// Workspace of a ticketed split launch: the counter area, the partial slots
+// of `groups` groups, then `extra_bytes` (256-byte aligned) for the
+// operation's own use.
+struct SplitWorkspace {
+  uint32_t* counters = nullptr;
+  uint32_t* watchdog = nullptr;
+  double* slots = nullptr;
+  char* extra = nullptr;
+};
+inline size_t split_workspace_bytes(int64_t groups, int members, int k_values,
+                                    size_t extra_bytes) {
+  const size_t slots = (split_slot_bytes(groups, members, k_values) + 255) / 256 * 256;
+  return slots + extra_bytes;
+}
+int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
+                            int k_values, size_t extra_bytes, SplitWorkspace* out);
 inline uint32_t* ws_watchdog(char* base) { return reinterpret_cast<uint32_t*>(base); }
 inline uint32_t* ws_counters(char* base) {
   return reinterpret_cast<uint32_t*>(base + kWorkspaceHeader);
@@ -88,6 +130,11 @@ int check_launch(const char* kernel);
 
 // Workspace sizes of the individual operations (bytes after the header).
 size_t row_sum_max_workspace(int64_t rows, int64_t cols, int variant, int split,
+                             int cu_count);
+size_t ffn_workspace(int64_t rows, int64_t ffn_dim);
+size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int split);
+size_t rmsnorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split);
+size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
                              int cu_count);
 
 // CU count of the current device, or 256 (MI355X) when none is visible.

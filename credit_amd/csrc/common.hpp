@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "api_internal.hpp"
+
 namespace credit {
 
 constexpr int kWave = 64;
@@ -156,6 +158,7 @@ __device__ __forceinline__ double block_reduce_sum_f64(double v, double* slots) 
 // nt bit) accept these, not HIP's struct-wrapped float4/uint4.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x4 load_nt(const f32x4* p) {
   return __builtin_nontemporal_load(p);
@@ -169,6 +172,8 @@ __device__ __forceinline__ void store_nt(f32x4* p, f32x4 v) {
 __device__ __forceinline__ void store_nt(u32x4* p, u32x4 v) {
   __builtin_nontemporal_store(v, p);
 }
+
+__global__ void fill_f32_kernel(float* __restrict__ p, float v, int64_t n);
 
 // ------------------------------------- cross-workgroup exchange (L2/MALL) --
 // CDNA4 has no distributed shared memory; workgroups exchange partials
@@ -221,115 +226,146 @@ __device__ __forceinline__ uint32_t counter_read(const uint32_t* counter) {
   return __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// --------------------------------------------- split-row group barrier ----
-// P workgroups ("members") that share a row form a group.  A persistent
-// cooperative grid gives every group a sequence of rows; for the k-th row a
-// member publishes its partial, arrives on the group's counter of parity
-// k & 1, and later waits until all P members have arrived.
+// ------------------------------------------------ ticketed split groups ---
+// P workgroups ("members") that share a row -- or a block of rows -- form a
+// group and meet at arrival barriers to combine their partial results.
 //
-//  - Within a launch each parity counter only grows, by P per use, so the
-//    k-th use of a parity completes at count == P * (uses + 1): a member can
-//    only arrive at row k+2 after waiting for row k, so arrivals of
-//    different rows never mix on one counter.
-//  - The arrival is a returning atomic whose result is not needed until the
-//    wait, so its latency overlaps whatever the member does in between.
-//  - After a member's last wait, member 0 returns both counters to zero; a
-//    waiter that reads a value at or below its own arrival index knows the
-//    reset happened, which only follows completion.  A zero-filled counter
-//    area therefore stays valid across launches of any shape.
-//  - Partial slots are indexed by k % 4: a member cannot publish row k+4
-//    before every member has arrived at row k+2, which each does only after
-//    it has finished reading row k's slots.
-//  - The two counters of a group sit in different 128-byte lines and
-//    waiters poll with s_sleep backoff, so polling does not queue behind the
-//    arrivals.
-// Co-residency of the P members is guaranteed by the cooperative launch the
-// host uses for every kernel that waits here.  The spin is still bounded: on
-// expiry it raises `*watchdog` and returns, so a broken launch produces a
+// Membership comes from a ticket, not from blockIdx.  The grid is split into
+// kDispensers subsets by blockIdx % kDispensers, each with its own
+// device-scope ticket dispenser; thread 0 of every workgroup draws the next
+// ticket of its subset as the workgroup starts, and ticket t of subset d
+// makes it member t % P of group d * (subset size / P) + t / P.  The grid
+// is a multiple of kDispensers * P, so every subset holds whole groups.
+// Within a subset a group's members hold consecutive tickets, so every group
+// whose P tickets are drawn has all P members running, and at most one group
+// per subset (the newest) is incomplete; its missing members are later
+// workgroups of the same subset, which the dispatcher can start because
+// complete groups never wait on anything and free their slots.  A plain
+// launch is thus deadlock-free whenever the device holds kDispensers * P
+// workgroups at once: no cooperative launch (which costs ~30 us on gfx950)
+// and no co-residency of the whole grid is needed.  One dispenser per subset
+// keeps the same-address atomics off a single serialisation point (one
+// shared dispenser costs ~12 ns per workgroup of the grid), and with
+// workgroups dealt to the 8 XCDs round-robin a subset -- so a group -- sits
+// on one XCD.
+//
+// Barrier protocol, per group, on one device-scope counter:
+//  - stage j (j = 0, 1, ...): each member stores its partials into ring slot
+//    j % kSlotRing with device-scope stores, waits for them to complete
+//    (s_waitcnt vmcnt(0)), then adds 1 to the counter; it proceeds once the
+//    counter reaches P * (j + 1).  The counter only grows inside a launch.
+//  - a member reads stage j's partials right after its wait and before it
+//    arrives at stage j + 1, so nobody can overwrite slot j % kSlotRing
+//    (at stage j + kSlotRing) before every member has read it.
+//  - after its last stage a member adds 1 more ("departs"); the member that
+//    departs last returns the counter to zero.  Each dispenser is returned
+//    to zero by the workgroup that draws its subset's last ticket.  A
+//    zero-filled counter area therefore stays zero between launches.
+// Partials are combined by every member in member order, so all members
+// (and every run) get bit-identical results.  The spin is bounded: on
+// expiry it raises *watchdog and continues, so a broken launch ends with a
 // reported error instead of a hung GPU.
-constexpr int kGroupCounterStride = 64;  // uint32 slots per group (2 x 128 B)
-constexpr int kMaxGroups = 16384 / kGroupCounterStride;
-constexpr uint32_t kSpinLimit = 1u << 21;  // several seconds of s_sleep spins
+constexpr uint32_t kSpinLimit = 1u << 21;  // ~1 s of s_sleep polling
 
-struct GroupSync {
-  uint32_t* count0;  // parity-0 counter
-  uint32_t* count1;  // parity-1 counter (different cache line)
-  uint32_t members;
-  uint32_t uses[2];
-  uint32_t old[2];
+struct SplitGroup {
+  int group;
+  int member;
+  int members;
+  uint32_t* count;
+  double* slots;    // this group's slots: [kSlotRing][K][members]
+  int k_values;     // K: partials per member per stage
+  uint32_t stage;
 };
 
-__device__ __forceinline__ GroupSync group_sync_init(uint32_t* counter_area, int group,
-                                                     int members) {
-  GroupSync s;
-  s.count0 = counter_area + group * kGroupCounterStride;
-  s.count1 = s.count0 + kGroupCounterStride / 2;
-  s.members = static_cast<uint32_t>(members);
-  s.uses[0] = s.uses[1] = 0;
-  s.old[0] = s.old[1] = 0;
-  return s;
-}
-
-// Called by every thread after this member's partial stores; only thread 0
-// touches the counter.
-__device__ __forceinline__ void group_arrive(GroupSync& s, int k) {
-  publish_wait();
-  __syncthreads();
-  if (threadIdx.x == 0) s.old[k & 1] = arrive((k & 1) ? s.count1 : s.count0);
-}
-
-__device__ __forceinline__ void group_wait(GroupSync& s, int k, uint32_t* watchdog) {
-  const int p = k & 1;
+// Draw a ticket and derive (group, member).  Every thread calls it; it
+// contains one __syncthreads.  grid = gridDim.x, a multiple of
+// kDispensers * members.
+__device__ __forceinline__ SplitGroup split_join(uint32_t* counters, double* scratch,
+                                                 int members, int k_values, uint32_t grid) {
+  __shared__ uint32_t ticket_s;
+  const uint32_t subset = blockIdx.x % kDispensers;
+  const uint32_t per_subset = grid / kDispensers;
   if (threadIdx.x == 0) {
-    const uint32_t target = s.members * (s.uses[p] + 1);
-    const uint32_t mine = s.old[p];
-    const uint32_t* c = p ? s.count1 : s.count0;
+    uint32_t* dispenser = counters + subset * kDispenserStride;
+    const uint32_t t = __hip_atomic_fetch_add(dispenser, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    if (t == per_subset - 1) counter_reset(dispenser);
+    ticket_s = t;
+  }
+  __syncthreads();
+  const uint32_t t = ticket_s;
+  const uint32_t p = static_cast<uint32_t>(members);
+  SplitGroup g;
+  g.group = static_cast<int>(subset * (per_subset / p) + t / p);
+  g.member = static_cast<int>(t % p);
+  g.members = members;
+  g.count = counters + kGroupCounterBase + g.group * kGroupCounterStride;
+  g.k_values = k_values;
+  g.slots = scratch + static_cast<size_t>(g.group) * kSlotRing * k_values * members;
+  g.stage = 0;
+  return g;
+}
+
+__device__ __forceinline__ double* split_slot(const SplitGroup& g, int k, int m) {
+  return g.slots + (static_cast<int>(g.stage % kSlotRing) * g.k_values + k) * g.members + m;
+}
+
+// Thread 0 only: store this member's k-th partial of the current stage.
+__device__ __forceinline__ void split_publish(const SplitGroup& g, int k, double v) {
+  publish(split_slot(g, k, g.member), v);
+}
+
+// Every thread: arrive at the current stage's barrier and wait for all
+// members.  Afterwards split_get() reads the stage's partials.
+__device__ __forceinline__ void split_arrive_wait(SplitGroup& g, uint32_t* watchdog) {
+  if (threadIdx.x == 0) {
+    publish_wait();
+    const uint32_t target = static_cast<uint32_t>(g.members) * (g.stage + 1);
+    uint32_t v = arrive(g.count) + 1;
     uint32_t spins = 0;
-    for (;;) {
-      const uint32_t v = counter_read(c);
-      if (v >= target || v <= mine) break;
-      __builtin_amdgcn_s_sleep(2);
+    while (v < target) {
+      __builtin_amdgcn_s_sleep(1);
+      v = counter_read(g.count);
       if (++spins > kSpinLimit) {
         __hip_atomic_store(watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
     }
   }
-  s.uses[p] += 1;
   __syncthreads();
 }
 
-// After the member's last wait: member 0 returns the counters to zero.
-__device__ __forceinline__ void group_finish(GroupSync& s, int member) {
-  if (member == 0 && threadIdx.x == 0) {
-    counter_reset(s.count0);
-    counter_reset(s.count1);
+__device__ __forceinline__ double split_get(const SplitGroup& g, int k, int m) {
+  return fetch(split_slot(g, k, m));
+}
+
+// Every thread, after the stage's partials have been read.
+__device__ __forceinline__ void split_next(SplitGroup& g) { g.stage += 1; }
+
+// Thread 0 of every member after its last stage: depart; the last member to
+// depart returns the counter to zero.
+__device__ __forceinline__ void split_leave(const SplitGroup& g) {
+  if (threadIdx.x == 0) {
+    const uint32_t final_count = static_cast<uint32_t>(g.members) * (g.stage + 1);
+    if (arrive(g.count) == final_count - 1) counter_reset(g.count);
   }
 }
 
-// Block -> (group, member) for a persistent split grid of groups x members
-// workgroups.  Workgroups are dispatched to the 8 XCDs round-robin, so
-// ids congruent mod 8 share an XCD: member m of group g is workgroup
-// (g / 8) * 8 * members + m * 8 + g % 8 whenever the group count is a
-// multiple of 8, and the group's exchange then stays on one XCD.
-__device__ __forceinline__ void split_coords(int members, int groups, int* group, int* member) {
-  const int b = blockIdx.x;
-  if ((groups & 7) == 0) {
-    const int tile = b / (8 * members);
-    const int within = b - tile * 8 * members;
-    *group = tile * 8 + (within & 7);
-    *member = within >> 3;
-  } else {
-    *group = b / members;
-    *member = b - *group * members;
-  }
+// Sum of the current stage's k-th partials in member order.
+__device__ __forceinline__ double split_sum(const SplitGroup& g, int k) {
+  double s = 0.0;
+  for (int m = 0; m < g.members; ++m) s += split_get(g, k, m);
+  return s;
 }
+
 
 // e^x through the hardware base-2 exponential (v_exp_f32).  The product
 // x*log2(e) is formed as t + e with an FMA-recovered residual (Dekker's exact
 // product) plus the fp32 rounding of log2(e) itself, and the residual is
 // applied as the first-order factor (1 + e*ln 2).  The relative error stays
-// within a few ulp over the softmax argument range x in [-88, 0].
+// within a few ulp over the softmax argument range x in [-88, 0].  For
+// x = +-inf the residual is not finite and exp2(t) is already exact
+// (+inf, 0); NaN stays NaN.
 __device__ __forceinline__ float exp_accurate(float x) {
   constexpr float kLog2eHi = 1.44269502162933349609375f;
   constexpr float kLog2eLo = 1.925963033500011079013347625732421875e-8f;
@@ -337,7 +373,8 @@ __device__ __forceinline__ float exp_accurate(float x) {
   const float t = x * kLog2eHi;
   const float e = __builtin_fmaf(x, kLog2eHi, -t) + x * kLog2eLo;
   const float p = __builtin_amdgcn_exp2f(t);
-  return __builtin_fmaf(p * e, kLn2, p);
+  const float r = __builtin_fmaf(p * e, kLn2, p);
+  return __builtin_isinf(t) ? p : r;
 }
 
 }  // namespace credit

@@ -1,0 +1,276 @@
+// C5: norm-fused FFN on MFMA, bf16 with fp32 accumulation.
+//
+//   a   = bf16(x * rstd),  rstd = 1/sqrt(mean_j x^2 + eps)   (unit RMSNorm weight)
+//   h   = bf16(GELU_tanh(a @ W1^T))
+//   out = bf16(x + h @ W2^T)
+//
+// No FFN exists in the reference; this is the consumer of the row-norm
+// kernels the BASELINE names.  Weights come in the nn.Linear layout
+// ([out_features, in_features], K contiguous): W1 [f, d], W2 [d, f], so
+// both GEMMs are "A row-major x B K-contiguous" and every MFMA operand
+// fragment (8 consecutive k per lane) is one 16-byte LDS read.
+// credit_transpose_bf16 converts a [d, f] weight once.
+//
+// Kernels:
+//  1. ffn_rstd_kernel: rstd per row of x (one read of x, 64 MiB at C5).
+//  2. ffn_gemm_kernel<kEpiGelu>: GEMM1.  The A tile is scaled by rstd and
+//     rounded to bf16 while it is staged into LDS (the RMSNorm is fused into
+//     the operand load); the epilogue applies GELU-tanh and stores h.
+//  3. ffn_gemm_kernel<kEpiResidual>: GEMM2, epilogue adds x.
+// GEMM tile: 128 x 128 x 64 per 256-lane workgroup; wave (wm, wn) of the
+// 2 x 2 wave grid owns a 64 x 64 quadrant as 2 x 2 v_mfma_f32_32x32x16_bf16
+// tiles.  Global tiles are prefetched into registers one K-step ahead, so
+// the next tile's HBM/L2 latency overlaps this step's MFMAs.
+#include "api_internal.hpp"
+#include "common.hpp"
+
+namespace credit {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 64;
+constexpr int kThreads = 256;
+constexpr int kLdsStride = kBK + 8;  // bf16 per LDS row: 16-byte pad against bank conflicts
+
+constexpr int kEpiGelu = 0;
+constexpr int kEpiResidual = 1;
+
+// GELU with the tanh approximation; tanh(u) = 1 - 2 / (e^(2u) + 1), which
+// saturates correctly for |u| large (e^(2u) -> inf or 0).
+__device__ __forceinline__ float gelu_tanh(float v) {
+  constexpr float kC = 0.7978845608028654f;  // sqrt(2/pi)
+  const float u = kC * (v + 0.044715f * v * v * v);
+  const float t = 1.0f - 2.0f / (exp_accurate(2.0f * u) + 1.0f);
+  return 0.5f * v * (1.0f + t);
+}
+
+__device__ __forceinline__ u32x4 scale_bf16x8(u32x4 v, float s) {
+  return u32x4{pack_bf16x2(bf16_lo(v.x) * s, bf16_hi(v.x) * s),
+               pack_bf16x2(bf16_lo(v.y) * s, bf16_hi(v.y) * s),
+               pack_bf16x2(bf16_lo(v.z) * s, bf16_hi(v.z) * s),
+               pack_bf16x2(bf16_lo(v.w) * s, bf16_hi(v.w) * s)};
+}
+
+// rstd[m] = 1/sqrt(mean(x[m]^2) + eps); cols % 8 == 0, rows 16-byte aligned.
+__global__ __launch_bounds__(256) void ffn_rstd_kernel(const uint16_t* __restrict__ x,
+                                                       float* __restrict__ rstd, int cols,
+                                                       float eps) {
+  __shared__ double red[4];
+  const u32x4* xr = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(blockIdx.x) * cols);
+  const int nvec = cols >> 3;
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < nvec; i += 256) {
+    const u32x4 v = xr[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = bf16_lo(v[e]), hi = bf16_hi(v[e]);
+      s += lo * lo + hi * hi;
+    }
+  }
+  const double t = block_reduce_sum_f64<4>(static_cast<double>(s), red);
+  if (threadIdx.x == 0) rstd[blockIdx.x] = static_cast<float>(1.0 / __builtin_sqrt(t / cols + eps));
+}
+
+// C[m, n] = epi(sum_k A[m, k] * B[n, k]).  A [M, K] and B [N, K] row-major
+// bf16; M % 128 == 0, N % 128 == 0, K % 64 == 0 (checked on the host).
+//  kEpiGelu:     A rows scaled by a_scale[m] on load; C = bf16(gelu(acc)).
+//  kEpiResidual: C = bf16(acc + R[m, n]).
+template <int EPI>
+__global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
+    const uint16_t* __restrict__ A, const float* __restrict__ a_scale,
+    const uint16_t* __restrict__ B, const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
+    int M, int N, int K) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[kBM * kLdsStride];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[kBN * kLdsStride];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  // Tile order: consecutive workgroups walk down M for a fixed N strip, so
+  // the B strip (the weight tile) is reused from L2 by neighbours.
+  const int tiles_m = M / kBM;
+  const int tm = blockIdx.x % tiles_m;
+  const int tn = blockIdx.x / tiles_m;
+  const int m0 = tm * kBM, n0 = tn * kBN;
+
+  // Global -> register staging: thread t moves rows t/8 + 32*i, 16-byte
+  // chunk t%8 of the 128-byte K-row, for i = 0..3 (A and B alike).
+  const int ld_row = tid >> 3;
+  const int ld_chunk = tid & 7;
+  const u32x4* a_src[4];
+  const u32x4* b_src[4];
+  float scale[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = ld_row + 32 * i;
+    a_src[i] = reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m0 + r) * K) + ld_chunk;
+    b_src[i] = reinterpret_cast<const u32x4*>(B + static_cast<size_t>(n0 + r) * K) + ld_chunk;
+    scale[i] = EPI == kEpiGelu ? a_scale[m0 + r] : 1.0f;
+  }
+  u32x4 ra[4], rb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    ra[i] = a_src[i][0];
+    rb[i] = b_src[i][0];
+  }
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int ksteps = K / kBK;
+  for (int ks = 0; ks < ksteps; ++ks) {
+    __syncthreads();  // previous step's fragment reads are done
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = ld_row + 32 * i;
+      const u32x4 av = EPI == kEpiGelu ? scale_bf16x8(ra[i], scale[i]) : ra[i];
+      *reinterpret_cast<u32x4*>(&As[r * kLdsStride + ld_chunk * 8]) = av;
+      *reinterpret_cast<u32x4*>(&Bs[r * kLdsStride + ld_chunk * 8]) = rb[i];
+    }
+    __syncthreads();
+    if (ks + 1 < ksteps) {  // prefetch the next K-step into registers
+      const int off = (ks + 1) * (kBK / 8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ra[i] = a_src[i][off];
+        rb[i] = b_src[i][off];
+      }
+    }
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      const int kcol = kk * 16 + (lane >> 5) * 8;
+      bf16x8_t af[2], bfr[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r = wm * 64 + i * 32 + (lane & 31);
+        af[i] = *reinterpret_cast<const bf16x8_t*>(&As[r * kLdsStride + kcol]);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int c = wn * 64 + j * 32 + (lane & 31);
+        bfr[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[c * kLdsStride + kcol]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Epilogue.  Accumulator register r of lane l holds row
+  // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of the 32 x 32 tile.
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+        const size_t idx = static_cast<size_t>(m) * N + n;
+        float v = acc[i][j][r];
+        if (EPI == kEpiGelu)
+          v = gelu_tanh(v);
+        else
+          v += bf16_to_f32(R[idx]);
+        C[idx] = f32_to_bf16(v);
+      }
+}
+
+// dst[c, r] = src[r, c] for a rows x cols bf16 matrix, through a 64 x 64
+// LDS tile.
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src,
+                                                             uint16_t* __restrict__ dst,
+                                                             int rows, int cols) {
+  __shared__ uint16_t tile[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    const int r = r0 + i, c = c0 + tx;
+    if (r < rows && c < cols) tile[i][tx] = src[static_cast<size_t>(r) * cols + c];
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int c = c0 + i, r = r0 + tx;
+    if (r < rows && c < cols) dst[static_cast<size_t>(c) * rows + r] = tile[tx][i];
+  }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+
+size_t ffn_workspace(int64_t rows, int64_t ffn_dim) {
+  return align_up(static_cast<size_t>(rows) * sizeof(float), 256) +
+         align_up(static_cast<size_t>(rows) * ffn_dim * sizeof(uint16_t), 256);
+}
+
+}  // namespace credit
+
+using namespace credit;
+
+extern "C" int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t rows,
+                                     int64_t cols, const credit_cfg* cfg) {
+  CREDIT_TRY(check_row_ptr(src, "src", rows));
+  CREDIT_TRY(check_row_ptr(dst, "dst", rows));
+  CREDIT_TRY(check_shape(rows, cols, int64_t{1} << 30));
+  CREDIT_TRY(check_cfg(cfg));
+  if (rows == 0) return CREDIT_OK;
+  if (rows > (int64_t{1} << 30))
+    return set_error(CREDIT_ERR_BAD_SHAPE, "transpose supports at most 2^30 rows");
+  const dim3 grid(static_cast<unsigned>((cols + 63) / 64), static_cast<unsigned>((rows + 63) / 64));
+  transpose_bf16_kernel<<<grid, 256, 0, cfg_stream(cfg)>>>(src, dst, static_cast<int>(rows),
+                                                           static_cast<int>(cols));
+  return check_launch("transpose_bf16_kernel");
+}
+
+extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w1,
+                                            const uint16_t* w2, uint16_t* out, int64_t rows,
+                                            int64_t d, int64_t f, float eps,
+                                            const credit_cfg* cfg) {
+  CREDIT_TRY(check_row_ptr(x, "x", rows));
+  CREDIT_TRY(check_ptr(w1, "w1"));
+  CREDIT_TRY(check_ptr(w2, "w2"));
+  CREDIT_TRY(check_row_ptr(out, "out", rows));
+  CREDIT_TRY(check_cfg(cfg));
+  if (rows < 0 || d < 1 || f < 1)
+    return set_error(CREDIT_ERR_BAD_SHAPE, "ffn: need rows >= 0, d >= 1, f >= 1");
+  if (!(eps >= 0.0f)) return set_error(CREDIT_ERR_BAD_CONFIG, "eps must be >= 0");
+  if (rows % kBM != 0 || d % kBN != 0 || f % kBN != 0 || d % kBK != 0 || f % kBK != 0)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "ffn: rows, d and f must be multiples of 128 (got %lld, %lld, %lld)",
+                     static_cast<long long>(rows), static_cast<long long>(d),
+                     static_cast<long long>(f));
+  if (rows > (int64_t{1} << 24) || d > (int64_t{1} << 20) || f > (int64_t{1} << 20))
+    return set_error(CREDIT_ERR_BAD_SHAPE, "ffn: shape too large");
+  if (!aligned16(x) || !aligned16(w1) || !aligned16(w2) || !aligned16(out))
+    return set_error(CREDIT_ERR_ALIGNMENT, "ffn: x, w1, w2 and out must be 16-byte aligned");
+  if (rows == 0) return CREDIT_OK;
+  char* ws = nullptr;
+  CREDIT_TRY(acquire_workspace(cfg, ffn_workspace(rows, f), &ws));
+  float* rstd = reinterpret_cast<float*>(ws_scratch(ws));
+  uint16_t* h = reinterpret_cast<uint16_t*>(
+      ws_scratch(ws) + align_up(static_cast<size_t>(rows) * sizeof(float), 256));
+  hipStream_t stream = cfg_stream(cfg);
+  const int M = static_cast<int>(rows), D = static_cast<int>(d), F = static_cast<int>(f);
+  ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, D, eps);
+  CREDIT_TRY(check_launch("ffn_rstd_kernel"));
+  const unsigned g1 = static_cast<unsigned>((M / kBM) * (F / kBN));
+  ffn_gemm_kernel<kEpiGelu><<<dim3(g1), dim3(kThreads), 0, stream>>>(x, rstd, w1, nullptr, h, M,
+                                                                    F, D);
+  CREDIT_TRY(check_launch("ffn_gemm_kernel<gelu>"));
+  const unsigned g2 = static_cast<unsigned>((M / kBM) * (D / kBN));
+  ffn_gemm_kernel<kEpiResidual><<<dim3(g2), dim3(kThreads), 0, stream>>>(h, nullptr, w2, x, out,
+                                                                        M, D, F);
+  return check_launch("ffn_gemm_kernel<residual>");
+}

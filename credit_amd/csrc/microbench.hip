@@ -171,20 +171,24 @@ __global__ void mb_pingpong_kernel(uint32_t* flag, int peer, int rounds, uint64_
 }
 
 // ------------------------------------------ arrival barrier cost (H3/H4) --
-// A cooperative grid of `groups` x `members` workgroups; each group meets at
-// `barriers` group barriers in a row (arrive, then wait at once: the
-// un-overlapped cost).  xcd_local keeps a group's members on one XCD.
-__global__ __launch_bounds__(256) void mb_barrier_kernel(uint32_t* counters, int members,
-                                                         int barriers, uint32_t* watchdog,
-                                                         int groups) {
-  int group, member;
-  split_coords(members, groups, &group, &member);
-  GroupSync s = group_sync_init(counters, group, members);
+// `groups` ticketed groups of `members` workgroups; each group meets at
+// `barriers` split barriers in a row (publish, arrive, wait, read the
+// partials): the un-overlapped cost of the exchange the split kernels use.
+__global__ __launch_bounds__(256) void mb_barrier_kernel(uint32_t* counters, double* slots,
+                                                         int members, int barriers,
+                                                         uint32_t* watchdog, uint32_t total,
+                                                         int groups, double* sink) {
+  SplitGroup g = split_join(counters, slots, members, 1, total);
+  if (g.group >= groups) return;  // padding group
+  double acc = 0.0;
   for (int k = 0; k < barriers; ++k) {
-    group_arrive(s, k);
-    group_wait(s, k, watchdog);
+    if (threadIdx.x == 0) split_publish(g, 0, static_cast<double>(g.member + k));
+    split_arrive_wait(g, watchdog);
+    acc += split_sum(g, 0);
+    split_next(g);
   }
-  group_finish(s, member);
+  split_leave(g);
+  if (acc == -1.0 && threadIdx.x == 0) sink[0] = acc;  // keeps the reads alive
 }
 
 __global__ __launch_bounds__(256) void mb_plain_kernel(int* sink) {
@@ -388,40 +392,51 @@ int bench_pingpong(int rounds, double* results, int n) {
 }  // namespace
 
 int control_overhead(int64_t rows, int split, int barriers, int warmup, int iters,
-                     double* plain_ms, double* split_ms, int xcd_local) {
+                     double* plain_ms, double* split_ms, int cooperative) {
   const DeviceProps* props = nullptr;
   CREDIT_TRY(current_device_props(&props));
   if (split < 1 || split > 64) return set_error(CREDIT_ERR_BAD_CONFIG, "split %d", split);
-  int per_cu = 0;
-  CREDIT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mb_barrier_kernel, 256, 0));
-  const int64_t cap = static_cast<int64_t>(per_cu) * props->cu_count;
   int64_t groups = rows;
-  if (groups * split > cap) groups = cap / split;
-  if (groups > kMaxGroups) groups = kMaxGroups;
-  if (xcd_local) groups = groups / 8 * 8;
-  else if (groups % 8 == 0) groups -= 1;  // a group count that is not a multiple
-                                          // of 8 selects the XCD-spread mapping
+  if (groups > kMaxGroupsPerLaunch) groups = kMaxGroupsPerLaunch;
+  if (cooperative) {
+    // A cooperative launch must fit the device at once.
+    int per_cu = 0;
+    CREDIT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mb_barrier_kernel, 256, 0));
+    const int64_t cap = static_cast<int64_t>(per_cu) * props->cu_count;
+    if (groups * split > cap) groups = cap / split;
+  }
+  if (cooperative) groups = groups / kDispensers * kDispensers;
   if (groups < 1) return set_error(CREDIT_ERR_UNSUPPORTED, "split %d does not fit", split);
+  const int64_t grid_groups = padded_groups(groups);
   DevBuf ws, sink;
-  CREDIT_TRY(ws.alloc(kScratchOffset));
+  CREDIT_TRY(ws.alloc(kScratchOffset + split_slot_bytes(grid_groups, split, 1)));
   CREDIT_TRY(sink.alloc(256));
-  uint32_t* counters = ws_counters(static_cast<char*>(ws.p));
-  uint32_t* watchdog = ws_watchdog(static_cast<char*>(ws.p));
-  const unsigned grid = static_cast<unsigned>(groups * split);
+  char* base = static_cast<char*>(ws.p);
+  uint32_t* counters = ws_counters(base);
+  uint32_t* watchdog = ws_watchdog(base);
+  double* slots = reinterpret_cast<double*>(ws_scratch(base));
+  double* sinkp = static_cast<double*>(sink.p);
+  const unsigned grid = static_cast<unsigned>(grid_groups * split);
+  uint32_t total = grid;
+  int valid = static_cast<int>(groups);
   auto plain = [&](int) -> int {
     mb_plain_kernel<<<grid, 256>>>(static_cast<int*>(sink.p));
     return check_launch("mb_plain_kernel");
   };
   int members = split;
-  int ngroups = static_cast<int>(groups);
-  auto coop = [&](int) -> int {
-    void* args[] = {&counters, &members, &barriers, &watchdog, &ngroups};
-    CREDIT_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mb_barrier_kernel),
-                                          dim3(grid), dim3(256), args, 0, nullptr));
-    return CREDIT_OK;
+  auto timed = [&](int) -> int {
+    if (cooperative) {
+      void* args[] = {&counters, &slots, &members, &barriers, &watchdog, &total, &valid, &sinkp};
+      CREDIT_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mb_barrier_kernel),
+                                            dim3(grid), dim3(256), args, 0, nullptr));
+      return CREDIT_OK;
+    }
+    mb_barrier_kernel<<<grid, 256>>>(counters, slots, members, barriers, watchdog, total, valid,
+                                     sinkp);
+    return check_launch("mb_barrier_kernel");
   };
   CREDIT_TRY(time_ms(plain, warmup, iters, plain_ms));
-  CREDIT_TRY(time_ms(coop, warmup, iters, split_ms));
+  CREDIT_TRY(time_ms(timed, warmup, iters, split_ms));
   uint32_t flag = 0;
   CREDIT_HIP(hipMemcpy(&flag, watchdog, sizeof(flag), hipMemcpyDeviceToHost));
   if (flag != 0) return set_error(CREDIT_ERR_WATCHDOG, "barrier benchmark timed out");
@@ -459,11 +474,11 @@ extern "C" int credit_microbench(int32_t which, int64_t bytes, int32_t iters, do
 }
 
 extern "C" int credit_control_overhead(int64_t rows, int32_t split, int32_t barriers,
-                                       int32_t warmup, int32_t iters, int32_t xcd_local,
+                                       int32_t warmup, int32_t iters, int32_t cooperative,
                                        double* plain_ms, double* split_ms) {
   CREDIT_TRY(check_ptr(plain_ms, "plain_ms"));
   CREDIT_TRY(check_ptr(split_ms, "split_ms"));
   if (rows < 1 || barriers < 0 || warmup < 0 || iters < 1)
     return set_error(CREDIT_ERR_BAD_CONFIG, "rows >= 1, barriers >= 0, iters >= 1 required");
-  return control_overhead(rows, split, barriers, warmup, iters, plain_ms, split_ms, xcd_local);
+  return control_overhead(rows, split, barriers, warmup, iters, plain_ms, split_ms, cooperative);
 }

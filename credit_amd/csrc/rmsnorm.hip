@@ -1,0 +1,626 @@
+// C3: RMSNorm forward and backward, bf16 in/out with fp32 statistics.
+//
+//   forward : rstd = 1/sqrt(mean(x^2) + eps),  y = x * rstd * w
+//   backward: g = dy * w,  xhat = x * rstd,  c = mean(g * xhat),
+//             dx = rstd * (g - xhat * c),    dw = sum over rows of dy * xhat
+//
+// The reference has no RMSNorm; its nearest pattern is the row sum of
+// squares of src/workloads/lars_momentum.cu:283-319 (block_read, block_smem
+// and cluster_smem variants).  gfx950 variants:
+//  - STAGED: one workgroup per row holds the row in VGPRs (a 1024-lane
+//            workgroup holds 8192 dwordx4 = a 128 KiB bf16 row at 32 VGPRs
+//            per lane): one HBM read of x, one write of y.
+//  - SPLIT : P workgroups per row (ticketed groups, common.hpp) each hold a
+//            1/P slice and exchange their partial sum of squares once.
+//  - READ  : one workgroup per row streams the row twice (sum of squares,
+//            then the output pass); any width, any alignment.
+// Backward: a group of P members covers a block of R rows; member m owns
+// column slice m for all R rows, so it accumulates dw for its slice across
+// the block in fp64 registers (dy*x is exact in fp32 and the product with
+// rstd is exact in fp64, so the column sums carry no per-term rounding) and
+// writes one fp64 partial row per block.  A second kernel sums the blocks'
+// partials in block order, which keeps dw deterministic with no float
+// atomics.  The row reduction c comes from the per-row exchange (SPLIT, P>1),
+// from the whole row held by one member (STAGED, P=1), or from a streaming
+// pre-pass (READ: rmsnorm_bwd_rowdot_kernel, then the slice kernel reading c).
+//
+// Algorithmic traffic (bytes): forward 2MN (x) + 2N (w) + 2MN (y) + 4M
+// (rstd); backward 4MN (x, dy) + 2N + 4M + 2MN (dx) + 4N (dw).
+#include <initializer_list>
+
+#include "api_internal.hpp"
+#include "common.hpp"
+
+namespace credit {
+namespace {
+
+// ------------------------------------------------------- bf16x8 helpers --
+__device__ __forceinline__ float sumsq8(u32x4 v) {
+  const float a = bf16_lo(v.x), b = bf16_hi(v.x), c = bf16_lo(v.y), d = bf16_hi(v.y);
+  const float e = bf16_lo(v.z), f = bf16_hi(v.z), g = bf16_lo(v.w), h = bf16_hi(v.w);
+  return ((a * a + b * b) + (c * c + d * d)) + ((e * e + f * f) + (g * g + h * h));
+}
+
+__device__ __forceinline__ uint32_t scale2(uint32_t xv, uint32_t wv, float rs) {
+  return pack_bf16x2(bf16_lo(xv) * rs * bf16_lo(wv), bf16_hi(xv) * rs * bf16_hi(wv));
+}
+
+__device__ __forceinline__ u32x4 scale8(u32x4 x, u32x4 w, float rs) {
+  return u32x4{scale2(x.x, w.x, rs), scale2(x.y, w.y, rs), scale2(x.z, w.z, rs),
+               scale2(x.w, w.w, rs)};
+}
+
+// sum over the 8 lanes of a vector of (dy*w) * x   (the row dot without rstd)
+__device__ __forceinline__ float gx8(u32x4 x, u32x4 dy, u32x4 w) {
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s += bf16_lo(dy[i]) * bf16_lo(w[i]) * bf16_lo(x[i]);
+    s += bf16_hi(dy[i]) * bf16_hi(w[i]) * bf16_hi(x[i]);
+  }
+  return s;
+}
+
+// dx for one vector: rs * (dy*w - x*rs*c)
+__device__ __forceinline__ u32x4 dx8(u32x4 x, u32x4 dy, u32x4 w, float rs, float c) {
+  u32x4 out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = rs * (bf16_lo(dy[i]) * bf16_lo(w[i]) - bf16_lo(x[i]) * rs * c);
+    const float hi = rs * (bf16_hi(dy[i]) * bf16_hi(w[i]) - bf16_hi(x[i]) * rs * c);
+    out[i] = pack_bf16x2(lo, hi);
+  }
+  return out;
+}
+
+// ------------------------------------------------------------- forward ---
+// One workgroup = one member of a row's group (members == 1: the whole row).
+// The member's slice is vectors [v0, v0 + vlen) of the row, held in VPT
+// dwordx4 registers per lane.
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    uint16_t* __restrict__ y, float* __restrict__ rstd_out, int cols, int chunk,
+    int members, int rows, float eps, uint32_t* __restrict__ counters,
+    double* __restrict__ slots, uint32_t total_workgroups, uint32_t* __restrict__ watchdog) {
+  constexpr int NW = THREADS / kWave;
+  __shared__ double red[NW];
+  const int tid = threadIdx.x;
+  SplitGroup g;
+  int row = blockIdx.x, member = 0;
+  if (members > 1) {
+    g = split_join(counters, slots, members, 1, total_workgroups);
+    row = g.group;
+    member = g.member;
+    if (row >= rows) return;  // padding group
+  }
+  const int nvec = cols >> 3;
+  const int v0 = member * chunk;
+  const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  const u32x4* xr = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(row) * cols) + v0;
+  u32x4 v[VPT];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int idx = tid + k * THREADS;
+    v[k] = idx < vlen ? load_nt(xr + idx) : u32x4{0, 0, 0, 0};
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) ss += sumsq8(v[k]);
+  double total = block_reduce_sum_f64<NW>(static_cast<double>(ss), red);
+  if (members > 1) {
+    if (tid == 0) split_publish(g, 0, total);
+    split_arrive_wait(g, watchdog);
+    total = split_sum(g, 0);
+    split_next(g);
+    split_leave(g);
+  }
+  const float rs = static_cast<float>(1.0 / __builtin_sqrt(total / cols + eps));
+  const u32x4* wr = reinterpret_cast<const u32x4*>(w) + v0;
+  u32x4* yr = reinterpret_cast<u32x4*>(y + static_cast<size_t>(row) * cols) + v0;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int idx = tid + k * THREADS;
+    if (idx < vlen) store_nt(yr + idx, scale8(v[k], wr[idx], rs));
+  }
+  if (member == 0 && tid == 0) rstd_out[row] = rs;
+}
+
+// Streaming forward: pass 1 sum of squares, pass 2 output.  VEC: rows are
+// 16-byte aligned and cols % 8 == 0, so both passes use dwordx4 with four
+// loads in flight per lane; otherwise element loads.
+template <int THREADS, bool VEC>
+__global__ __launch_bounds__(THREADS) void rmsnorm_fwd_read_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    uint16_t* __restrict__ y, float* __restrict__ rstd_out, int cols, float eps) {
+  constexpr int NW = THREADS / kWave;
+  __shared__ double red[NW];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint16_t* xr = x + static_cast<size_t>(row) * cols;
+  uint16_t* yr = y + static_cast<size_t>(row) * cols;
+  double ss = 0.0;
+  if (VEC) {
+    const int nvec = cols >> 3;
+    const u32x4* xv = reinterpret_cast<const u32x4*>(xr);
+    int i = tid;
+    for (; i + 3 * THREADS < nvec; i += 4 * THREADS) {
+      const u32x4 a = xv[i], b = xv[i + THREADS], c = xv[i + 2 * THREADS],
+                  d = xv[i + 3 * THREADS];
+      ss += static_cast<double>((sumsq8(a) + sumsq8(b)) + (sumsq8(c) + sumsq8(d)));
+    }
+    for (; i < nvec; i += THREADS) ss += static_cast<double>(sumsq8(xv[i]));
+  } else {
+    for (int c = tid; c < cols; c += THREADS) {
+      const float v = bf16_to_f32(xr[c]);
+      ss += static_cast<double>(v * v);
+    }
+  }
+  const double total = block_reduce_sum_f64<NW>(ss, red);
+  const float rs = static_cast<float>(1.0 / __builtin_sqrt(total / cols + eps));
+  if (VEC) {
+    const int nvec = cols >> 3;
+    const u32x4* xv = reinterpret_cast<const u32x4*>(xr);
+    const u32x4* wv = reinterpret_cast<const u32x4*>(w);
+    u32x4* yv = reinterpret_cast<u32x4*>(yr);
+    int i = tid;
+    for (; i + 3 * THREADS < nvec; i += 4 * THREADS) {
+      const u32x4 a = load_nt(xv + i), b = load_nt(xv + i + THREADS),
+                  c = load_nt(xv + i + 2 * THREADS), d = load_nt(xv + i + 3 * THREADS);
+      store_nt(yv + i, scale8(a, wv[i], rs));
+      store_nt(yv + i + THREADS, scale8(b, wv[i + THREADS], rs));
+      store_nt(yv + i + 2 * THREADS, scale8(c, wv[i + 2 * THREADS], rs));
+      store_nt(yv + i + 3 * THREADS, scale8(d, wv[i + 3 * THREADS], rs));
+    }
+    for (; i < nvec; i += THREADS) store_nt(yv + i, scale8(load_nt(xv + i), wv[i], rs));
+  } else {
+    for (int c = tid; c < cols; c += THREADS)
+      yr[c] = f32_to_bf16(bf16_to_f32(xr[c]) * rs * bf16_to_f32(w[c]));
+  }
+  if (tid == 0) rstd_out[row] = rs;
+}
+
+// ------------------------------------------------------------ backward ---
+// mode of the backward slice kernel: where the row reduction c comes from.
+constexpr int kBwdExchange = 0;  // ticketed group of `members`, one exchange per row
+constexpr int kBwdWhole = 1;     // members == 1: the member holds the whole row
+constexpr int kBwdGiven = 2;     // c precomputed in rowdot[] (READ variant)
+
+// Member `member` of group `group` covers rows [group*R, group*R + R) and
+// vectors [member*chunk, ...) of each.  Registers per lane: VPT dwordx4 of x
+// and of dy, 8*VPT fp64 dw accumulators.
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ dy, const float* __restrict__ rstd,
+    const float* __restrict__ rowdot, uint16_t* __restrict__ dx,
+    double* __restrict__ dw_part, int rows, int cols, int chunk, int members,
+    int rows_per_group, int mode, uint32_t* __restrict__ counters,
+    double* __restrict__ slots, uint32_t total_workgroups, uint32_t* __restrict__ watchdog) {
+  constexpr int NW = THREADS / kWave;
+  __shared__ double red[2][NW];
+  const int tid = threadIdx.x;
+  SplitGroup g;
+  int group, member;
+  if (mode == kBwdExchange) {
+    g = split_join(counters, slots, members, 1, total_workgroups);
+    group = g.group;
+    member = g.member;
+    if (group * rows_per_group >= rows) return;  // padding group
+  } else {
+    group = blockIdx.x / members;
+    member = blockIdx.x - group * members;
+  }
+  const int nvec = cols >> 3;
+  const int v0 = member * chunk;
+  const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  const int r0 = group * rows_per_group;
+  const int r1 = r0 + rows_per_group < rows ? r0 + rows_per_group : rows;
+  const u32x4* wr = reinterpret_cast<const u32x4*>(w) + v0;
+  double acc[VPT][8];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[k][e] = 0.0;
+
+  for (int r = r0; r < r1; ++r) {
+    const size_t off = static_cast<size_t>(r) * cols;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(x + off) + v0;
+    const u32x4* dyr = reinterpret_cast<const u32x4*>(dy + off) + v0;
+    u32x4 xv[VPT], dv[VPT];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const int idx = tid + k * THREADS;
+      const bool in = idx < vlen;
+      xv[k] = in ? load_nt(xr + idx) : u32x4{0, 0, 0, 0};
+      dv[k] = in ? load_nt(dyr + idx) : u32x4{0, 0, 0, 0};
+    }
+    const float rs = rstd[r];
+    double dot;
+    if (mode == kBwdGiven) {
+      dot = static_cast<double>(rowdot[r]);
+    } else {
+      float part = 0.0f;
+#pragma unroll
+      for (int k = 0; k < VPT; ++k) {
+        const int idx = tid + k * THREADS;
+        if (idx < vlen) part += gx8(xv[k], dv[k], wr[idx]);
+      }
+      dot = block_reduce_sum_f64<NW>(static_cast<double>(part), red[r & 1]);
+      if (mode == kBwdExchange) {
+        if (tid == 0) split_publish(g, 0, dot);
+        split_arrive_wait(g, watchdog);
+        dot = split_sum(g, 0);
+        split_next(g);
+      }
+    }
+    // c = mean(g * xhat) = rs * sum(dy*w*x) / cols
+    const float c = static_cast<float>(dot * rs / cols);
+    u32x4* dxr = reinterpret_cast<u32x4*>(dx + off) + v0;
+    const double rsd = static_cast<double>(rs);
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const int idx = tid + k * THREADS;
+      if (idx < vlen) store_nt(dxr + idx, dx8(xv[k], dv[k], wr[idx], rs, c));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // dy*x is exact in fp32 (bf16 x bf16); times rstd it is exact in fp64.
+        acc[k][2 * i] += static_cast<double>(bf16_lo(dv[k][i]) * bf16_lo(xv[k][i])) * rsd;
+        acc[k][2 * i + 1] += static_cast<double>(bf16_hi(dv[k][i]) * bf16_hi(xv[k][i])) * rsd;
+      }
+    }
+  }
+  if (mode == kBwdExchange) split_leave(g);
+  // One fp64 partial row per block: rounding the block sums to fp32 here
+  // would add ~ulp(block sum) per block to dw.
+  double* pr = dw_part + static_cast<size_t>(group) * cols + 8 * static_cast<size_t>(v0);
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int idx = tid + k * THREADS;
+    if (idx < vlen) {
+      f64x2* q = reinterpret_cast<f64x2*>(pr + 8 * static_cast<size_t>(idx));
+      q[0] = f64x2{acc[k][0], acc[k][1]};
+      q[1] = f64x2{acc[k][2], acc[k][3]};
+      q[2] = f64x2{acc[k][4], acc[k][5]};
+      q[3] = f64x2{acc[k][6], acc[k][7]};
+    }
+  }
+}
+
+// READ variant pre-pass: rowdot[r] = sum_j dy*w*x over the row, streamed.
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void rmsnorm_bwd_rowdot_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ dy, float* __restrict__ rowdot, int cols) {
+  constexpr int NW = THREADS / kWave;
+  __shared__ double red[NW];
+  const int row = blockIdx.x;
+  const int nvec = cols >> 3;
+  const size_t off = static_cast<size_t>(row) * cols;
+  const u32x4* xv = reinterpret_cast<const u32x4*>(x + off);
+  const u32x4* dv = reinterpret_cast<const u32x4*>(dy + off);
+  const u32x4* wv = reinterpret_cast<const u32x4*>(w);
+  double s = 0.0;
+  int i = threadIdx.x;
+  for (; i + THREADS < nvec; i += 2 * THREADS) {
+    const u32x4 a = load_nt(xv + i), b = load_nt(xv + i + THREADS);
+    const u32x4 da = load_nt(dv + i), db = load_nt(dv + i + THREADS);
+    s += static_cast<double>(gx8(a, da, wv[i]) + gx8(b, db, wv[i + THREADS]));
+  }
+  for (; i < nvec; i += THREADS) s += static_cast<double>(gx8(load_nt(xv + i), load_nt(dv + i), wv[i]));
+  const double t = block_reduce_sum_f64<NW>(s, red);
+  if (threadIdx.x == 0) rowdot[row] = static_cast<float>(t);
+}
+
+// dw[c] = sum over blocks b (in order) of part[b][c], rounded once to fp32.
+__global__ __launch_bounds__(256) void rmsnorm_dw_reduce_kernel(
+    const double* __restrict__ part, float* __restrict__ dw, int blocks, int cols) {
+  const int q = blockIdx.x * 256 + threadIdx.x;  // two columns
+  const int nq = cols >> 1;
+  if (q >= nq) return;
+  const f64x2* p = reinterpret_cast<const f64x2*>(part) + q;
+  double a0 = 0.0, a1 = 0.0;
+  for (int b = 0; b < blocks; ++b) {
+    const f64x2 v = p[static_cast<size_t>(b) * nq];
+    a0 += v.x;
+    a1 += v.y;
+  }
+  reinterpret_cast<float2_t*>(dw)[q] = float2_t{static_cast<float>(a0), static_cast<float>(a1)};
+}
+
+// ------------------------------------------------------------ dispatch ---
+using FwdSliceFn = void (*)(const uint16_t*, const uint16_t*, uint16_t*, float*, int, int,
+                            int, int, float, uint32_t*, double*, uint32_t, uint32_t*);
+using BwdSliceFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, const float*,
+                            const float*, uint16_t*, double*, int, int, int, int, int, int,
+                            uint32_t*, double*, uint32_t, uint32_t*);
+
+struct FwdPick {
+  FwdSliceFn fn;
+  int threads;
+  int capacity;  // dwordx4 per workgroup
+};
+struct BwdPick {
+  BwdSliceFn fn;
+  int threads;
+  int capacity;
+};
+
+// Smallest footprint first.  VPT stays at 4-8 dwordx4 per lane: deeper
+// register staging makes the compiler hoist the weight loads of the output
+// loop and spill.
+const FwdPick kFwd[] = {
+    {rmsnorm_fwd_slice_kernel<64, 4>, 64, 256},
+    {rmsnorm_fwd_slice_kernel<128, 4>, 128, 512},
+    {rmsnorm_fwd_slice_kernel<256, 4>, 256, 1024},
+    {rmsnorm_fwd_slice_kernel<256, 8>, 256, 2048},
+    {rmsnorm_fwd_slice_kernel<512, 8>, 512, 4096},
+    {rmsnorm_fwd_slice_kernel<1024, 8>, 1024, 8192},
+};
+// fp64 dw accumulators cost 16 VGPRs per dwordx4 held, so the backward
+// holds at most 4 per lane (VPT 4) in workgroups of up to 512 lanes.
+const BwdPick kBwd[] = {
+    {rmsnorm_bwd_slice_kernel<64, 4>, 64, 256},
+    {rmsnorm_bwd_slice_kernel<128, 4>, 128, 512},
+    {rmsnorm_bwd_slice_kernel<256, 4>, 256, 1024},
+    {rmsnorm_bwd_slice_kernel<512, 4>, 512, 2048},
+};
+constexpr int kFwdMaxCapacity = 8192;
+constexpr int kBwdMaxCapacity = 2048;
+
+template <class Pick, int N>
+const Pick* pick_for(const Pick (&table)[N], int64_t chunk) {
+  for (const Pick& p : table)
+    if (chunk <= p.capacity) return &p;
+  return nullptr;
+}
+
+bool vec_ok(int64_t cols, std::initializer_list<const void*> ptrs) {
+  if (cols % 8 != 0) return false;
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+  return true;
+}
+
+// Split plan: members P and vectors per member.  Members are trimmed so
+// that none is empty.
+struct Plan {
+  int variant;
+  int members;
+  int64_t chunk;
+};
+
+Plan plan_split(int64_t nvec, int members) {
+  Plan p{CREDIT_VARIANT_SPLIT, members, (nvec + members - 1) / members};
+  p.members = static_cast<int>((nvec + p.chunk - 1) / p.chunk);
+  return p;
+}
+
+int resolve_fwd(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
+  const int variant = cfg_variant(cfg);
+  const int64_t nvec = cols / 8;
+  if (variant == CREDIT_VARIANT_READ || (!vec && variant == CREDIT_VARIANT_AUTO)) {
+    *plan = Plan{CREDIT_VARIANT_READ, 1, nvec};
+    return CREDIT_OK;
+  }
+  if (!vec)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "rmsnorm_fwd staged/split variants need cols %% 8 == 0 and 16-byte "
+                     "aligned buffers");
+  if (variant == CREDIT_VARIANT_STAGED || variant == CREDIT_VARIANT_AUTO) {
+    if (nvec <= kFwdMaxCapacity) {
+      *plan = Plan{CREDIT_VARIANT_STAGED, 1, nvec};
+      return CREDIT_OK;
+    }
+    if (variant == CREDIT_VARIANT_STAGED)
+      return set_error(CREDIT_ERR_UNSUPPORTED,
+                       "rmsnorm_fwd staged variant holds at most %d columns", kFwdMaxCapacity * 8);
+    // AUTO on a row wider than one workgroup: split just enough.
+    *plan = plan_split(nvec, static_cast<int>((nvec + kFwdMaxCapacity - 1) / kFwdMaxCapacity));
+    return CREDIT_OK;
+  }
+  int p = cfg_split(cfg);
+  if (p == 0) p = static_cast<int>((nvec + kFwdMaxCapacity - 1) / kFwdMaxCapacity);
+  if (p < 2) p = 2;
+  if (p > nvec) p = static_cast<int>(nvec);
+  *plan = plan_split(nvec, p);
+  if (plan->chunk > kFwdMaxCapacity)
+    return set_error(CREDIT_ERR_UNSUPPORTED, "rmsnorm_fwd split %d leaves %lld vectors per member",
+                     p, static_cast<long long>(plan->chunk));
+  if (plan->members < 2) *plan = Plan{CREDIT_VARIANT_STAGED, 1, nvec};
+  return CREDIT_OK;
+}
+
+// Backward plan: members P, vectors per member, rows per group R.
+struct BwdPlan {
+  int variant;
+  int members;
+  int64_t chunk;
+  int rows_per_group;
+  int64_t groups;
+};
+
+int rows_per_group_for(int64_t rows, int members, int cu_count) {
+  // Aim for about two workgroups per CU in total; more rows per group cut
+  // the dw partial traffic (one fp32 row per group).
+  const int64_t target_groups = (2 * static_cast<int64_t>(cu_count) + members - 1) / members;
+  int64_t r = (rows + target_groups - 1) / (target_groups > 0 ? target_groups : 1);
+  if (r < 1) r = 1;
+  if (r > 64) r = 64;
+  return static_cast<int>(r);
+}
+
+int resolve_bwd(const credit_cfg* cfg, int64_t rows, int64_t cols, bool vec, int cu_count,
+                BwdPlan* plan) {
+  if (!vec)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "rmsnorm_bwd needs cols %% 8 == 0 and 16-byte aligned buffers");
+  const int variant = cfg_variant(cfg);
+  const int64_t nvec = cols / 8;
+  int p = 0;
+  int v = variant;
+  if (v == CREDIT_VARIANT_AUTO) v = nvec <= kBwdMaxCapacity ? CREDIT_VARIANT_STAGED
+                                                            : CREDIT_VARIANT_SPLIT;
+  if (v == CREDIT_VARIANT_STAGED) {
+    if (nvec > kBwdMaxCapacity)
+      return set_error(CREDIT_ERR_UNSUPPORTED,
+                       "rmsnorm_bwd staged variant holds at most %d columns", kBwdMaxCapacity * 8);
+    p = 1;
+  } else if (v == CREDIT_VARIANT_SPLIT) {
+    p = cfg_split(cfg);
+    const int need = static_cast<int>((nvec + kBwdMaxCapacity - 1) / kBwdMaxCapacity);
+    if (p == 0) p = need < 2 ? 2 : need;
+    if (p < need)
+      return set_error(CREDIT_ERR_UNSUPPORTED,
+                       "rmsnorm_bwd split %d leaves more than %d vectors per member", p,
+                       kBwdMaxCapacity);
+    if (p > nvec) p = static_cast<int>(nvec);
+  } else {  // READ: column tiles of the largest slice, c from the pre-pass
+    p = static_cast<int>((nvec + kBwdMaxCapacity - 1) / kBwdMaxCapacity);
+  }
+  const Plan sp = plan_split(nvec, p);
+  plan->variant = v;
+  plan->members = sp.members;
+  plan->chunk = sp.chunk;
+  if (v == CREDIT_VARIANT_SPLIT && plan->members < 2) plan->variant = CREDIT_VARIANT_STAGED;
+  plan->rows_per_group = rows_per_group_for(rows, plan->members, cu_count);
+  plan->groups = (rows + plan->rows_per_group - 1) / plan->rows_per_group;
+  return CREDIT_OK;
+}
+
+size_t bwd_extra_bytes(const BwdPlan& p, int64_t rows, int64_t cols) {
+  size_t b = align_up(static_cast<size_t>(p.groups) * cols * sizeof(double), 256);
+  if (p.variant == CREDIT_VARIANT_READ) b += align_up(static_cast<size_t>(rows) * sizeof(float), 256);
+  return b;
+}
+
+}  // namespace
+
+size_t rmsnorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split) {
+  credit_cfg c{nullptr, variant, split, nullptr, 0};
+  Plan p;
+  if (resolve_fwd(&c, cols, cols % 8 == 0, &p) != CREDIT_OK) return 0;
+  if (p.variant != CREDIT_VARIANT_SPLIT) return 0;
+  const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
+  return split_workspace_bytes(padded_groups(groups), p.members, 1, 0);
+}
+
+size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
+                             int cu_count) {
+  credit_cfg c{nullptr, variant, split, nullptr, 0};
+  BwdPlan p;
+  if (resolve_bwd(&c, rows, cols, cols % 8 == 0, cu_count, &p) != CREDIT_OK) return 0;
+  return split_workspace_bytes(padded_groups(p.groups), p.members, 1,
+                               bwd_extra_bytes(p, rows, cols));
+}
+
+}  // namespace credit
+
+using namespace credit;
+
+extern "C" int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y,
+                                       float* rstd, int64_t rows, int64_t cols, float eps,
+                                       const credit_cfg* cfg) {
+  CREDIT_TRY(check_row_ptr(x, "x", rows));
+  CREDIT_TRY(check_ptr(w, "w"));
+  CREDIT_TRY(check_row_ptr(y, "y", rows));
+  CREDIT_TRY(check_row_ptr(rstd, "rstd", rows));
+  CREDIT_TRY(check_shape(rows, cols, int64_t{1} << 30));
+  CREDIT_TRY(check_aligned(x, 2, "x"));
+  CREDIT_TRY(check_cfg(cfg));
+  if (!(eps >= 0.0f)) return set_error(CREDIT_ERR_BAD_CONFIG, "eps must be >= 0");
+  if (rows == 0) return CREDIT_OK;
+  const bool vec = vec_ok(cols, {x, w, y});
+  Plan plan;
+  CREDIT_TRY(resolve_fwd(cfg, cols, vec, &plan));
+  hipStream_t stream = cfg_stream(cfg);
+  const int c = static_cast<int>(cols);
+  if (plan.variant == CREDIT_VARIANT_READ) {
+    if (vec)
+      rmsnorm_fwd_read_kernel<256, true>
+          <<<dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream>>>(x, w, y, rstd, c, eps);
+    else
+      rmsnorm_fwd_read_kernel<256, false>
+          <<<dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream>>>(x, w, y, rstd, c, eps);
+    return check_launch("rmsnorm_fwd_read_kernel");
+  }
+  const FwdPick* pick = pick_for(kFwd, plan.chunk);
+  if (plan.variant == CREDIT_VARIANT_STAGED) {
+    hipLaunchKernelGGL(pick->fn, dim3(static_cast<unsigned>(rows)), dim3(pick->threads), 0,
+                       stream, x, w, y, rstd, c, static_cast<int>(plan.chunk), 1,
+                       static_cast<int>(rows), eps, nullptr, nullptr, 0u, nullptr);
+    return check_launch("rmsnorm_fwd_slice_kernel");
+  }
+  const int64_t launch_groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
+  SplitWorkspace ws;
+  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(launch_groups), plan.members, 1, 0, &ws));
+  for (int64_t r0 = 0; r0 < rows; r0 += launch_groups) {
+    const int64_t n = rows - r0 < launch_groups ? rows - r0 : launch_groups;
+    const uint32_t total = static_cast<uint32_t>(padded_groups(n) * plan.members);
+    hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), 0, stream, x + r0 * cols, w,
+                       y + r0 * cols, rstd + r0, c, static_cast<int>(plan.chunk), plan.members,
+                       static_cast<int>(n), eps, ws.counters, ws.slots, total, ws.watchdog);
+    CREDIT_TRY(check_launch("rmsnorm_fwd_slice_kernel(split)"));
+  }
+  return CREDIT_OK;
+}
+
+extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
+                                       const uint16_t* dy, const float* rstd, uint16_t* dx,
+                                       float* dw, int64_t rows, int64_t cols,
+                                       const credit_cfg* cfg) {
+  CREDIT_TRY(check_row_ptr(x, "x", rows));
+  CREDIT_TRY(check_ptr(w, "w"));
+  CREDIT_TRY(check_row_ptr(dy, "dy", rows));
+  CREDIT_TRY(check_row_ptr(rstd, "rstd", rows));
+  CREDIT_TRY(check_row_ptr(dx, "dx", rows));
+  CREDIT_TRY(check_ptr(dw, "dw"));
+  CREDIT_TRY(check_shape(rows, cols, int64_t{1} << 30));
+  CREDIT_TRY(check_cfg(cfg));
+  if (rows > (int64_t{1} << 24))
+    return set_error(CREDIT_ERR_BAD_SHAPE, "rmsnorm_bwd supports at most 2^24 rows");
+  const bool vec = vec_ok(cols, {x, w, dy, dx, dw});
+  const DeviceProps* props = nullptr;
+  CREDIT_TRY(current_device_props(&props));
+  BwdPlan plan;
+  CREDIT_TRY(resolve_bwd(cfg, rows, cols, vec, props->cu_count, &plan));
+  hipStream_t stream = cfg_stream(cfg);
+  if (rows == 0) {
+    // No rows: dw is a sum over nothing.  A fill kernel, not a memset node,
+    // so the call stays correct under stream capture.
+    fill_f32_kernel<<<dim3(static_cast<unsigned>((cols + 255) / 256)), dim3(256), 0, stream>>>(
+        dw, 0.0f, cols);
+    return check_launch("fill_f32_kernel");
+  }
+  if (padded_groups(plan.groups) > kMaxGroupsPerLaunch)
+    return set_error(CREDIT_ERR_BAD_SHAPE, "rmsnorm_bwd: %lld row groups exceed %d",
+                     static_cast<long long>(plan.groups), kMaxGroupsPerLaunch);
+  SplitWorkspace ws;
+  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(plan.groups), plan.members, 1,
+                                     bwd_extra_bytes(plan, rows, cols), &ws));
+  double* dw_part = reinterpret_cast<double*>(ws.extra);
+  float* rowdot = reinterpret_cast<float*>(
+      ws.extra + align_up(static_cast<size_t>(plan.groups) * cols * sizeof(double), 256));
+  const BwdPick* pick = pick_for(kBwd, plan.chunk);
+  const int c = static_cast<int>(cols);
+  int mode = kBwdWhole;
+  if (plan.variant == CREDIT_VARIANT_SPLIT) mode = kBwdExchange;
+  // Ticketed launches cover whole dispenser subsets (padding groups exit).
+  const int64_t grid_groups = mode == kBwdExchange ? padded_groups(plan.groups) : plan.groups;
+  const uint32_t total = static_cast<uint32_t>(grid_groups * plan.members);
+  if (plan.variant == CREDIT_VARIANT_READ) {
+    mode = kBwdGiven;
+    rmsnorm_bwd_rowdot_kernel<256>
+        <<<dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream>>>(x, w, dy, rowdot, c);
+    CREDIT_TRY(check_launch("rmsnorm_bwd_rowdot_kernel"));
+  }
+  hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), 0, stream, x, w, dy, rstd,
+                     rowdot, dx, dw_part, static_cast<int>(rows), c,
+                     static_cast<int>(plan.chunk), plan.members, plan.rows_per_group, mode,
+                     ws.counters, ws.slots, total, ws.watchdog);
+  CREDIT_TRY(check_launch("rmsnorm_bwd_slice_kernel"));
+  const unsigned reduce_blocks = static_cast<unsigned>((cols / 2 + 255) / 256);
+  rmsnorm_dw_reduce_kernel<<<dim3(reduce_blocks), dim3(256), 0, stream>>>(
+      dw_part, dw, static_cast<int>(plan.groups), c);
+  return check_launch("rmsnorm_dw_reduce_kernel");
+}

@@ -135,11 +135,14 @@ struct SplitLayout {
   size_t part_sum_off, part_max_off, bytes;
 };
 
-// Partials for one launch of at most kCounterSlots rows (the arrival
-// counters live in the workspace's counter area, one per row of a launch).
+// Arrival counters live in the workspace's counter area, one per row of a
+// launch, after the ticket dispenser's slots; a launch covers at most
+// kLaunchRows rows and the partials are sized for one launch.
+constexpr int64_t kLaunchRows = kCounterSlots - kGroupCounterBase;
+
 SplitLayout split_layout(int64_t rows, int split) {
   SplitLayout l;
-  const int64_t launch_rows = rows < kCounterSlots ? rows : kCounterSlots;
+  const int64_t launch_rows = rows < kLaunchRows ? rows : kLaunchRows;
   const size_t slots = static_cast<size_t>(launch_rows) * split;
   l.part_sum_off = 0;
   l.part_max_off = align_up(slots * sizeof(double), 256);
@@ -194,9 +197,9 @@ using namespace credit;
 extern "C" int credit_row_sum_max_f32(const float* x, float* sum, float* max,
                                       int64_t rows, int64_t cols,
                                       const credit_cfg* cfg) {
-  CREDIT_TRY(check_ptr(x, "x"));
-  CREDIT_TRY(check_ptr(sum, "sum"));
-  CREDIT_TRY(check_ptr(max, "max"));
+  CREDIT_TRY(check_row_ptr(x, "x", rows));
+  CREDIT_TRY(check_row_ptr(sum, "sum", rows));
+  CREDIT_TRY(check_row_ptr(max, "max", rows));
   CREDIT_TRY(check_shape(rows, cols, int64_t{1} << 30));
   CREDIT_TRY(check_aligned(x, 4, "x"));
   CREDIT_TRY(check_cfg(cfg));
@@ -223,13 +226,14 @@ extern "C" int credit_row_sum_max_f32(const float* x, float* sum, float* max,
   char* ws = nullptr;
   CREDIT_TRY(acquire_workspace(cfg, l.bytes, &ws));
   char* scratch = ws_scratch(ws);
-  for (int64_t r0 = 0; r0 < rows; r0 += kCounterSlots) {
-    const int64_t n = rows - r0 < kCounterSlots ? rows - r0 : kCounterSlots;
+  for (int64_t r0 = 0; r0 < rows; r0 += kLaunchRows) {
+    const int64_t n = rows - r0 < kLaunchRows ? rows - r0 : kLaunchRows;
     row_sum_max_split_kernel<kRowThreads>
         <<<dim3(static_cast<unsigned>(n * split)), dim3(kRowThreads), 0, stream>>>(
             x + r0 * cols, sum + r0, max + r0, c, split, chunk,
             reinterpret_cast<double*>(scratch + l.part_sum_off),
-            reinterpret_cast<float*>(scratch + l.part_max_off), ws_counters(ws));
+            reinterpret_cast<float*>(scratch + l.part_max_off),
+            ws_counters(ws) + kGroupCounterBase);
     CREDIT_TRY(check_launch("row_sum_max_split_kernel"));
   }
   return CREDIT_OK;

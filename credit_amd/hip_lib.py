@@ -109,6 +109,13 @@ SIGNATURES: dict[str, list] = {
     "credit_check_watchdog": [_CFG],
     "credit_row_sum_max_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_layernorm_fwd_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _CFG],
+    "credit_rmsnorm_fwd_bf16": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
+    "credit_rmsnorm_bwd_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _CFG],
+    "credit_softmax_fwd_f32": [_P, _P, _P, _P, _I64, _I64, _CFG],
+    "credit_softmax_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
+    "credit_softmax_logits_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
+    "credit_ffn_rmsnorm_gelu_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
+    "credit_transpose_bf16": [_P, _P, _I64, _I64, _CFG],
     "credit_microbench": [ctypes.c_int32, _I64, ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
                           ctypes.c_int32],
     "credit_control_overhead": [_I64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
@@ -237,13 +244,15 @@ def microbench(name: str, nbytes: int = 0, iters: int = 0, n_results: int = 16) 
 
 
 def control_overhead(rows: int, split: int, barriers: int, warmup: int = 3, iters: int = 20,
-                     xcd_local: bool = True) -> tuple[float, float]:
-    """(plain_ms, split_ms): cooperative grid with `barriers` arrival barriers
-    per group against a plain launch (replaces build/cluster_control)."""
+                     cooperative: bool = False) -> tuple[float, float]:
+    """(plain_ms, split_ms): a grid of `rows` ticketed groups of `split`
+    workgroups meeting at `barriers` split barriers, against a plain launch
+    of the same grid (replaces build/cluster_control)."""
     plain = ctypes.c_double()
     split_ms = ctypes.c_double()
-    check(load_library().credit_control_overhead(rows, split, barriers, warmup, iters, int(xcd_local),
-                                                 ctypes.byref(plain), ctypes.byref(split_ms)),
+    check(load_library().credit_control_overhead(rows, split, barriers, warmup, iters,
+                                                 int(cooperative), ctypes.byref(plain),
+                                                 ctypes.byref(split_ms)),
           "credit_control_overhead")
     return plain.value, split_ms.value
 
@@ -294,6 +303,102 @@ def layernorm_fwd(
     )
 
 
+def rmsnorm_fwd(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, rstd: torch.Tensor,
+                eps: float, cfg: CreditCfg) -> None:
+    rows, cols = _rows_cols(x)
+    check(
+        load_library().credit_rmsnorm_fwd_bf16(
+            _ptr(x, "x", torch.bfloat16), _ptr(w, "w", torch.bfloat16),
+            _ptr(y, "y", torch.bfloat16), _ptr(rstd, "rstd", torch.float32),
+            rows, cols, float(eps), ctypes.byref(cfg)),
+        "credit_rmsnorm_fwd_bf16",
+    )
+
+
+def rmsnorm_bwd(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, rstd: torch.Tensor,
+                dx: torch.Tensor, dw: torch.Tensor, cfg: CreditCfg) -> None:
+    rows, cols = _rows_cols(x)
+    check(
+        load_library().credit_rmsnorm_bwd_bf16(
+            _ptr(x, "x", torch.bfloat16), _ptr(w, "w", torch.bfloat16),
+            _ptr(dy, "dy", torch.bfloat16), _ptr(rstd, "rstd", torch.float32),
+            _ptr(dx, "dx", torch.bfloat16), _ptr(dw, "dw", torch.float32),
+            rows, cols, ctypes.byref(cfg)),
+        "credit_rmsnorm_bwd_bf16",
+    )
+
+
+def softmax_fwd(x: torch.Tensor, p: torch.Tensor, rowmax: torch.Tensor, lse: torch.Tensor,
+                cfg: CreditCfg) -> None:
+    rows, cols = _rows_cols(x)
+    check(
+        load_library().credit_softmax_fwd_f32(
+            _ptr(x, "x", torch.float32), _ptr(p, "p", torch.float32),
+            _ptr(rowmax, "rowmax", torch.float32), _ptr(lse, "lse", torch.float32),
+            rows, cols, ctypes.byref(cfg)),
+        "credit_softmax_fwd_f32",
+    )
+
+
+def softmax_bwd(p: torch.Tensor, dy: torch.Tensor, dx: torch.Tensor, cfg: CreditCfg) -> None:
+    rows, cols = _rows_cols(p)
+    check(
+        load_library().credit_softmax_bwd_f32(
+            _ptr(p, "p", torch.float32), _ptr(dy, "dy", torch.float32),
+            _ptr(dx, "dx", torch.float32), rows, cols, ctypes.byref(cfg)),
+        "credit_softmax_bwd_f32",
+    )
+
+
+def softmax_logits_backward(logits: torch.Tensor, dy: torch.Tensor, dx: torch.Tensor,
+                            cfg: CreditCfg) -> None:
+    rows, cols = _rows_cols(logits)
+    check(
+        load_library().credit_softmax_logits_bwd_f32(
+            _ptr(logits, "logits", torch.float32), _ptr(dy, "dy", torch.float32),
+            _ptr(dx, "dx", torch.float32), rows, cols, ctypes.byref(cfg)),
+        "credit_softmax_logits_bwd_f32",
+    )
+
+
+def ffn(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, out: torch.Tensor, eps: float,
+        cfg: CreditCfg) -> None:
+    """out = x + GELU_tanh(RMSNorm(x) @ w1.T) @ w2.T; w1 [f, d], w2 [d, f]."""
+    rows, d = _rows_cols(x)
+    f = int(w1.shape[0])
+    if tuple(w1.shape) != (f, d) or tuple(w2.shape) != (d, f):
+        raise ValueError(f"ffn: w1 must be [f, d] and w2 [d, f]; got {tuple(w1.shape)}, "
+                         f"{tuple(w2.shape)} for d={d}")
+    check(
+        load_library().credit_ffn_rmsnorm_gelu_bf16(
+            _ptr(x, "x", torch.bfloat16), _ptr(w1, "w1", torch.bfloat16),
+            _ptr(w2, "w2", torch.bfloat16), _ptr(out, "out", torch.bfloat16),
+            rows, d, f, float(eps), ctypes.byref(cfg)),
+        "credit_ffn_rmsnorm_gelu_bf16",
+    )
+
+
+def transpose(src: torch.Tensor, dst: torch.Tensor, cfg: CreditCfg | None = None) -> None:
+    rows, cols = _rows_cols(src)
+    if tuple(dst.shape) != (cols, rows):
+        raise ValueError("transpose: dst must be [cols, rows]")
+    cfg = cfg if cfg is not None else make_cfg()
+    check(
+        load_library().credit_transpose_bf16(
+            _ptr(src, "src", torch.bfloat16), _ptr(dst, "dst", torch.bfloat16),
+            rows, cols, ctypes.byref(cfg)),
+        "credit_transpose_bf16",
+    )
+
+
+def linear_layout(w: torch.Tensor) -> torch.Tensor:
+    """A [in, out] weight (the BASELINE's W1 [d, f]) in the nn.Linear layout
+    [out, in] the FFN takes, transposed on the GPU by this library."""
+    out = torch.empty((w.shape[1], w.shape[0]), dtype=w.dtype, device=w.device)
+    transpose(w, out)
+    return out
+
+
 # ------------------------------------------------- reference-shaped table --
 
 
@@ -318,9 +423,60 @@ def launch_layernorm_fwd(inputs, outputs, config: LaunchConfig = LaunchConfig())
     layernorm_fwd(x, gamma, beta, y, mean, rstd, 1.0e-5, make_cfg(config.variant, config.split))
 
 
+RMSNORM_EPS = 1.0e-6
+
+
+def launch_rmsnorm_fwd(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    x, w = inputs[0], inputs[1]
+    y, rstd = outputs
+    rmsnorm_fwd(x, w, y, rstd, RMSNORM_EPS, make_cfg(config.variant, config.split))
+
+
+def launch_rmsnorm_bwd(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    """inputs: (x, w, dy, rstd) -- rstd from the forward."""
+    x, w, dy, rstd = inputs
+    dx, dw = outputs
+    rmsnorm_bwd(x, w, dy, rstd, dx, dw, make_cfg(config.variant, config.split))
+
+
+def launch_softmax_fwd(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    x = inputs[0]
+    p, rowmax, lse = outputs
+    softmax_fwd(x, p, rowmax, lse, make_cfg(config.variant, config.split))
+
+
+def launch_softmax_bwd(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    """inputs: (p, dy) -- p from the forward."""
+    p, dy = inputs[0], inputs[1]
+    (dx,) = outputs
+    softmax_bwd(p, dy, dx, make_cfg(config.variant, config.split))
+
+
+def launch_softmax_logits_backward(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    logits, dy = inputs
+    (dx,) = outputs
+    softmax_logits_backward(logits, dy, dx, make_cfg(config.variant, config.split))
+
+
+FFN_EPS = 1.0e-6
+
+
+def launch_ffn(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    """inputs: (x, w1 [f, d], w2 [d, f]) in the nn.Linear layout."""
+    x, w1, w2 = inputs
+    (out,) = outputs
+    ffn(x, w1, w2, out, FFN_EPS, make_cfg(config.variant, config.split))
+
+
 HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
+    "ffn": launch_ffn,
     "row_sum_max": launch_row_sum_max,
     "layernorm_fwd": launch_layernorm_fwd,
+    "rmsnorm_fwd": launch_rmsnorm_fwd,
+    "rmsnorm_bwd": launch_rmsnorm_bwd,
+    "softmax_fwd": launch_softmax_fwd,
+    "softmax_bwd": launch_softmax_bwd,
+    "softmax_logits_backward": launch_softmax_logits_backward,
 }
 
 
@@ -333,4 +489,12 @@ def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch
         return torch.empty(rows, **f32), torch.empty(rows, **f32)
     if name == "layernorm_fwd":
         return torch.empty_like(x), torch.empty(rows, **f32), torch.empty(rows, **f32)
+    if name == "rmsnorm_fwd":
+        return torch.empty_like(x), torch.empty(rows, **f32)
+    if name == "rmsnorm_bwd":
+        return torch.empty_like(x), torch.empty(x.shape[1], **f32)
+    if name == "softmax_fwd":
+        return torch.empty_like(x), torch.empty(rows, **f32), torch.empty(rows, **f32)
+    if name in ("softmax_bwd", "softmax_logits_backward", "ffn"):
+        return (torch.empty_like(x),)
     raise KeyError(name)

@@ -91,15 +91,18 @@ def run_microbenchmarks(hbm_bytes: int = 1 << 30, iters: int = 20) -> dict[str, 
 
 def run_control_sweep(rows: int = 1024, splits=(2, 4, 8, 16), barriers=(1, 2, 3),
                       warmup: int = 3, iters: int = 20) -> list[dict[str, Any]]:
-    """credit_control_overhead over (P, barriers) for both group placements.
-    Replaces the per-shape build/cluster_control runs of
+    """credit_control_overhead over (P, barriers) with the plain ticketed
+    launch the split kernels use, plus the cooperative launch at one barrier
+    for comparison.  Replaces the per-shape build/cluster_control runs of
     dsmem_eval/runner.py:313-347."""
     out = []
     for p in splits:
         for b in barriers:
-            for xcd_local in (True, False):
-                plain, split = hip_lib.control_overhead(rows, p, b, warmup, iters, xcd_local)
-                out.append({"rows": rows, "split": p, "barriers": b, "xcd_local": xcd_local,
+            for coop in (False, True):
+                if coop and b != 1:
+                    continue
+                plain, split = hip_lib.control_overhead(rows, p, b, warmup, iters, coop)
+                out.append({"rows": rows, "split": p, "barriers": b, "cooperative": coop,
                             "plain_ms": plain, "split_ms": split,
                             "overhead_ms": max(split - plain, 0.0)})
     return out
@@ -171,7 +174,7 @@ def main(argv=None) -> int:
     if args.control:
         result["control"] = run_control_sweep()
         for row in result["control"]:
-            print("CONTROL,{rows},{split},{barriers},{xcd_local:d},{plain_ms:.6f},{split_ms:.6f},"
+            print("CONTROL,{rows},{split},{barriers},{cooperative:d},{plain_ms:.6f},{split_ms:.6f},"
                   "{overhead_ms:.6f}".format(**row))
     if args.json:
         with open(args.json, "w", encoding="utf-8") as fh:

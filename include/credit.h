@@ -147,6 +147,77 @@ int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamma,
                               float* rstd, int64_t rows, int64_t cols,
                               float eps, const credit_cfg* cfg);
 
+/* ------------------------------------------ C3: RMSNorm forward ---------
+ * rstd[r] = 1/sqrt(mean_j x[r,j]^2 + eps) (fp32), y = x * rstd * w (bf16).
+ * No RMSNorm exists in the reference; the row sum of squares is the LARS
+ * norm of src/workloads/lars_momentum.cu:283-319 (dsmem_eval/workloads.py:
+ * 139-140).  Variants: STAGED (row in one workgroup's VGPRs, cols <= 65536),
+ * SPLIT (cfg->split workgroups per row exchanging one partial), READ (two
+ * streaming passes; any shape).  AUTO: STAGED when the row fits, else the
+ * smallest SPLIT that holds it; READ for cols % 8 != 0 or unaligned
+ * buffers. */
+int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, float* rstd,
+                            int64_t rows, int64_t cols, float eps, const credit_cfg* cfg);
+
+/* ------------------------------------------ C3: RMSNorm backward --------
+ * Given the forward's rstd: g = dy*w, xhat = x*rstd, c = mean_j(g*xhat),
+ * dx = rstd*(g - xhat*c) (bf16), dw[j] = sum_r dy[r,j]*xhat[r,j] (fp32,
+ * accumulated in fp64, summed over row blocks in a fixed order, so it is
+ * deterministic).  Needs cols % 8 == 0 and 16-byte aligned x, w, dy, dx, dw.
+ * Variants: STAGED (cols <= 16384), SPLIT (P >= cols/16384 members per row
+ * block, one exchange per row), READ (a streaming row-dot pre-pass, then
+ * column tiles).  rows == 0 writes dw = 0.  Always uses the workspace (dw
+ * partials). */
+int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* dy,
+                            const float* rstd, uint16_t* dx, float* dw, int64_t rows,
+                            int64_t cols, const credit_cfg* cfg);
+
+/* ------------------------------------- C4: online softmax forward -------
+ * m = max_j x, s = sum_j e^(x - m): p = e^(x - m)/s, rowmax = m (NaN-
+ * propagating, bit-exact with torch.amax), lse = m + ln s; fp32.  The
+ * reference fuses softmax into its backward (src/workloads/
+ * softmax_logits_backward.cu:314-476) and emits no p, max or lse.
+ * Variants: STAGED (row <= 65536 columns in one workgroup's VGPRs), SPLIT
+ * (P workgroups per row merging (max, sum) pairs once: one read, one write),
+ * READ (online streaming pass + output pass; any shape).  AUTO: the fewest
+ * members that hold the row; READ for cols % 4 != 0 or unaligned buffers. */
+int credit_softmax_fwd_f32(const float* x, float* p, float* rowmax, float* lse, int64_t rows,
+                           int64_t cols, const credit_cfg* cfg);
+
+/* ------------------------------------- C4: softmax backward -------------
+ * dx = p * (dy - sum_j p*dy), fp32, given the forward's p.  Variants as the
+ * forward; STAGED holds p and dy for rows <= 32768 columns. */
+int credit_softmax_bwd_f32(const float* p, const float* dy, float* dx, int64_t rows,
+                           int64_t cols, const credit_cfg* cfg);
+
+/* ------------------------------- softmax-logits backward (reference) ----
+ * p = softmax(logits), dx = p * (dy - sum_j p*dy): the reference workload
+ * softmax_logits_backward (dsmem_eval/workloads.py:122-125, kernels
+ * src/workloads/softmax_logits_backward.cu:314-476, launched per
+ * dsmem_eval/runner.py:280-310), fp32.  SPLIT exchanges twice per row
+ * ((max, sum), then sum p*dy); READ streams three passes. */
+int credit_softmax_logits_bwd_f32(const float* logits, const float* dy, float* dx,
+                                  int64_t rows, int64_t cols, const credit_cfg* cfg);
+
+/* ------------------------------------------ C5: norm-fused FFN ----------
+ * out = bf16(x + bf16(GELU_tanh(bf16(x * rstd) @ W1^T)) @ W2^T) with
+ * rstd = 1/sqrt(mean_j x^2 + eps) per row (RMSNorm with unit weight), fp32
+ * accumulation on bf16 MFMA.  Weights in the nn.Linear layout:
+ * w1 [f, d] and w2 [d, f] (K contiguous).  x, out [rows, d].  rows, d and
+ * f must be multiples of 128; buffers 16-byte aligned.  The hidden
+ * activation h [rows, f] lives in the workspace (query with
+ * credit_workspace_bytes(CREDIT_OP_FFN, rows, f, ...)).  No FFN exists in
+ * the reference. */
+int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w1, const uint16_t* w2,
+                                 uint16_t* out, int64_t rows, int64_t d, int64_t f, float eps,
+                                 const credit_cfg* cfg);
+
+/* dst[c, r] = src[r, c] for a rows x cols bf16 matrix: converts a [d, f]
+ * weight to the [f, d] layout credit_ffn_rmsnorm_gelu_bf16 takes.  No
+ * counterpart in the reference. */
+int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t cols,
+                          const credit_cfg* cfg);
+
 /* ------------------------------------------- calibration (gfx950) -------
  * Replaces the reference's build/primitive_benchmark executable
  * (src/primitive_benchmark.cu:605-993, its stdout parsed by
@@ -177,13 +248,14 @@ int credit_microbench(int32_t which, int64_t bytes, int32_t iters, double* resul
                       int32_t n_results);
 
 /* Replaces build/cluster_control (src/cluster_control.cu:114-180, read at
- * dsmem_eval/runner.py:313-347): time of a cooperative grid whose groups of
- * `split` workgroups meet at `barriers` arrival barriers, against a plain
- * launch of the same grid that does nothing.  The grid covers min(rows,
- * co-resident capacity / split) groups.  xcd_local != 0 places a group's
- * members on one XCD (workgroup ids congruent mod 8). */
+ * dsmem_eval/runner.py:313-347): time of a grid of `rows` groups of `split`
+ * workgroups that meet at `barriers` split-row barriers (the ticketed
+ * exchange of the split kernels), against a plain launch of the same grid
+ * that does nothing.  cooperative != 0 launches the barrier grid with
+ * hipLaunchCooperativeKernel instead (capped at what fits the device), to
+ * expose that launch path's fixed cost. */
 int credit_control_overhead(int64_t rows, int32_t split, int32_t barriers, int32_t warmup,
-                            int32_t iters, int32_t xcd_local, double* plain_ms,
+                            int32_t iters, int32_t cooperative, double* plain_ms,
                             double* split_ms);
 
 #ifdef __cplusplus

@@ -1,0 +1,87 @@
+"""GPU parity of credit_ffn_rmsnorm_gelu_bf16 (C5) and credit_transpose_bf16.
+
+out = x + GELU_tanh(RMSNorm(x) @ W1) @ W2 against the float64 oracle
+(oracle.reference.ffn_rmsnorm_gelu, which rounds the normalised activations
+and h to bf16 as the MFMA path feeds them).  Tolerance: bf16 output within
+rtol 1e-2 / atol 1e-2.  The small shapes also pin the
+MFMA operand/accumulator lane layout: a wrong row/column mapping scrambles
+every output.  At the full C5 shape the oracle checks a sample of rows
+(each row of out depends only on the same row of x)."""
+import numpy as np
+import pytest
+import torch
+
+from credit_amd import hip_lib
+from credit_amd.workloads import WORKLOADS, make_ffn_inputs
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1.0e-6
+BF16 = dict(rtol=1e-2, atol=1e-2)
+
+
+def make(rows, d, f, seed):
+    g = torch.Generator().manual_seed(seed)
+    return make_ffn_inputs(rows, d, g, ffn_dim=f)
+
+
+def run_ffn(x, w1, w2, gpu):
+    xs = x.to(gpu)
+    w1t = hip_lib.linear_layout(w1.to(gpu))
+    w2t = hip_lib.linear_layout(w2.to(gpu))
+    out = torch.full_like(xs, float("nan"))
+    hip_lib.ffn(xs, w1t, w2t, out, EPS, hip_lib.make_cfg())
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def oracle(x, w1, w2, rows=None):
+    xs = x.float().numpy() if rows is None else x[rows].float().numpy()
+    return ref.ffn_rmsnorm_gelu(xs, w1.float().numpy(), w2.float().numpy(), EPS)
+
+
+@pytest.mark.parametrize("shape", [(64, 96), (128, 200), (3, 5), (257, 130)])
+def test_transpose_is_exact(gpu, shape):
+    src = torch.randn(shape, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    dst = torch.empty(shape[1], shape[0], dtype=torch.bfloat16, device=gpu)
+    hip_lib.transpose(src.to(gpu), dst)
+    torch.cuda.synchronize()
+    assert torch.equal(dst.cpu(), src.t().contiguous())
+
+
+@pytest.mark.parametrize("rows,d,f", [(128, 128, 128), (128, 256, 384), (256, 128, 512),
+                                      (384, 512, 256)])
+def test_ffn_small_shapes(gpu, rows, d, f):
+    print(f"ffn rows={rows} d={d} f={f}", flush=True)
+    x, w1, w2 = make(rows, d, f, seed=rows + d + f)
+    np.testing.assert_allclose(run_ffn(x, w1, w2, gpu), oracle(x, w1, w2), **BF16)
+
+
+def test_ffn_structured_inputs_pin_layout(gpu):
+    """Identity-like weights make each output element depend on one input
+    element, so any transposed or shifted fragment mapping fails."""
+    rows, d = 128, 256
+    f = d
+    x = (torch.arange(rows * d, dtype=torch.float32).reshape(rows, d) % 7 - 3).to(torch.bfloat16)
+    w1 = torch.eye(d, dtype=torch.bfloat16) * 2
+    w2 = torch.eye(d, dtype=torch.bfloat16)
+    out = run_ffn(x, w1, w2, gpu)
+    np.testing.assert_allclose(out, oracle(x, w1, w2), **BF16)
+
+
+def test_ffn_rejects_unsupported_shapes(gpu):
+    x, w1, w2 = make(100, 128, 128, seed=3)
+    with pytest.raises(hip_lib.CreditError) as err:
+        run_ffn(x, w1, w2, gpu)
+    assert err.value.status == -4
+
+
+def test_ffn_full_config_sampled_rows(gpu):
+    """BASELINE C5: x [4096, 8192], W1 [8192, 28672], W2 [28672, 8192]; 48
+    rows (spread over all row tiles) against the float64 oracle."""
+    x, w1, w2 = WORKLOADS["ffn"].make_inputs()
+    out = run_ffn(x, w1, w2, gpu)
+    rows = np.linspace(0, x.shape[0] - 1, 48).astype(int)
+    np.testing.assert_allclose(out[rows], oracle(x, w1, w2, rows), **BF16)
+    assert np.isfinite(out).all()
