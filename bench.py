@@ -27,6 +27,31 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
+# Kernels one AUTO call launches at the BASELINE shape, and the committed
+# rocprofv3 PMC summary (FETCH_SIZE / WRITE_SIZE, scaled by a copy kernel of
+# known size; credit_amd/traffic.py) their HBM bytes per call come from.
+TRAFFIC_SUMMARY = ROOT / "profiles" / "hbm_traffic_suite.json"
+CALL_KERNELS = {
+    "row_sum_max": ["row_sum_max_read_kernel<256>"],
+    "layernorm_fwd": ["layernorm_fwd_staged_kernel<512, 8>"],
+    "rmsnorm_fwd": ["rmsnorm_fwd_slice_kernel<1024, 8>"],
+    "rmsnorm_bwd": ["rmsnorm_bwd_slice_kernel<512, 4>", "rmsnorm_dw_reduce_kernel"],
+    "softmax_fwd": ["softmax_fwd_slice_kernel<1024, 16>"],
+    "softmax_bwd": ["softmax_bwd_slice_kernel<1024, 8>"],
+    "softmax_logits_backward": ["softmax_logits_bwd_slice_kernel<1024, 8>"],
+    "ffn": ["ffn_rstd_kernel", "ffn_gemm_kernel<0>", "ffn_gemm_kernel<1>"],
+}
+
+
+def measured_traffic(name):
+    """HBM bytes per call from the PMC summary, or None when not profiled."""
+    try:
+        kernels = json.loads(TRAFFIC_SUMMARY.read_text())["kernels"]
+        return sum(kernels[k]["fetch_bytes"] + kernels[k]["write_bytes"]
+                   for k in CALL_KERNELS[name])
+    except (OSError, KeyError, ValueError):
+        return None
+
 
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
@@ -185,14 +210,15 @@ def measure(name, args, hip_lib, torch, dev, with_cpu):
                    roofline={"bound": "mfma", "achieved": round(flops / (kernel_ms * 1e-3) / 1e12, 2),
                              "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(flops / (kernel_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                             "traffic": None})
+                             "traffic": measured_traffic(name)})
     else:
         nbytes = spec.algorithmic_bytes(spec.rows, spec.cols)
         achieved = nbytes / (kernel_ms * 1e-3) / 1e9
         out.update(metric="HBM GB/s", value=round(nbytes / (ms_step * 1e-3) / 1e9, 1), unit="GB/s",
                    bytes_per_call=nbytes,
                    roofline={"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None})
+                             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                             "traffic": measured_traffic(name)})
         variants = {}
         for variant, split in VARIANT_SWEEP.get(name, []):
             try:

@@ -164,8 +164,16 @@ def main(argv=None) -> int:
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--control", action="store_true", help="also sweep the barrier overhead")
     ap.add_argument("--json", help="write the measurements (and control sweep) here")
+    ap.add_argument("--only", choices=sorted(hip_lib.MICROBENCH),
+                    help="run just this microbenchmark (e.g. hbm_copy of --hbm-bytes as the "
+                         "known-size reference for PMC byte counters) and print its results")
     args = ap.parse_args(argv)
     import torch  # noqa: F401  (loads the HIP runtime torch uses before the library)
+
+    if args.only:
+        res = hip_lib.microbench(args.only, args.hbm_bytes, args.iters)
+        print(f"{args.only} bytes={args.hbm_bytes} iters={args.iters} results={res}", flush=True)
+        return 0
 
     parsed = run_microbenchmarks(args.hbm_bytes, args.iters)
     sys.stdout.write(format_profile_text(parsed))

@@ -1,0 +1,90 @@
+"""Per-kernel HBM traffic from rocprofv3 counter runs.
+
+``rocprofv3 --pmc FETCH_SIZE`` and ``--pmc WRITE_SIZE`` (one counter per run)
+write ``*_counter_collection.csv`` with one row per dispatch; the values are
+KiB.  On gfx950 the raw FETCH_SIZE reads half of the bytes a kernel fetches
+and WRITE_SIZE reads all of them, so each counter is scaled by what it reads
+for a plain copy kernel of known size (``python -m credit_amd.profile --only
+hbm_copy --hbm-bytes B``, whose every ``mb_copy*`` dispatch reads B bytes
+and writes B bytes).
+
+    python -m credit_amd.traffic --fetch F.csv --write W.csv \\
+        --copy-fetch CF.csv --copy-write CW.csv --copy-bytes B --json out.json
+
+The JSON maps a short kernel name (template arguments kept, namespaces and
+parameter lists dropped) to its mean fetched and written bytes per dispatch;
+bench.py reports the sum as ``roofline.traffic`` for the headline kernel.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import json
+from pathlib import Path
+
+
+def short_name(kernel: str) -> str:
+    """'void credit::(anonymous namespace)::f<512, 8>(args)' -> 'f<512, 8>'."""
+    name = kernel.strip().replace("(anonymous namespace)::", "")
+    if name.startswith("void "):
+        name = name[5:]
+    depth = 0
+    for i, ch in enumerate(name):  # drop the parameter list (first '(' outside <>)
+        depth += (ch == "<") - (ch == ">")
+        if ch == "(" and depth == 0:
+            name = name[:i]
+            break
+    head, sep, tail = name.partition("<")
+    return head.split("::")[-1] + sep + tail
+
+
+def per_kernel_kib(path: str | Path) -> dict[str, tuple[float, int]]:
+    """Mean counter value (KiB) per dispatch and dispatch count, by kernel."""
+    acc: dict[str, list[float]] = collections.defaultdict(list)
+    with open(path, newline="") as fh:
+        for row in csv.DictReader(fh):
+            acc[short_name(row["Kernel_Name"])].append(float(row["Counter_Value"]))
+    return {k: (sum(v) / len(v), len(v)) for k, v in acc.items()}
+
+
+def copy_scale(path: str | Path, copy_bytes: int) -> float:
+    """Bytes per counted KiB, from the mb_copy dispatches of a known size."""
+    vals = [kib for name, (kib, _) in per_kernel_kib(path).items() if name.startswith("mb_copy")]
+    if not vals:
+        raise RuntimeError(f"{path}: no mb_copy dispatches")
+    return copy_bytes / (sum(vals) / len(vals))
+
+
+def summarize(fetch: str, write: str, copy_fetch: str, copy_write: str,
+              copy_bytes: int) -> dict:
+    fs = copy_scale(copy_fetch, copy_bytes)
+    ws = copy_scale(copy_write, copy_bytes)
+    f = per_kernel_kib(fetch)
+    w = per_kernel_kib(write)
+    kernels = {}
+    for name in sorted(set(f) | set(w)):
+        fk = f.get(name, (0.0, 0))
+        wk = w.get(name, (0.0, 0))
+        kernels[name] = {"fetch_bytes": round(fk[0] * fs), "write_bytes": round(wk[0] * ws),
+                         "dispatches": max(fk[1], wk[1])}
+    return {"fetch_bytes_per_kib": fs, "write_bytes_per_kib": ws, "copy_bytes": copy_bytes,
+            "kernels": kernels}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--fetch", required=True)
+    ap.add_argument("--write", required=True)
+    ap.add_argument("--copy-fetch", required=True)
+    ap.add_argument("--copy-write", required=True)
+    ap.add_argument("--copy-bytes", type=int, required=True)
+    ap.add_argument("--json", required=True)
+    args = ap.parse_args(argv)
+    out = summarize(args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_bytes)
+    Path(args.json).write_text(json.dumps(out, indent=1) + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
