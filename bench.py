@@ -40,6 +40,8 @@ CALL_KERNELS = {
     "softmax_bwd": ["softmax_bwd_slice_kernel<1024, 8>"],
     "softmax_logits_backward": ["softmax_logits_bwd_slice_kernel<1024, 8>"],
     "ffn": ["ffn_rstd_kernel", "ffn_gemm_kernel<0>", "ffn_gemm_kernel<1>"],
+    "layernorm_backward": ["layernorm_bwd_slice_kernel<float, 1024, 8>"],
+    "layernorm_backward_bf16": ["layernorm_bwd_slice_kernel<unsigned short, 1024, 4>"],
 }
 
 
@@ -243,6 +245,8 @@ VARIANT_SWEEP = {
     "softmax_fwd": [("read", 0), ("split", 4), ("split", 8), ("split", 16)],
     "softmax_bwd": [("read", 0), ("split", 8), ("split", 16)],
     "softmax_logits_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
+    "layernorm_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
+    "layernorm_backward_bf16": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
 }
 
 
@@ -286,7 +290,8 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if args.workload in ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd", "ffn") else "f32",
+        "dtype": "bf16" if args.workload in ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd", "ffn",
+                                             "layernorm_backward_bf16") else "f32",
         "data": "synthetic (seeded CPU generator, BASELINE distributions)",
         "config": {"workload": args.workload, "rows": head["rows"], "cols": head["cols"],
                    "device": info["name"], "arch": info["arch"], "cus": info["cu_count"],

@@ -243,6 +243,12 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
     case CREDIT_OP_RMSNORM_BWD:
       body = rmsnorm_bwd_workspace(rows, cols, variant, split, cus);
       break;
+    case CREDIT_OP_LAYERNORM_BWD:
+      body = layernorm_bwd_workspace(rows, cols, variant, split, 4);
+      break;
+    case CREDIT_OP_LAYERNORM_BWD_BF16:
+      body = layernorm_bwd_workspace(rows, cols, variant, split, 2);
+      break;
     case CREDIT_OP_FFN:  // cols = the FFN hidden width f
       body = ffn_workspace(rows, cols);
       break;

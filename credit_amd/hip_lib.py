@@ -51,6 +51,7 @@ OPS = {
     "softmax_bwd": 7,
     "softmax_logits_backward": 8,
     "ffn": 9,
+    "layernorm_backward_bf16": 10,
 }
 
 
@@ -115,6 +116,8 @@ SIGNATURES: dict[str, list] = {
     "credit_softmax_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_softmax_logits_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_ffn_rmsnorm_gelu_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
+    "credit_layernorm_bwd_f32": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
+    "credit_layernorm_bwd_bf16": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_transpose_bf16": [_P, _P, _I64, _I64, _CFG],
     "credit_microbench": [ctypes.c_int32, _I64, ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
                           ctypes.c_int32],
@@ -361,6 +364,21 @@ def softmax_logits_backward(logits: torch.Tensor, dy: torch.Tensor, dx: torch.Te
     )
 
 
+def layernorm_backward(x: torch.Tensor, dy: torch.Tensor, gamma: torch.Tensor,
+                       dx: torch.Tensor, eps: float, cfg: CreditCfg) -> None:
+    """fp32 or bf16 (all four tensors the same dtype)."""
+    rows, cols = _rows_cols(x)
+    if x.dtype == torch.float32:
+        fn, name, dt = load_library().credit_layernorm_bwd_f32, "credit_layernorm_bwd_f32", x.dtype
+    elif x.dtype == torch.bfloat16:
+        fn, name, dt = (load_library().credit_layernorm_bwd_bf16, "credit_layernorm_bwd_bf16",
+                        x.dtype)
+    else:
+        raise TypeError(f"layernorm_backward: unsupported dtype {x.dtype}")
+    check(fn(_ptr(x, "x", dt), _ptr(dy, "dy", dt), _ptr(gamma, "gamma", dt), _ptr(dx, "dx", dt),
+             rows, cols, float(eps), ctypes.byref(cfg)), name)
+
+
 def ffn(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, out: torch.Tensor, eps: float,
         cfg: CreditCfg) -> None:
     """out = x + GELU_tanh(RMSNorm(x) @ w1.T) @ w2.T; w1 [f, d], w2 [d, f]."""
@@ -468,8 +486,19 @@ def launch_ffn(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
     ffn(x, w1, w2, out, FFN_EPS, make_cfg(config.variant, config.split))
 
 
+LAYERNORM_EPS = 1.0e-5  # dsmem_eval/workloads.py:55
+
+
+def launch_layernorm_backward(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    x, dy, gamma = inputs
+    (dx,) = outputs
+    layernorm_backward(x, dy, gamma, dx, LAYERNORM_EPS, make_cfg(config.variant, config.split))
+
+
 HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
     "ffn": launch_ffn,
+    "layernorm_backward": launch_layernorm_backward,
+    "layernorm_backward_bf16": launch_layernorm_backward,
     "row_sum_max": launch_row_sum_max,
     "layernorm_fwd": launch_layernorm_fwd,
     "rmsnorm_fwd": launch_rmsnorm_fwd,
@@ -495,6 +524,7 @@ def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch
         return torch.empty_like(x), torch.empty(x.shape[1], **f32)
     if name == "softmax_fwd":
         return torch.empty_like(x), torch.empty(rows, **f32), torch.empty(rows, **f32)
-    if name in ("softmax_bwd", "softmax_logits_backward", "ffn"):
+    if name in ("softmax_bwd", "softmax_logits_backward", "ffn", "layernorm_backward",
+                "layernorm_backward_bf16"):
         return (torch.empty_like(x),)
     raise KeyError(name)

@@ -136,6 +136,10 @@ def make_layernorm_backward_inputs(rows, cols, g):
     )
 
 
+def make_layernorm_backward_bf16_inputs(rows, cols, g):
+    return tuple(t.to(torch.bfloat16) for t in make_layernorm_backward_inputs(rows, cols, g))
+
+
 def make_softmax_logits_inputs(rows, cols, g):
     return (
         _uniform((rows, cols), -4.0, 4.0, g),
@@ -265,6 +269,22 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         modeled_bytes_per_element=32.0,
         reread_bytes_per_element=12.0,
         staged_bytes_per_element=4,
+        reductions_per_stage=(2, 2),
+    ),
+    "layernorm_backward_bf16": WorkloadSpec(
+        name="layernorm_backward_bf16",
+        label="LayerNorm backward (bf16)",
+        category="normalization",
+        rows=2048,
+        cols=65536,
+        input_factory=make_layernorm_backward_bf16_inputs,
+        output_names=("dx",),
+        algorithmic_bytes=lambda r, c: 2 * r * c * 3 + 2 * c,
+        tolerances=((1.0e-2, 1.0e-2),),
+        seed=1234,
+        modeled_bytes_per_element=16.0,
+        reread_bytes_per_element=6.0,
+        staged_bytes_per_element=2,
         reductions_per_stage=(2, 2),
     ),
     "softmax_logits_backward": WorkloadSpec(

@@ -81,6 +81,7 @@ typedef struct credit_cfg {
 #define CREDIT_OP_SOFTMAX_BWD 7
 #define CREDIT_OP_SOFTMAX_LOGITS_BWD 8
 #define CREDIT_OP_FFN 9
+#define CREDIT_OP_LAYERNORM_BWD_BF16 10
 
 /* ------------------------------------------------------------ library --- */
 
@@ -146,6 +147,21 @@ int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamma,
                               const uint16_t* beta, uint16_t* y, float* mean,
                               float* rstd, int64_t rows, int64_t cols,
                               float eps, const credit_cfg* cfg);
+
+/* -------------------------------- LayerNorm backward (reference) -------
+ * dx = (g - mean(g) - xhat * mean(g * xhat)) * rstd with g = dy * gamma and
+ * the row's two-pass statistics (xhat = (x - mean) * rstd): the reference
+ * workload layernorm_backward (dsmem_eval/workloads.py:53-61, kernels
+ * src/workloads/layernorm_backward.cu:274-438, launched per
+ * dsmem_eval/runner.py:280-310).  fp32 and bf16 (fp32 arithmetic).
+ * Variants: STAGED (x and dy of the row in one workgroup's VGPRs: 32768 fp32
+ * / 32768 bf16 columns), SPLIT (two exchanges per row, as the reference's
+ * two cluster stages), READ (three streaming passes; any shape). */
+int credit_layernorm_bwd_f32(const float* x, const float* dy, const float* gamma, float* dx,
+                             int64_t rows, int64_t cols, float eps, const credit_cfg* cfg);
+int credit_layernorm_bwd_bf16(const uint16_t* x, const uint16_t* dy, const uint16_t* gamma,
+                              uint16_t* dx, int64_t rows, int64_t cols, float eps,
+                              const credit_cfg* cfg);
 
 /* ------------------------------------------ C3: RMSNorm forward ---------
  * rstd[r] = 1/sqrt(mean_j x[r,j]^2 + eps) (fp32), y = x * rstd * w (bf16).

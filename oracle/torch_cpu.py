@@ -79,6 +79,8 @@ FUNCTIONS = {
     "softmax_fwd": lambda x, dy: softmax_fwd(x),
     "softmax_bwd": lambda x, dy: softmax_bwd(torch.softmax(x, dim=-1), dy),
     "layernorm_backward": layernorm_backward,
+    "layernorm_backward_bf16": lambda x, dy, g: layernorm_backward(
+        x.float(), dy.float(), g.float()).to(x.dtype),
     "softmax_logits_backward": softmax_logits_backward,
     "ffn": ffn,
 }
