@@ -73,37 +73,10 @@ def parse_args(argv=None):
 # ----------------------------------------------------------- GPU timing ---
 
 
-def prepare_inputs(name, cpu_inputs, hip_lib, torch, dev):
-    """Launcher inputs on the GPU.  The backward passes take what their
-    forward produced (rstd, p); it is computed here by this library's own
-    forward kernels, outside the timed region."""
-    ins = tuple(t.to(dev) for t in cpu_inputs)
-    if name == "rmsnorm_fwd":
-        return ins[:2]
-    if name == "rmsnorm_bwd":
-        x, w, dy = ins
-        y, rstd = hip_lib.allocate_outputs("rmsnorm_fwd", (x, w))
-        hip_lib.HIP_LAUNCHERS["rmsnorm_fwd"]((x, w), (y, rstd))
-        del y
-        return x, w, dy, rstd
-    if name == "softmax_fwd":
-        return ins[:1]
-    if name == "ffn":
-        x, w1, w2 = ins  # BASELINE layout: W1 [d, f], W2 [f, d]
-        return x, hip_lib.linear_layout(w1), hip_lib.linear_layout(w2)
-    if name == "softmax_bwd":
-        x, dy = ins
-        p, m, lse = hip_lib.allocate_outputs("softmax_fwd", (x,))
-        hip_lib.HIP_LAUNCHERS["softmax_fwd"]((x,), (p, m, lse))
-        del x, m, lse
-        return p, dy
-    return ins
-
-
 def build_case(name, spec, hip_lib, torch, dev, nsets):
     """Inputs (resident), rotating output sets and a launch(set_index, variant, split)."""
     cpu_inputs = spec.make_inputs()
-    inputs = [prepare_inputs(name, cpu_inputs, hip_lib, torch, dev) for _ in range(nsets)]
+    inputs = [hip_lib.prepare_inputs(name, cpu_inputs, dev) for _ in range(nsets)]
     outputs = [hip_lib.allocate_outputs(name, ins) for ins in inputs]
     torch.cuda.synchronize()
     launcher = hip_lib.HIP_LAUNCHERS[name]

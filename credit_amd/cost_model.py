@@ -134,6 +134,12 @@ def staged_bytes_per_workgroup(spec: WorkloadModelSpec, cols: int, split: int) -
 
 
 def row_fits_one_workgroup(spec: WorkloadModelSpec, cols: int, profile: DeviceProfile) -> bool:
+    """Whether the no-split variant holds the row on chip (single HBM pass):
+    the kernel's own STAGED capacity when the spec states it, else the
+    VGPR + LDS budget of one workgroup."""
+    cap = getattr(spec, "staged_max_cols", 0)
+    if cap:
+        return cols <= cap
     return staged_bytes_per_workgroup(spec, cols, 1) <= profile.onchip_bytes_per_workgroup
 
 

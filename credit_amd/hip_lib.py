@@ -509,6 +509,33 @@ HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
 }
 
 
+def prepare_inputs(name: str, cpu_inputs: tuple[torch.Tensor, ...],
+                   device: torch.device | str) -> tuple[torch.Tensor, ...]:
+    """The workload registry's inputs (credit_amd.workloads) as launcher
+    inputs on `device`.  The backward passes take what their forward
+    produced (rstd, p), computed here by this library's own forward kernels;
+    the FFN weights are moved to the nn.Linear layout."""
+    ins = tuple(t.to(device) for t in cpu_inputs)
+    if name == "rmsnorm_fwd":
+        return ins[:2]
+    if name == "rmsnorm_bwd":
+        x, w, dy = ins
+        y, rstd = allocate_outputs("rmsnorm_fwd", (x, w))
+        HIP_LAUNCHERS["rmsnorm_fwd"]((x, w), (y, rstd))
+        return x, w, dy, rstd
+    if name == "softmax_fwd":
+        return ins[:1]
+    if name == "softmax_bwd":
+        x, dy = ins
+        p, m, lse = allocate_outputs("softmax_fwd", (x,))
+        HIP_LAUNCHERS["softmax_fwd"]((x,), (p, m, lse))
+        return p, dy
+    if name == "ffn":
+        x, w1, w2 = ins  # W1 [d, f], W2 [f, d]
+        return x, linear_layout(w1), linear_layout(w2)
+    return ins
+
+
 def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch.Tensor, ...]:
     """Output buffers of a launcher, as dsmem_eval/triton_kernels.py:403-414."""
     x = inputs[0]

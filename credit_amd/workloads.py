@@ -42,13 +42,17 @@ class WorkloadSpec:
     # Per-output (atol, rtol); None means bit-exact.
     tolerances: tuple[tuple[float, float] | None, ...]
     seed: int = 0
-    # Cost-model metadata (dsmem_eval/workload_metadata.py:6-35): bytes per
-    # element of the no-staging variant, the re-read share staging removes,
-    # bytes staged on chip per element, partials exchanged per stage.
+    # Cost-model metadata (dsmem_eval/workload_metadata.py:6-35): HBM bytes
+    # per element of this build's READ (no-staging) variant, the re-read share
+    # staging removes, bytes staged on chip per element, partials exchanged
+    # per split stage.
     modeled_bytes_per_element: float = 0.0
     reread_bytes_per_element: float = 0.0
     staged_bytes_per_element: int = 0
     reductions_per_stage: tuple[int, ...] = field(default_factory=tuple)
+    # Widest row the STAGED (no-split, row held on chip) variant takes; 0 when
+    # the operation has no split variant.  Wider rows need SPLIT or READ.
+    staged_max_cols: int = 0
 
     @property
     def barrier_count(self) -> int:
@@ -167,6 +171,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         reread_bytes_per_element=0.0,
         staged_bytes_per_element=0,
         reductions_per_stage=(2,),
+        staged_max_cols=1 << 30,
     ),
     "layernorm_fwd": WorkloadSpec(
         name="layernorm_fwd",
@@ -182,6 +187,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         reread_bytes_per_element=4.0,   # the second and third reads of x
         staged_bytes_per_element=2,
         reductions_per_stage=(1, 1),
+        staged_max_cols=65536,
     ),
     "rmsnorm_fwd": WorkloadSpec(
         name="rmsnorm_fwd",
@@ -197,6 +203,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         reread_bytes_per_element=2.0,
         staged_bytes_per_element=2,
         reductions_per_stage=(1,),
+        staged_max_cols=65536,
     ),
     "rmsnorm_bwd": WorkloadSpec(
         name="rmsnorm_bwd",
@@ -212,6 +219,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         reread_bytes_per_element=4.0,
         staged_bytes_per_element=4,
         reductions_per_stage=(1,),
+        staged_max_cols=16384,
     ),
     "softmax_fwd": WorkloadSpec(
         name="softmax_fwd",
@@ -227,6 +235,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         reread_bytes_per_element=4.0,
         staged_bytes_per_element=4,
         reductions_per_stage=(2,),
+        staged_max_cols=65536,
     ),
     "softmax_bwd": WorkloadSpec(
         name="softmax_bwd",
@@ -242,6 +251,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         reread_bytes_per_element=8.0,
         staged_bytes_per_element=8,
         reductions_per_stage=(1,),
+        staged_max_cols=32768,
     ),
     "ffn": WorkloadSpec(
         name="ffn",
@@ -266,10 +276,11 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         algorithmic_bytes=lambda r, c: 4 * r * c * 3 + 4 * c,
         tolerances=((2.0e-2, 2.0e-2),),
         seed=1234,
-        modeled_bytes_per_element=32.0,
+        modeled_bytes_per_element=24.0,
         reread_bytes_per_element=12.0,
         staged_bytes_per_element=4,
         reductions_per_stage=(2, 2),
+        staged_max_cols=32768,
     ),
     "layernorm_backward_bf16": WorkloadSpec(
         name="layernorm_backward_bf16",
@@ -282,10 +293,11 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         algorithmic_bytes=lambda r, c: 2 * r * c * 3 + 2 * c,
         tolerances=((1.0e-2, 1.0e-2),),
         seed=1234,
-        modeled_bytes_per_element=16.0,
+        modeled_bytes_per_element=12.0,
         reread_bytes_per_element=6.0,
         staged_bytes_per_element=2,
         reductions_per_stage=(2, 2),
+        staged_max_cols=32768,
     ),
     "softmax_logits_backward": WorkloadSpec(
         name="softmax_logits_backward",
@@ -298,10 +310,11 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         algorithmic_bytes=lambda r, c: 4 * r * c * 3,
         tolerances=((3.0e-3, 3.0e-3),),
         seed=1234,
-        modeled_bytes_per_element=28.0,
-        reread_bytes_per_element=16.0,
+        modeled_bytes_per_element=24.0,
+        reread_bytes_per_element=12.0,
         staged_bytes_per_element=8,
-        reductions_per_stage=(1, 1, 1),
+        reductions_per_stage=(2, 1),
+        staged_max_cols=32768,
     ),
 }
 
