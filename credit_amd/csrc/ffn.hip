@@ -21,6 +21,8 @@
 // 2 x 2 wave grid owns a 64 x 64 quadrant as 2 x 2 v_mfma_f32_32x32x16_bf16
 // tiles.  Global tiles are prefetched into registers one K-step ahead, so
 // the next tile's HBM/L2 latency overlaps this step's MFMAs.
+#include <initializer_list>
+
 #include "api_internal.hpp"
 #include "common.hpp"
 
@@ -187,6 +189,191 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
       }
 }
 
+// ----------------------------------------------------- 256 x 256 tiles ---
+// The main GEMM: C[m, n] = epi(sum_k A[m, k] * B[n, k]) with 256 x 256 x 32
+// tiles per 256-lane workgroup.  Wave (wm, wn) of the 2 x 2 wave grid owns a
+// 128 x 128 quadrant as 4 x 4 v_mfma_f32_32x32x16_bf16 tiles (256 fp32
+// accumulators per lane, held in AGPRs).
+//  - Operand tiles go straight from global memory to LDS
+//    (global_load_lds_dwordx4: lane l of a wave writes bytes [16 l, 16 l + 16)
+//    of the wave's 1 KiB LDS block) through a ring of kStages K-steps.
+//  - Each K-step is two half-steps of 16 MFMAs (k = 16 each).  The operand
+//    fragments of the next half-step are read from LDS while the current
+//    half-step's MFMAs issue (one ds_read_b128 after every two MFMAs, pinned
+//    with sched_group_barrier), so the MFMA pipe never waits on LDS latency.
+//  - One barrier per K-step, lagged: it publishes step ks+2 and proves every
+//    wave is done reading stage ks, which the following issue refills; the
+//    next step's first fragments (stage ks+1, published one step earlier)
+//    are read before it.
+//  - The K loop is unrolled over the kStages stages so every stage offset
+//    is a compile-time constant.
+//  - LDS rows are 64 bytes (32 bf16 of K); the 16-byte chunk c of row r sits
+//    at position c ^ ((r >> 2) & 3), so the fragment reads of 16 consecutive
+//    rows (four rows share a 256-byte bank row) hit 16 distinct 4-bank groups.
+//   kEpiGelu:     C = bf16(GELU(acc * scale[m]))   (RMSNorm folded in: the
+//                 row scale commutes with the GEMM)
+//   kEpiResidual: C = bf16(acc + R[m, n])
+constexpr int kBig = 256;
+constexpr int kBigK = 32;
+constexpr int kStages = 4;
+constexpr int kBigTile = kBig * kBigK * 2;   // one operand tile, bytes (16 KiB)
+constexpr int kBigStage = 2 * kBigTile;      // A and B tiles of one stage
+constexpr int kBigLds = kStages * kBigStage; // 128 KiB
+// Tile blocks within an XCD: 8 M-tiles x 4 N-tiles run concurrently and
+// share their A rows and B columns through that XCD's L2.
+constexpr int kGroupM = 8;
+
+// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in
+// bits 15:14; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt(((N >> 4) << 14) | (0xF << 8) | (0x7 << 4) | (N & 15));
+}
+
+// sched_group_barrier masks.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+struct Frags {
+  bf16x8_t a[4], b[4];
+};
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads) void ffn_gemm256_kernel(
+    const uint16_t* __restrict__ A, const float* __restrict__ scale,
+    const uint16_t* __restrict__ B, const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
+    int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin,
+  // so XCD x runs ids x, x + 8, ...; give each XCD a contiguous run of the
+  // tile sequence, and walk that run in blocks of kGroupM M-tiles.
+  const int tiles_m = M / kBig, tiles_n = N / kBig;
+  const int total = tiles_m * tiles_n;
+  const int per_xcd = total / 8;  // host guarantees total % 8 == 0
+  const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  const int group = t / (kGroupM * tiles_n);
+  const int gm = tiles_m - group * kGroupM < kGroupM ? tiles_m - group * kGroupM : kGroupM;
+  const int within = t - group * kGroupM * tiles_n;
+  const int tm = group * kGroupM + within % gm;
+  const int tn = within / gm;
+  const int m0 = tm * kBig, n0 = tn * kBig;
+
+  // Load assignment: instruction i (0..3) of wave w fills LDS rows
+  // (4 i + w) * 16 + lane / 4, swizzled position lane % 4.  Element offsets
+  // fit 32 bits (host checks M*K and N*K < 2^31).
+  uint32_t a_off[4], b_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (4 * i + wave) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    a_off[i] = static_cast<uint32_t>((m0 + r) * K + c * 8);
+    b_off[i] = static_cast<uint32_t>((n0 + r) * K + c * 8);
+  }
+  auto issue = [&](int ks, int stage) {
+    char* a_base = smem + stage * kBigStage;
+    char* b_base = a_base + kBigTile;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int blk = (4 * i + wave) * 1024;
+      __builtin_amdgcn_global_load_lds(A + a_off[i] + ks * kBigK, (lds_ptr_t)(a_base + blk), 16,
+                                       0, 0);
+      __builtin_amdgcn_global_load_lds(B + b_off[i] + ks * kBigK, (lds_ptr_t)(b_base + blk), 16,
+                                       0, 0);
+    }
+  };
+
+  // Fragment addresses: row part (lane-dependent) plus the swizzled chunk of
+  // half-step kk; rows i*32 / j*32 further are +2048 bytes.
+  const int sw = ((lane & 31) >> 2) & 3;
+  const int a_row = (wm * 128 + (lane & 31)) * 64;
+  const int b_row = kBigTile + (wn * 128 + (lane & 31)) * 64;
+  const int koff[2] = {((lane >> 5) ^ sw) << 4, ((2 + (lane >> 5)) ^ sw) << 4};
+  auto read_frags = [&](int stage, int kk, Frags& f) {
+    const char* base = smem + stage * kBigStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      f.a[i] = *reinterpret_cast<const bf16x8_t*>(base + a_row + koff[kk] + i * 2048);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      f.b[j] = *reinterpret_cast<const bf16x8_t*>(base + b_row + koff[kk] + j * 2048);
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // 16 MFMAs on `cur` while the 8 fragment reads of `nxt` go out.
+  auto half_step = [&](const Frags& cur, Frags& nxt, int nstage, int nkk) {
+    read_frags(nstage, nkk, nxt);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur.a[i], cur.b[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+  };
+
+  const int ksteps = K / kBigK;  // host guarantees ksteps % kStages == 0
+#pragma unroll
+  for (int s = 0; s < kStages; ++s) issue(s, s);
+  wait_vmcnt<16>();  // steps 0 and 1 landed (this thread's loads)
+  __syncthreads();
+  Frags f0, f1;
+  read_frags(0, 0, f0);
+  for (int ks0 = 0; ks0 < ksteps; ks0 += kStages) {
+#pragma unroll
+    for (int s = 0; s < kStages; ++s) {
+      const int ks = ks0 + s;
+      half_step(f0, f1, s, 1);                    // MFMAs k 0..15; read k 16..31
+      half_step(f1, f0, (s + 1) % kStages, 0);    // MFMAs k 16..31; read next step
+      // Own loads of step ks+2 landed: only step ks+3 may stay in flight.
+      if (ks + 3 < ksteps)
+        wait_vmcnt<8>();
+      else
+        wait_vmcnt<0>();
+      __syncthreads();
+      if (ks + kStages < ksteps) issue(ks + kStages, s);
+    }
+  }
+
+  // Epilogue.  Accumulator register r of lane l holds row
+  // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of its 32 x 32 tile.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const float sc = EPI == kEpiGelu ? scale[m] : 1.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 128 + j * 32 + (lane & 31);
+        const size_t idx = static_cast<size_t>(m) * N + n;
+        float v = acc[i][j][r];
+        if (EPI == kEpiGelu)
+          v = gelu_tanh(v * sc);
+        else
+          v += bf16_to_f32(R[idx]);
+        C[idx] = f32_to_bf16(v);
+      }
+    }
+  }
+}
+
 // dst[c, r] = src[r, c] for a rows x cols bf16 matrix, through a 64 x 64
 // LDS tile.
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src,
@@ -207,6 +394,21 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// The 256-tile kernels take 128 KiB of dynamic LDS; allow it once per
+// process (the attribute belongs to the kernel, not to a device).
+int enable_big_lds() {
+  static int status = [] {
+    for (const void* fn : {reinterpret_cast<const void*>(ffn_gemm256_kernel<kEpiGelu>),
+                           reinterpret_cast<const void*>(ffn_gemm256_kernel<kEpiResidual>)}) {
+      const hipError_t e =
+          hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kBigLds);
+      if (e != hipSuccess) return hip_failure(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
+    }
+    return static_cast<int>(CREDIT_OK);
+  }();
+  return status;
+}
 
 }  // namespace
 
@@ -265,6 +467,24 @@ extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w
   const int M = static_cast<int>(rows), D = static_cast<int>(d), F = static_cast<int>(f);
   ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, D, eps);
   CREDIT_TRY(check_launch("ffn_rstd_kernel"));
+  // The 256-tile kernels: every dimension a multiple of 256 (so K / 32 is a
+  // multiple of kStages), tile counts a multiple of the 8 XCDs, 32-bit
+  // element offsets.
+  const bool big = M % kBig == 0 && D % kBig == 0 && F % kBig == 0 &&
+                   ((M / kBig) * (F / kBig)) % 8 == 0 && ((M / kBig) * (D / kBig)) % 8 == 0 &&
+                   static_cast<int64_t>(M) * F < (int64_t{1} << 31) &&
+                   static_cast<int64_t>(F) * D < (int64_t{1} << 31);
+  if (big) {
+    CREDIT_TRY(enable_big_lds());
+    const unsigned g1 = static_cast<unsigned>((M / kBig) * (F / kBig));
+    ffn_gemm256_kernel<kEpiGelu><<<dim3(g1), dim3(kThreads), kBigLds, stream>>>(
+        x, rstd, w1, nullptr, h, M, F, D);
+    CREDIT_TRY(check_launch("ffn_gemm256_kernel<gelu>"));
+    const unsigned g2 = static_cast<unsigned>((M / kBig) * (D / kBig));
+    ffn_gemm256_kernel<kEpiResidual><<<dim3(g2), dim3(kThreads), kBigLds, stream>>>(
+        h, nullptr, w2, x, out, M, D, F);
+    return check_launch("ffn_gemm256_kernel<residual>");
+  }
   const unsigned g1 = static_cast<unsigned>((M / kBM) * (F / kBN));
   ffn_gemm_kernel<kEpiGelu><<<dim3(g1), dim3(kThreads), 0, stream>>>(x, rstd, w1, nullptr, h, M,
                                                                     F, D);

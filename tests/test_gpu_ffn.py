@@ -50,18 +50,24 @@ def test_transpose_is_exact(gpu, shape):
     assert torch.equal(dst.cpu(), src.t().contiguous())
 
 
+# The first four take the 128-tile kernels; the last three the 256-tile
+# direct-to-LDS kernels (every dimension a multiple of 256 and each GEMM's
+# tile count a multiple of 8).
 @pytest.mark.parametrize("rows,d,f", [(128, 128, 128), (128, 256, 384), (256, 128, 512),
-                                      (384, 512, 256)])
+                                      (384, 512, 256), (512, 1024, 1024), (256, 2048, 2048),
+                                      (1024, 512, 4096)])
 def test_ffn_small_shapes(gpu, rows, d, f):
     print(f"ffn rows={rows} d={d} f={f}", flush=True)
     x, w1, w2 = make(rows, d, f, seed=rows + d + f)
     np.testing.assert_allclose(run_ffn(x, w1, w2, gpu), oracle(x, w1, w2), **BF16)
 
 
-def test_ffn_structured_inputs_pin_layout(gpu):
+@pytest.mark.parametrize("rows,d", [(128, 256), (2048, 256)])
+def test_ffn_structured_inputs_pin_layout(gpu, rows, d):
     """Identity-like weights make each output element depend on one input
-    element, so any transposed or shifted fragment mapping fails."""
-    rows, d = 128, 256
+    element, so any transposed or shifted fragment mapping (or a wrong LDS
+    swizzle / direct-to-LDS lane placement) fails.  (2048, 256) takes the
+    256-tile kernels."""
     f = d
     x = (torch.arange(rows * d, dtype=torch.float32).reshape(rows, d) % 7 - 3).to(torch.bfloat16)
     w1 = torch.eye(d, dtype=torch.bfloat16) * 2

@@ -106,3 +106,11 @@ def test_build_summary_scores_model_like_the_reference():
     assert len(sweep) == 4
     agg = aggregate(summary)
     assert agg["points"] == 2 and 0 <= agg["model_accuracy"] <= 1
+
+
+def test_write_csv_takes_the_union_of_keys(tmp_path):
+    from credit_amd.runner import write_csv
+
+    write_csv(tmp_path / "r.csv", [{"a": 1, "b": 2}, {"a": 3, "error": "x"}])
+    lines = (tmp_path / "r.csv").read_text().splitlines()
+    assert lines[0] == "a,b,error" and lines[2] == "3,,x"
