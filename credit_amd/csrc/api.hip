@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -144,15 +145,27 @@ __global__ void fill_f32_kernel(float* __restrict__ p, float v, int64_t n) {
   if (i < n) p[i] = v;
 }
 
+uint32_t next_split_epoch() {
+  // Epoch 0 is the zero-filled state, so it is never handed out.
+  static std::atomic<uint32_t> epoch{0};
+  uint32_t e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+  if (e == 0) e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+  return e;
+}
+
 int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
-                            int k_values, size_t extra_bytes, SplitWorkspace* out) {
+                            int k_values, int stages, size_t extra_bytes, SplitWorkspace* out) {
+  if (members * k_values > kMaxExchangeValues)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "split of %d members exchanges %d partials per stage (at most %d)", members,
+                     members * k_values, kMaxExchangeValues);
   const size_t slot_bytes =
-      align_up(split_slot_bytes(groups, members, k_values), 256);
+      align_up(split_slot_bytes(groups, members, k_values, stages), 256);
   char* base = nullptr;
   CREDIT_TRY(acquire_workspace(cfg, slot_bytes + extra_bytes, &base));
   out->counters = ws_counters(base);
   out->watchdog = ws_watchdog(base);
-  out->slots = reinterpret_cast<double*>(ws_scratch(base));
+  out->slots = reinterpret_cast<uint64_t*>(ws_scratch(base));
   out->extra = ws_scratch(base) + slot_bytes;
   return CREDIT_OK;
 }

@@ -89,16 +89,21 @@ constexpr int kGroupCounterBase = kDispensers * kDispenserStride;  // first grou
 constexpr int kGroupCounterStride = 16;  // one 64-byte line per group counter
 constexpr int kMaxGroupsPerLaunch =
     (kCounterSlots - kGroupCounterBase) / kGroupCounterStride / kDispensers * kDispensers;
-constexpr int kSlotRing = 4;             // stages a group's partial slots rotate over
 // Groups of a split launch are padded to a multiple of kDispensers (the
 // padding groups exit at once).
 inline int64_t padded_groups(int64_t groups) {
   return (groups + kDispensers - 1) / kDispensers * kDispensers;
 }
-// Bytes of partial slots a split launch of `groups` groups needs.
-inline size_t split_slot_bytes(int64_t groups, int members, int k_values) {
-  return static_cast<size_t>(groups) * kSlotRing * k_values * members * sizeof(double);
+// Partials one exchange stage carries (members * values): one wave polls
+// them, one lane per slot.
+constexpr int kMaxExchangeValues = 64;
+// Bytes of exchange slots a split launch needs: one 64-bit slot per
+// (group, stage, value, member).
+inline size_t split_slot_bytes(int64_t groups, int members, int k_values, int stages) {
+  return static_cast<size_t>(groups) * stages * k_values * members * sizeof(uint64_t);
 }
+// Tag of the next split launch (process-wide counter, never 0).
+uint32_t next_split_epoch();
 int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base);
 
 // Workspace of a ticketed split launch: the counter area, the partial slots
@@ -107,16 +112,16 @@ int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base);
 struct SplitWorkspace {
   uint32_t* counters = nullptr;
   uint32_t* watchdog = nullptr;
-  double* slots = nullptr;
+  uint64_t* slots = nullptr;
   char* extra = nullptr;
 };
-inline size_t split_workspace_bytes(int64_t groups, int members, int k_values,
+inline size_t split_workspace_bytes(int64_t groups, int members, int k_values, int stages,
                                     size_t extra_bytes) {
-  const size_t slots = (split_slot_bytes(groups, members, k_values) + 255) / 256 * 256;
+  const size_t slots = (split_slot_bytes(groups, members, k_values, stages) + 255) / 256 * 256;
   return slots + extra_bytes;
 }
 int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
-                            int k_values, size_t extra_bytes, SplitWorkspace* out);
+                            int k_values, int stages, size_t extra_bytes, SplitWorkspace* out);
 inline uint32_t* ws_watchdog(char* base) { return reinterpret_cast<uint32_t*>(base); }
 inline uint32_t* ws_counters(char* base) {
   return reinterpret_cast<uint32_t*>(base + kWorkspaceHeader);

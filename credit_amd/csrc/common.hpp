@@ -166,6 +166,9 @@ __device__ __forceinline__ f32x4 load_nt(const f32x4* p) {
 __device__ __forceinline__ u32x4 load_nt(const u32x4* p) {
   return __builtin_nontemporal_load(p);
 }
+__device__ __forceinline__ f64x2 load_nt(const f64x2* p) {
+  return __builtin_nontemporal_load(p);
+}
 __device__ __forceinline__ void store_nt(f32x4* p, f32x4 v) {
   __builtin_nontemporal_store(v, p);
 }
@@ -228,7 +231,7 @@ __device__ __forceinline__ uint32_t counter_read(const uint32_t* counter) {
 
 // ------------------------------------------------ ticketed split groups ---
 // P workgroups ("members") that share a row -- or a block of rows -- form a
-// group and meet at arrival barriers to combine their partial results.
+// group and exchange partial results to combine them.
 //
 // Membership comes from a ticket, not from blockIdx.  The grid is split into
 // kDispensers subsets by blockIdx % kDispensers, each with its own
@@ -244,49 +247,59 @@ __device__ __forceinline__ uint32_t counter_read(const uint32_t* counter) {
 // launch is thus deadlock-free whenever the device holds kDispensers * P
 // workgroups at once: no cooperative launch (which costs ~30 us on gfx950)
 // and no co-residency of the whole grid is needed.  One dispenser per subset
-// keeps the same-address atomics off a single serialisation point (one
-// shared dispenser costs ~12 ns per workgroup of the grid), and with
+// keeps the same-address atomics off a single serialisation point, and with
 // workgroups dealt to the 8 XCDs round-robin a subset -- so a group -- sits
-// on one XCD.
+// on one XCD.  The workgroup that draws a subset's last ticket returns that
+// dispenser to zero.
 //
-// Barrier protocol, per group, on one device-scope counter:
-//  - stage j (j = 0, 1, ...): each member stores its partials into ring slot
-//    j % kSlotRing with device-scope stores, waits for them to complete
-//    (s_waitcnt vmcnt(0)), then adds 1 to the counter; it proceeds once the
-//    counter reaches P * (j + 1).  The counter only grows inside a launch.
-//  - a member reads stage j's partials right after its wait and before it
-//    arrives at stage j + 1, so nobody can overwrite slot j % kSlotRing
-//    (at stage j + kSlotRing) before every member has read it.
-//  - after its last stage a member adds 1 more ("departs"); the member that
-//    departs last returns the counter to zero.  Each dispenser is returned
-//    to zero by the workgroup that draws its subset's last ticket.  A
-//    zero-filled counter area therefore stays zero between launches.
-// Partials are combined by every member in member order, so all members
-// (and every run) get bit-identical results.  The spin is bounded: on
+// Exchange protocol: tagged slots, no counters.  Every (group, stage, value
+// k, member) has its own 64-bit slot: the partial's fp32 bits in the low
+// word and the launch's epoch (a host counter, different for every split
+// launch) in the high word, written by ONE device-scope atomic store.  So a
+// publisher never waits for anything (no fence, no vmcnt drain of its own
+// loads and stores), and a reader that sees the epoch in a slot sees that
+// launch's value.  Stage s of a group only ever uses its own slots, so no
+// slot is rewritten within a launch.  One wave of each member polls the
+// group's P*K slots of the stage (contiguous: one request per poll) until
+// every tag matches, puts the values in LDS, and after a barrier every
+// thread combines them in member order: all members, and every run, get
+// bit-identical results.  Partials travel as fp32 (the block reductions
+// before them are fp64); the combination is fp64.  The poll is bounded: on
 // expiry it raises *watchdog and continues, so a broken launch ends with a
 // reported error instead of a hung GPU.
 constexpr uint32_t kSpinLimit = 1u << 21;  // ~1 s of s_sleep polling
+constexpr int kMaxExchange = kMaxExchangeValues;  // members * values per stage
+static_assert(kMaxExchange <= kWave, "one wave polls a stage's slots");
+
+// Split-launch arguments, passed by value to every split kernel.
+struct SplitArgs {
+  uint32_t* counters;  // workspace counter area (dispensers)
+  uint64_t* slots;     // workspace slots, [group][stage][k][member]
+  uint32_t* watchdog;
+  uint32_t grid;       // gridDim.x, a multiple of kDispensers * members
+  uint32_t epoch;      // tag of this launch, never 0
+  int stages;          // exchange stages per group
+};
 
 struct SplitGroup {
   int group;
   int member;
   int members;
-  uint32_t* count;
-  double* slots;    // this group's slots: [kSlotRing][K][members]
-  int k_values;     // K: partials per member per stage
-  uint32_t stage;
+  int k_values;
+  int stage;
+  uint32_t epoch;
+  uint64_t* slots;    // this group's slots
+  uint32_t* watchdog;
 };
 
 // Draw a ticket and derive (group, member).  Every thread calls it; it
-// contains one __syncthreads.  grid = gridDim.x, a multiple of
-// kDispensers * members.
-__device__ __forceinline__ SplitGroup split_join(uint32_t* counters, double* scratch,
-                                                 int members, int k_values, uint32_t grid) {
+// contains one __syncthreads.
+__device__ __forceinline__ SplitGroup split_join(const SplitArgs& a, int members, int k_values) {
   __shared__ uint32_t ticket_s;
   const uint32_t subset = blockIdx.x % kDispensers;
-  const uint32_t per_subset = grid / kDispensers;
+  const uint32_t per_subset = a.grid / kDispensers;
   if (threadIdx.x == 0) {
-    uint32_t* dispenser = counters + subset * kDispenserStride;
+    uint32_t* dispenser = a.counters + subset * kDispenserStride;
     const uint32_t t = __hip_atomic_fetch_add(dispenser, 1u, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
     if (t == per_subset - 1) counter_reset(dispenser);
@@ -299,65 +312,72 @@ __device__ __forceinline__ SplitGroup split_join(uint32_t* counters, double* scr
   g.group = static_cast<int>(subset * (per_subset / p) + t / p);
   g.member = static_cast<int>(t % p);
   g.members = members;
-  g.count = counters + kGroupCounterBase + g.group * kGroupCounterStride;
   g.k_values = k_values;
-  g.slots = scratch + static_cast<size_t>(g.group) * kSlotRing * k_values * members;
   g.stage = 0;
+  g.epoch = a.epoch;
+  g.slots = a.slots + static_cast<size_t>(g.group) * a.stages * k_values * members;
+  g.watchdog = a.watchdog;
   return g;
 }
 
-__device__ __forceinline__ double* split_slot(const SplitGroup& g, int k, int m) {
-  return g.slots + (static_cast<int>(g.stage % kSlotRing) * g.k_values + k) * g.members + m;
-}
-
-// Thread 0 only: store this member's k-th partial of the current stage.
+// Thread 0 only: publish this member's k-th partial of the current stage.
 __device__ __forceinline__ void split_publish(const SplitGroup& g, int k, double v) {
-  publish(split_slot(g, k, g.member), v);
+  const uint64_t word = (static_cast<uint64_t>(g.epoch) << 32) |
+                        __builtin_bit_cast(uint32_t, static_cast<float>(v));
+  uint64_t* slot = g.slots + (static_cast<size_t>(g.stage) * g.k_values + k) * g.members + g.member;
+  __hip_atomic_store(slot, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Every thread: arrive at the current stage's barrier and wait for all
-// members.  Afterwards split_get() reads the stage's partials.
-__device__ __forceinline__ void split_arrive_wait(SplitGroup& g, uint32_t* watchdog) {
-  if (threadIdx.x == 0) {
-    publish_wait();
-    const uint32_t target = static_cast<uint32_t>(g.members) * (g.stage + 1);
-    uint32_t v = arrive(g.count) + 1;
+// LDS copy of the current stage's partials, double-buffered by stage parity
+// (each exchange ends with a barrier, so no wave is two exchanges behind).
+__device__ __forceinline__ float* split_lds(int stage) {
+  __shared__ float xch[2][kMaxExchange];
+  return xch[stage & 1];
+}
+
+// Every thread: wait for all members' partials of the current stage and
+// make them readable through split_get / split_sum; advances the stage.
+// `values` (default: the group's k_values) is how many partials per member
+// this stage publishes: values 0..values-1.  Contains one __syncthreads.
+__device__ __forceinline__ void split_exchange(SplitGroup& g, int values = 0) {
+  float* xch = split_lds(g.stage);
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    const int n = g.members * (values > 0 ? values : g.k_values);
+    const uint64_t* base = g.slots + static_cast<size_t>(g.stage) * g.k_values * g.members;
+    uint64_t word = 0;
     uint32_t spins = 0;
-    while (v < target) {
-      __builtin_amdgcn_s_sleep(1);
-      v = counter_read(g.count);
+    for (;;) {
+      bool ok = true;
+      if (lane < n) {
+        word = __hip_atomic_load(base + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = static_cast<uint32_t>(word >> 32) == g.epoch;
+      }
+      if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
       if (++spins > kSpinLimit) {
-        __hip_atomic_store(watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0)
+          __hip_atomic_store(g.watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
+      __builtin_amdgcn_s_sleep(1);
     }
+    if (lane < n) xch[lane] = __builtin_bit_cast(float, static_cast<uint32_t>(word));
   }
   __syncthreads();
+  g.stage += 1;
 }
 
+// After split_exchange: member m's k-th partial of the stage just completed.
 __device__ __forceinline__ double split_get(const SplitGroup& g, int k, int m) {
-  return fetch(split_slot(g, k, m));
+  return static_cast<double>(split_lds(g.stage - 1)[k * g.members + m]);
 }
 
-// Every thread, after the stage's partials have been read.
-__device__ __forceinline__ void split_next(SplitGroup& g) { g.stage += 1; }
-
-// Thread 0 of every member after its last stage: depart; the last member to
-// depart returns the counter to zero.
-__device__ __forceinline__ void split_leave(const SplitGroup& g) {
-  if (threadIdx.x == 0) {
-    const uint32_t final_count = static_cast<uint32_t>(g.members) * (g.stage + 1);
-    if (arrive(g.count) == final_count - 1) counter_reset(g.count);
-  }
-}
-
-// Sum of the current stage's k-th partials in member order.
+// Sum of the completed stage's k-th partials in member order.
 __device__ __forceinline__ double split_sum(const SplitGroup& g, int k) {
   double s = 0.0;
   for (int m = 0; m < g.members; ++m) s += split_get(g, k, m);
   return s;
 }
-
 
 // e^x through the hardware base-2 exponential (v_exp_f32).  The product
 // x*log2(e) is formed as t + e with an FMA-recovered residual (Dekker's exact

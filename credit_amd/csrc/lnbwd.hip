@@ -68,9 +68,7 @@ __device__ __forceinline__ RowStats stats_from(double s1, double s2, float x0, i
 template <class T, int THREADS, int VPT>
 __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
     const T* __restrict__ x, const T* __restrict__ dy, const T* __restrict__ gamma,
-    T* __restrict__ dx, int cols, int chunk, int members, int rows, float eps,
-    uint32_t* __restrict__ counters, double* __restrict__ slots, uint32_t total,
-    uint32_t* __restrict__ watchdog) {
+    T* __restrict__ dx, int cols, int chunk, int members, int rows, float eps, SplitArgs sa) {
   using V = Vec<T>;
   using raw = typename V::raw;
   constexpr int NW = THREADS / kWave;
@@ -80,7 +78,7 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
   SplitGroup g;
   int row = blockIdx.x, member = 0;
   if (members > 1) {
-    g = split_join(counters, slots, members, 2, total);
+    g = split_join(sa, members, 2);
     row = g.group;
     member = g.member;
     if (row >= rows) return;  // padding group
@@ -120,10 +118,9 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
       split_publish(g, 0, s1);
       split_publish(g, 1, s2);
     }
-    split_arrive_wait(g, watchdog);
+    split_exchange(g);
     s1 = split_sum(g, 0);
     s2 = split_sum(g, 1);
-    split_next(g);
   }
   const RowStats st = stats_from(s1, s2, x0, cols, eps);
   float b1 = 0.0f, b2 = 0.0f;
@@ -147,11 +144,9 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
       split_publish(g, 0, t1);
       split_publish(g, 1, t2);
     }
-    split_arrive_wait(g, watchdog);
+    split_exchange(g);
     t1 = split_sum(g, 0);
     t2 = split_sum(g, 1);
-    split_next(g);
-    split_leave(g);
   }
   const float mg = static_cast<float>(t1 / cols);
   const float mgx = static_cast<float>(t2 / cols);
@@ -211,7 +206,7 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_read_kernel(
 
 template <class T>
 using SliceFn = void (*)(const T*, const T*, const T*, T*, int, int, int, int, float,
-                         uint32_t*, double*, uint32_t, uint32_t*);
+                         SplitArgs);
 
 template <class T>
 struct Pick {
@@ -330,19 +325,19 @@ int layernorm_bwd(const T* x, const T* dy, const T* gamma, T* dx, int64_t rows, 
   if (plan.members == 1) {
     hipLaunchKernelGGL(pk->fn, dim3(static_cast<unsigned>(rows)), dim3(pk->threads), 0, stream,
                        x, dy, gamma, dx, c, static_cast<int>(plan.chunk), 1,
-                       static_cast<int>(rows), eps, nullptr, nullptr, 0u, nullptr);
+                       static_cast<int>(rows), eps, SplitArgs{});
     return check_launch("layernorm_bwd_slice_kernel");
   }
   const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
   SplitWorkspace ws;
-  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(groups), plan.members, 2, 0, &ws));
+  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(groups), plan.members, 2, 2, 0, &ws));
   for (int64_t r0 = 0; r0 < rows; r0 += groups) {
     const int64_t n = rows - r0 < groups ? rows - r0 : groups;
     const uint32_t total = static_cast<uint32_t>(padded_groups(n) * plan.members);
     hipLaunchKernelGGL(pk->fn, dim3(total), dim3(pk->threads), 0, stream, x + r0 * cols,
                        dy + r0 * cols, gamma, dx + r0 * cols, c, static_cast<int>(plan.chunk),
-                       plan.members, static_cast<int>(n), eps, ws.counters, ws.slots, total,
-                       ws.watchdog);
+                       plan.members, static_cast<int>(n), eps,
+                       SplitArgs{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(), 2});
     CREDIT_TRY(check_launch("layernorm_bwd_slice_kernel(split)"));
   }
   return CREDIT_OK;
@@ -358,7 +353,7 @@ size_t layernorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int spli
   const int64_t cap = elem_bytes == 4 ? Slices<float>::capacity : Slices<uint16_t>::capacity;
   if (resolve(&c, cols / e, cols % e == 0, cap, &p) != CREDIT_OK || p.members <= 1) return 0;
   const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
-  return split_workspace_bytes(padded_groups(groups), p.members, 2, 0);
+  return split_workspace_bytes(padded_groups(groups), p.members, 2, 2, 0);
 }
 
 }  // namespace credit

@@ -174,20 +174,17 @@ __global__ void mb_pingpong_kernel(uint32_t* flag, int peer, int rounds, uint64_
 // `groups` ticketed groups of `members` workgroups; each group meets at
 // `barriers` split barriers in a row (publish, arrive, wait, read the
 // partials): the un-overlapped cost of the exchange the split kernels use.
-__global__ __launch_bounds__(256) void mb_barrier_kernel(uint32_t* counters, double* slots,
-                                                         int members, int barriers,
-                                                         uint32_t* watchdog, uint32_t total,
-                                                         int groups, double* sink) {
-  SplitGroup g = split_join(counters, slots, members, 1, total);
+__global__ __launch_bounds__(256) void mb_barrier_kernel(SplitArgs sa, int members,
+                                                         int barriers, int groups,
+                                                         double* sink) {
+  SplitGroup g = split_join(sa, members, 1);
   if (g.group >= groups) return;  // padding group
   double acc = 0.0;
   for (int k = 0; k < barriers; ++k) {
     if (threadIdx.x == 0) split_publish(g, 0, static_cast<double>(g.member + k));
-    split_arrive_wait(g, watchdog);
+    split_exchange(g);
     acc += split_sum(g, 0);
-    split_next(g);
   }
-  split_leave(g);
   if (acc == -1.0 && threadIdx.x == 0) sink[0] = acc;  // keeps the reads alive
 }
 
@@ -409,12 +406,13 @@ int control_overhead(int64_t rows, int split, int barriers, int warmup, int iter
   if (groups < 1) return set_error(CREDIT_ERR_UNSUPPORTED, "split %d does not fit", split);
   const int64_t grid_groups = padded_groups(groups);
   DevBuf ws, sink;
-  CREDIT_TRY(ws.alloc(kScratchOffset + split_slot_bytes(grid_groups, split, 1)));
+  const int stages = barriers > 0 ? barriers : 1;
+  CREDIT_TRY(ws.alloc(kScratchOffset + split_slot_bytes(grid_groups, split, 1, stages)));
   CREDIT_TRY(sink.alloc(256));
   char* base = static_cast<char*>(ws.p);
   uint32_t* counters = ws_counters(base);
   uint32_t* watchdog = ws_watchdog(base);
-  double* slots = reinterpret_cast<double*>(ws_scratch(base));
+  uint64_t* slots = reinterpret_cast<uint64_t*>(ws_scratch(base));
   double* sinkp = static_cast<double*>(sink.p);
   const unsigned grid = static_cast<unsigned>(grid_groups * split);
   uint32_t total = grid;
@@ -425,14 +423,14 @@ int control_overhead(int64_t rows, int split, int barriers, int warmup, int iter
   };
   int members = split;
   auto timed = [&](int) -> int {
+    SplitArgs sa{counters, slots, watchdog, total, next_split_epoch(), stages};
     if (cooperative) {
-      void* args[] = {&counters, &slots, &members, &barriers, &watchdog, &total, &valid, &sinkp};
+      void* args[] = {&sa, &members, &barriers, &valid, &sinkp};
       CREDIT_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mb_barrier_kernel),
                                             dim3(grid), dim3(256), args, 0, nullptr));
       return CREDIT_OK;
     }
-    mb_barrier_kernel<<<grid, 256>>>(counters, slots, members, barriers, watchdog, total, valid,
-                                     sinkp);
+    mb_barrier_kernel<<<grid, 256>>>(sa, members, barriers, valid, sinkp);
     return check_launch("mb_barrier_kernel");
   };
   CREDIT_TRY(time_ms(plain, warmup, iters, plain_ms));

@@ -81,15 +81,14 @@ template <int THREADS, int VPT>
 __global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     uint16_t* __restrict__ y, float* __restrict__ rstd_out, int cols, int chunk,
-    int members, int rows, float eps, uint32_t* __restrict__ counters,
-    double* __restrict__ slots, uint32_t total_workgroups, uint32_t* __restrict__ watchdog) {
+    int members, int rows, float eps, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
   __shared__ double red[NW];
   const int tid = threadIdx.x;
   SplitGroup g;
   int row = blockIdx.x, member = 0;
   if (members > 1) {
-    g = split_join(counters, slots, members, 1, total_workgroups);
+    g = split_join(sa, members, 1);
     row = g.group;
     member = g.member;
     if (row >= rows) return;  // padding group
@@ -110,10 +109,8 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
   double total = block_reduce_sum_f64<NW>(static_cast<double>(ss), red);
   if (members > 1) {
     if (tid == 0) split_publish(g, 0, total);
-    split_arrive_wait(g, watchdog);
+    split_exchange(g);
     total = split_sum(g, 0);
-    split_next(g);
-    split_leave(g);
   }
   const float rs = static_cast<float>(1.0 / __builtin_sqrt(total / cols + eps));
   const u32x4* wr = reinterpret_cast<const u32x4*>(w) + v0;
@@ -187,23 +184,29 @@ constexpr int kBwdWhole = 1;     // members == 1: the member holds the whole row
 constexpr int kBwdGiven = 2;     // c precomputed in rowdot[] (READ variant)
 
 // Member `member` of group `group` covers rows [group*R, group*R + R) and
-// vectors [member*chunk, ...) of each.  Registers per lane: VPT dwordx4 of x
-// and of dy, 8*VPT fp64 dw accumulators.
+// vectors [member*chunk, ...) of each.  Per lane: VPT dwordx4 of x and of dy
+// for the current row plus the same for the next row, whose loads are
+// issued before the current row's reduction and exchange wait, so HBM
+// traffic continues through them.  The dw accumulators (8*VPT fp64 per
+// lane) live in LDS, laid out [slot][lane] so each lane's read-add-write
+// touches consecutive banks; that keeps VGPRs low enough for two
+// workgroups per CU.
 template <int THREADS, int VPT>
 __global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ dy, const float* __restrict__ rstd,
     const float* __restrict__ rowdot, uint16_t* __restrict__ dx,
     double* __restrict__ dw_part, int rows, int cols, int chunk, int members,
-    int rows_per_group, int mode, uint32_t* __restrict__ counters,
-    double* __restrict__ slots, uint32_t total_workgroups, uint32_t* __restrict__ watchdog) {
+    int rows_per_group, int mode, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
+  constexpr int kSlots = 8 * VPT;
+  extern __shared__ double dw_lds[];  // [kSlots][THREADS]
   __shared__ double red[2][NW];
   const int tid = threadIdx.x;
   SplitGroup g;
   int group, member;
   if (mode == kBwdExchange) {
-    g = split_join(counters, slots, members, 1, total_workgroups);
+    g = split_join(sa, members, 1);
     group = g.group;
     member = g.member;
     if (group * rows_per_group >= rows) return;  // padding group
@@ -217,24 +220,25 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
   const int r0 = group * rows_per_group;
   const int r1 = r0 + rows_per_group < rows ? r0 + rows_per_group : rows;
   const u32x4* wr = reinterpret_cast<const u32x4*>(w) + v0;
-  double acc[VPT][8];
 #pragma unroll
-  for (int k = 0; k < VPT; ++k)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[k][e] = 0.0;
+  for (int q = 0; q < kSlots; ++q) dw_lds[q * THREADS + tid] = 0.0;
 
-  for (int r = r0; r < r1; ++r) {
+  u32x4 xv[VPT], dv[VPT], xn[VPT], dn[VPT];
+  auto load_row = [&](u32x4 (&xa)[VPT], u32x4 (&da)[VPT], int r) {
     const size_t off = static_cast<size_t>(r) * cols;
     const u32x4* xr = reinterpret_cast<const u32x4*>(x + off) + v0;
     const u32x4* dyr = reinterpret_cast<const u32x4*>(dy + off) + v0;
-    u32x4 xv[VPT], dv[VPT];
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       const int idx = tid + k * THREADS;
       const bool in = idx < vlen;
-      xv[k] = in ? load_nt(xr + idx) : u32x4{0, 0, 0, 0};
-      dv[k] = in ? load_nt(dyr + idx) : u32x4{0, 0, 0, 0};
+      xa[k] = in ? load_nt(xr + idx) : u32x4{0, 0, 0, 0};
+      da[k] = in ? load_nt(dyr + idx) : u32x4{0, 0, 0, 0};
     }
+  };
+  load_row(xv, dv, r0);
+  for (int r = r0; r < r1; ++r) {
+    if (r + 1 < r1) load_row(xn, dn, r + 1);
     const float rs = rstd[r];
     double dot;
     if (mode == kBwdGiven) {
@@ -249,28 +253,34 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
       dot = block_reduce_sum_f64<NW>(static_cast<double>(part), red[r & 1]);
       if (mode == kBwdExchange) {
         if (tid == 0) split_publish(g, 0, dot);
-        split_arrive_wait(g, watchdog);
+        split_exchange(g);
         dot = split_sum(g, 0);
-        split_next(g);
       }
     }
     // c = mean(g * xhat) = rs * sum(dy*w*x) / cols
     const float c = static_cast<float>(dot * rs / cols);
-    u32x4* dxr = reinterpret_cast<u32x4*>(dx + off) + v0;
     const double rsd = static_cast<double>(rs);
+    u32x4* dxr = reinterpret_cast<u32x4*>(dx + static_cast<size_t>(r) * cols) + v0;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       const int idx = tid + k * THREADS;
-      if (idx < vlen) store_nt(dxr + idx, dx8(xv[k], dv[k], wr[idx], rs, c));
+      if (idx < vlen) {
+        store_nt(dxr + idx, dx8(xv[k], dv[k], wr[idx], rs, c));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        // dy*x is exact in fp32 (bf16 x bf16); times rstd it is exact in fp64.
-        acc[k][2 * i] += static_cast<double>(bf16_lo(dv[k][i]) * bf16_lo(xv[k][i])) * rsd;
-        acc[k][2 * i + 1] += static_cast<double>(bf16_hi(dv[k][i]) * bf16_hi(xv[k][i])) * rsd;
+        for (int i = 0; i < 4; ++i) {
+          // dy*x is exact in fp32 (bf16 x bf16); times rstd it is exact in fp64.
+          double* a = dw_lds + (k * 8 + 2 * i) * THREADS + tid;
+          a[0] += static_cast<double>(bf16_lo(dv[k][i]) * bf16_lo(xv[k][i])) * rsd;
+          a[THREADS] += static_cast<double>(bf16_hi(dv[k][i]) * bf16_hi(xv[k][i])) * rsd;
+        }
       }
     }
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      xv[k] = xn[k];
+      dv[k] = dn[k];
+    }
   }
-  if (mode == kBwdExchange) split_leave(g);
   // One fp64 partial row per block: rounding the block sums to fp32 here
   // would add ~ulp(block sum) per block to dw.
   double* pr = dw_part + static_cast<size_t>(group) * cols + 8 * static_cast<size_t>(v0);
@@ -279,10 +289,11 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
     const int idx = tid + k * THREADS;
     if (idx < vlen) {
       f64x2* q = reinterpret_cast<f64x2*>(pr + 8 * static_cast<size_t>(idx));
-      q[0] = f64x2{acc[k][0], acc[k][1]};
-      q[1] = f64x2{acc[k][2], acc[k][3]};
-      q[2] = f64x2{acc[k][4], acc[k][5]};
-      q[3] = f64x2{acc[k][6], acc[k][7]};
+      const double* a = dw_lds + k * 8 * THREADS + tid;
+      q[0] = f64x2{a[0], a[THREADS]};
+      q[1] = f64x2{a[2 * THREADS], a[3 * THREADS]};
+      q[2] = f64x2{a[4 * THREADS], a[5 * THREADS]};
+      q[3] = f64x2{a[6 * THREADS], a[7 * THREADS]};
     }
   }
 }
@@ -320,8 +331,9 @@ __global__ __launch_bounds__(256) void rmsnorm_dw_reduce_kernel(
   if (q >= nq) return;
   const f64x2* p = reinterpret_cast<const f64x2*>(part) + q;
   double a0 = 0.0, a1 = 0.0;
+#pragma unroll 8
   for (int b = 0; b < blocks; ++b) {
-    const f64x2 v = p[static_cast<size_t>(b) * nq];
+    const f64x2 v = load_nt(p + static_cast<size_t>(b) * nq);
     a0 += v.x;
     a1 += v.y;
   }
@@ -330,10 +342,10 @@ __global__ __launch_bounds__(256) void rmsnorm_dw_reduce_kernel(
 
 // ------------------------------------------------------------ dispatch ---
 using FwdSliceFn = void (*)(const uint16_t*, const uint16_t*, uint16_t*, float*, int, int,
-                            int, int, float, uint32_t*, double*, uint32_t, uint32_t*);
+                            int, int, float, SplitArgs);
 using BwdSliceFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, const float*,
                             const float*, uint16_t*, double*, int, int, int, int, int, int,
-                            uint32_t*, double*, uint32_t, uint32_t*);
+                            SplitArgs);
 
 struct FwdPick {
   FwdSliceFn fn;
@@ -344,6 +356,7 @@ struct BwdPick {
   BwdSliceFn fn;
   int threads;
   int capacity;
+  int lds_bytes() const { return capacity * 8 * static_cast<int>(sizeof(double)); }
 };
 
 // Smallest footprint first.  VPT stays at 4-8 dwordx4 per lane: deeper
@@ -357,16 +370,17 @@ const FwdPick kFwd[] = {
     {rmsnorm_fwd_slice_kernel<512, 8>, 512, 4096},
     {rmsnorm_fwd_slice_kernel<1024, 8>, 1024, 8192},
 };
-// fp64 dw accumulators cost 16 VGPRs per dwordx4 held, so the backward
-// holds at most 4 per lane (VPT 4) in workgroups of up to 512 lanes.
+// Two row buffers of x and dy at VPT = 2 per lane; the fp64 dw accumulators
+// take 16 * VPT * 8 bytes of LDS per lane (64 KiB at 512 lanes), so two
+// workgroups share a CU.
 const BwdPick kBwd[] = {
-    {rmsnorm_bwd_slice_kernel<64, 4>, 64, 256},
-    {rmsnorm_bwd_slice_kernel<128, 4>, 128, 512},
-    {rmsnorm_bwd_slice_kernel<256, 4>, 256, 1024},
-    {rmsnorm_bwd_slice_kernel<512, 4>, 512, 2048},
+    {rmsnorm_bwd_slice_kernel<64, 2>, 64, 128},
+    {rmsnorm_bwd_slice_kernel<128, 2>, 128, 256},
+    {rmsnorm_bwd_slice_kernel<256, 2>, 256, 512},
+    {rmsnorm_bwd_slice_kernel<512, 2>, 512, 1024},
 };
 constexpr int kFwdMaxCapacity = 8192;
-constexpr int kBwdMaxCapacity = 2048;
+constexpr int kBwdMaxCapacity = 1024;
 
 template <class Pick, int N>
 const Pick* pick_for(const Pick (&table)[N], int64_t chunk) {
@@ -442,7 +456,7 @@ struct BwdPlan {
 
 int rows_per_group_for(int64_t rows, int members, int cu_count) {
   // Aim for about two workgroups per CU in total; more rows per group cut
-  // the dw partial traffic (one fp32 row per group).
+  // the dw partial traffic (one fp64 row per group).
   const int64_t target_groups = (2 * static_cast<int64_t>(cu_count) + members - 1) / members;
   int64_t r = (rows + target_groups - 1) / (target_groups > 0 ? target_groups : 1);
   if (r < 1) r = 1;
@@ -502,7 +516,7 @@ size_t rmsnorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split)
   if (resolve_fwd(&c, cols, cols % 8 == 0, &p) != CREDIT_OK) return 0;
   if (p.variant != CREDIT_VARIANT_SPLIT) return 0;
   const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
-  return split_workspace_bytes(padded_groups(groups), p.members, 1, 0);
+  return split_workspace_bytes(padded_groups(groups), p.members, 1, 1, 0);
 }
 
 size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
@@ -510,7 +524,7 @@ size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
   credit_cfg c{nullptr, variant, split, nullptr, 0};
   BwdPlan p;
   if (resolve_bwd(&c, rows, cols, cols % 8 == 0, cu_count, &p) != CREDIT_OK) return 0;
-  return split_workspace_bytes(padded_groups(p.groups), p.members, 1,
+  return split_workspace_bytes(padded_groups(p.groups), p.members, 1, p.rows_per_group,
                                bwd_extra_bytes(p, rows, cols));
 }
 
@@ -548,18 +562,20 @@ extern "C" int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uin
   if (plan.variant == CREDIT_VARIANT_STAGED) {
     hipLaunchKernelGGL(pick->fn, dim3(static_cast<unsigned>(rows)), dim3(pick->threads), 0,
                        stream, x, w, y, rstd, c, static_cast<int>(plan.chunk), 1,
-                       static_cast<int>(rows), eps, nullptr, nullptr, 0u, nullptr);
+                       static_cast<int>(rows), eps, SplitArgs{});
     return check_launch("rmsnorm_fwd_slice_kernel");
   }
   const int64_t launch_groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
   SplitWorkspace ws;
-  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(launch_groups), plan.members, 1, 0, &ws));
+  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(launch_groups), plan.members, 1, 1, 0,
+                                     &ws));
   for (int64_t r0 = 0; r0 < rows; r0 += launch_groups) {
     const int64_t n = rows - r0 < launch_groups ? rows - r0 : launch_groups;
     const uint32_t total = static_cast<uint32_t>(padded_groups(n) * plan.members);
+    const SplitArgs sa{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(), 1};
     hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), 0, stream, x + r0 * cols, w,
                        y + r0 * cols, rstd + r0, c, static_cast<int>(plan.chunk), plan.members,
-                       static_cast<int>(n), eps, ws.counters, ws.slots, total, ws.watchdog);
+                       static_cast<int>(n), eps, sa);
     CREDIT_TRY(check_launch("rmsnorm_fwd_slice_kernel(split)"));
   }
   return CREDIT_OK;
@@ -597,7 +613,7 @@ extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
                      static_cast<long long>(plan.groups), kMaxGroupsPerLaunch);
   SplitWorkspace ws;
   CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(plan.groups), plan.members, 1,
-                                     bwd_extra_bytes(plan, rows, cols), &ws));
+                                     plan.rows_per_group, bwd_extra_bytes(plan, rows, cols), &ws));
   double* dw_part = reinterpret_cast<double*>(ws.extra);
   float* rowdot = reinterpret_cast<float*>(
       ws.extra + align_up(static_cast<size_t>(plan.groups) * cols * sizeof(double), 256));
@@ -614,10 +630,13 @@ extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
         <<<dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream>>>(x, w, dy, rowdot, c);
     CREDIT_TRY(check_launch("rmsnorm_bwd_rowdot_kernel"));
   }
-  hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), 0, stream, x, w, dy, rstd,
-                     rowdot, dx, dw_part, static_cast<int>(rows), c,
+  if (pick->lds_bytes() > 65536)
+    return set_error(CREDIT_ERR_UNSUPPORTED, "rmsnorm_bwd: slice needs too much LDS");
+  hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), pick->lds_bytes(), stream, x,
+                     w, dy, rstd, rowdot, dx, dw_part, static_cast<int>(rows), c,
                      static_cast<int>(plan.chunk), plan.members, plan.rows_per_group, mode,
-                     ws.counters, ws.slots, total, ws.watchdog);
+                     SplitArgs{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(),
+                               plan.rows_per_group});
   CREDIT_TRY(check_launch("rmsnorm_bwd_slice_kernel"));
   const unsigned reduce_blocks = static_cast<unsigned>((cols / 2 + 255) / 256);
   rmsnorm_dw_reduce_kernel<<<dim3(reduce_blocks), dim3(256), 0, stream>>>(

@@ -103,13 +103,12 @@ struct Slice {
 // Row and slice of this workgroup: ticketed member of a group when
 // members > 1, otherwise row = blockIdx.x holding the whole row.
 __device__ __forceinline__ Slice slice_of(SplitGroup* g, int members, int k_values, int chunk,
-                                          int nvec, uint32_t* counters, double* slots,
-                                          uint32_t total) {
+                                          int nvec, const SplitArgs& sa) {
   // s.row >= rows marks a padding group of a ticketed launch: the caller
   // returns at once.
   Slice s{static_cast<int>(blockIdx.x), 0, 0, 0};
   if (members > 1) {
-    *g = split_join(counters, slots, members, k_values, total);
+    *g = split_join(sa, members, k_values);
     s.row = g->group;
     s.member = g->member;
   }
@@ -122,15 +121,13 @@ __device__ __forceinline__ Slice slice_of(SplitGroup* g, int members, int k_valu
 template <int THREADS, int VPT>
 __global__ __launch_bounds__(THREADS) void softmax_fwd_slice_kernel(
     const float* __restrict__ x, float* __restrict__ p, float* __restrict__ rowmax,
-    float* __restrict__ lse, int cols, int chunk, int members, int rows,
-    uint32_t* __restrict__ counters, double* __restrict__ slots, uint32_t total,
-    uint32_t* __restrict__ watchdog) {
+    float* __restrict__ lse, int cols, int chunk, int members, int rows, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
   __shared__ float mred[NW];
   __shared__ double sred[NW];
   const int tid = threadIdx.x;
   SplitGroup g;
-  const Slice sl = slice_of(&g, members, 2, chunk, cols >> 2, counters, slots, total);
+  const Slice sl = slice_of(&g, members, 2, chunk, cols >> 2, sa);
   if (sl.row >= rows) return;
   const f32x4* xr = reinterpret_cast<const f32x4*>(x + static_cast<size_t>(sl.row) * cols) + sl.v0;
   f32x4 v[VPT];
@@ -156,10 +153,8 @@ __global__ __launch_bounds__(THREADS) void softmax_fwd_slice_kernel(
       split_publish(g, 0, static_cast<double>(wm));
       split_publish(g, 1, ws);
     }
-    split_arrive_wait(g, watchdog);
+    split_exchange(g);
     split_merge_maxsum(g, &m, &s);
-    split_next(g);
-    split_leave(g);
   }
   const float inv_s = static_cast<float>(1.0 / s);
   f32x4* pr = reinterpret_cast<f32x4*>(p + static_cast<size_t>(sl.row) * cols) + sl.v0;
@@ -243,13 +238,12 @@ __global__ __launch_bounds__(THREADS) void softmax_fwd_read_kernel(
 template <int THREADS, int VPT>
 __global__ __launch_bounds__(THREADS) void softmax_bwd_slice_kernel(
     const float* __restrict__ p, const float* __restrict__ dy, float* __restrict__ dx, int cols,
-    int chunk, int members, int rows, uint32_t* __restrict__ counters,
-    double* __restrict__ slots, uint32_t total, uint32_t* __restrict__ watchdog) {
+    int chunk, int members, int rows, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
   __shared__ double sred[NW];
   const int tid = threadIdx.x;
   SplitGroup g;
-  const Slice sl = slice_of(&g, members, 1, chunk, cols >> 2, counters, slots, total);
+  const Slice sl = slice_of(&g, members, 1, chunk, cols >> 2, sa);
   if (sl.row >= rows) return;
   const size_t off = static_cast<size_t>(sl.row) * cols;
   const f32x4* pr = reinterpret_cast<const f32x4*>(p + off) + sl.v0;
@@ -268,10 +262,8 @@ __global__ __launch_bounds__(THREADS) void softmax_bwd_slice_kernel(
   double dot = block_reduce_sum_f64<NW>(static_cast<double>(ld), sred);
   if (members > 1) {
     if (tid == 0) split_publish(g, 0, dot);
-    split_arrive_wait(g, watchdog);
+    split_exchange(g);
     dot = split_sum(g, 0);
-    split_next(g);
-    split_leave(g);
   }
   const float d = static_cast<float>(dot);
   f32x4* xr = reinterpret_cast<f32x4*>(dx + off) + sl.v0;
@@ -330,14 +322,13 @@ __global__ __launch_bounds__(THREADS) void softmax_bwd_read_kernel(
 template <int THREADS, int VPT>
 __global__ __launch_bounds__(THREADS) void softmax_logits_bwd_slice_kernel(
     const float* __restrict__ logits, const float* __restrict__ dy, float* __restrict__ dx,
-    int cols, int chunk, int members, int rows, uint32_t* __restrict__ counters,
-    double* __restrict__ slots, uint32_t total, uint32_t* __restrict__ watchdog) {
+    int cols, int chunk, int members, int rows, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
   __shared__ float mred[NW];
   __shared__ double sred[2][NW];
   const int tid = threadIdx.x;
   SplitGroup g;
-  const Slice sl = slice_of(&g, members, 2, chunk, cols >> 2, counters, slots, total);
+  const Slice sl = slice_of(&g, members, 2, chunk, cols >> 2, sa);
   if (sl.row >= rows) return;
   const size_t off = static_cast<size_t>(sl.row) * cols;
   const f32x4* lr = reinterpret_cast<const f32x4*>(logits + off) + sl.v0;
@@ -367,9 +358,8 @@ __global__ __launch_bounds__(THREADS) void softmax_logits_bwd_slice_kernel(
       split_publish(g, 0, static_cast<double>(wm));
       split_publish(g, 1, ws);
     }
-    split_arrive_wait(g, watchdog);
+    split_exchange(g);
     split_merge_maxsum(g, &m, &s);
-    split_next(g);
   }
   const float inv_s = static_cast<float>(1.0 / s);
   float ld = 0.0f;
@@ -381,10 +371,8 @@ __global__ __launch_bounds__(THREADS) void softmax_logits_bwd_slice_kernel(
   double dot = block_reduce_sum_f64<NW>(static_cast<double>(ld), sred[1]);
   if (members > 1) {
     if (tid == 0) split_publish(g, 0, dot);
-    split_arrive_wait(g, watchdog);
+    split_exchange(g, 1);  // stage 2 carries the dot only
     dot = split_sum(g, 0);
-    split_next(g);
-    split_leave(g);
   }
   const float d = static_cast<float>(dot);
   f32x4* xr = reinterpret_cast<f32x4*>(dx + off) + sl.v0;
@@ -453,10 +441,8 @@ __global__ __launch_bounds__(THREADS) void softmax_logits_bwd_read_kernel(
 }
 
 // ------------------------------------------------------------ dispatch ---
-using FwdFn = void (*)(const float*, float*, float*, float*, int, int, int, int, uint32_t*,
-                       double*, uint32_t, uint32_t*);
-using BwdFn = void (*)(const float*, const float*, float*, int, int, int, int, uint32_t*,
-                       double*, uint32_t, uint32_t*);
+using FwdFn = void (*)(const float*, float*, float*, float*, int, int, int, int, SplitArgs);
+using BwdFn = void (*)(const float*, const float*, float*, int, int, int, int, SplitArgs);
 
 template <class Fn>
 struct Pick {
@@ -558,28 +544,29 @@ constexpr int64_t kBwdCapacity = 8192;
 // (members == 1) or ticketed groups, at most kMaxGroupsPerLaunch per launch.
 template <class Fn, class Launch>
 int launch_slices(const credit_cfg* cfg, int64_t rows, const Plan& plan, int k_values,
-                  const char* name, Launch&& launch) {
+                  int stages, const char* name, Launch&& launch) {
   if (plan.members == 1) {
-    launch(static_cast<unsigned>(rows), int64_t{0}, static_cast<int>(rows), nullptr, nullptr,
-           0u, nullptr);
+    launch(static_cast<unsigned>(rows), int64_t{0}, static_cast<int>(rows), SplitArgs{});
     return check_launch(name);
   }
   const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
   SplitWorkspace ws;
-  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(groups), plan.members, k_values, 0, &ws));
+  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(groups), plan.members, k_values, stages,
+                                     0, &ws));
   for (int64_t r0 = 0; r0 < rows; r0 += groups) {
     const int64_t n = rows - r0 < groups ? rows - r0 : groups;
     const uint32_t total = static_cast<uint32_t>(padded_groups(n) * plan.members);
-    launch(total, r0, static_cast<int>(n), ws.counters, ws.slots, total, ws.watchdog);
+    launch(total, r0, static_cast<int>(n),
+           SplitArgs{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(), stages});
     CREDIT_TRY(check_launch(name));
   }
   return CREDIT_OK;
 }
 
-size_t slice_workspace(int64_t rows, const Plan& p, int k_values) {
+size_t slice_workspace(int64_t rows, const Plan& p, int k_values, int stages) {
   if (p.members <= 1) return 0;
   const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
-  return split_workspace_bytes(padded_groups(groups), p.members, k_values, 0);
+  return split_workspace_bytes(padded_groups(groups), p.members, k_values, stages, 0);
 }
 
 }  // namespace
@@ -590,7 +577,8 @@ size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int sp
   const int64_t cap = op == CREDIT_OP_SOFTMAX_FWD ? kFwdCapacity : kBwdCapacity;
   if (resolve(&c, cols, cols % 4 == 0, cap, "softmax", &p) != CREDIT_OK) return 0;
   const int k = op == CREDIT_OP_SOFTMAX_BWD ? 1 : 2;
-  return slice_workspace(rows, p, k);
+  const int stages = op == CREDIT_OP_SOFTMAX_LOGITS_BWD ? 2 : 1;
+  return slice_workspace(rows, p, k, stages);
 }
 
 }  // namespace credit
@@ -622,13 +610,11 @@ extern "C" int credit_softmax_fwd_f32(const float* x, float* p, float* rowmax, f
   }
   const Pick<FwdFn>* pk = pick_for(kFwd, plan.chunk);
   return launch_slices<FwdFn>(
-      cfg, rows, plan, 2, "softmax_fwd_slice_kernel",
-      [&](unsigned grid, int64_t r0, int n, uint32_t* counters, double* slots, uint32_t total,
-          uint32_t* watchdog) {
+      cfg, rows, plan, 2, 1, "softmax_fwd_slice_kernel",
+      [&](unsigned grid, int64_t r0, int n, const SplitArgs& sa) {
         hipLaunchKernelGGL(pk->fn, dim3(grid), dim3(pk->threads), 0, stream, x + r0 * cols,
                            p + r0 * cols, rowmax + r0, lse + r0, c,
-                           static_cast<int>(plan.chunk), plan.members, n, counters, slots,
-                           total, watchdog);
+                           static_cast<int>(plan.chunk), plan.members, n, sa);
       });
 }
 
@@ -658,12 +644,11 @@ extern "C" int credit_softmax_bwd_f32(const float* p, const float* dy, float* dx
   }
   const Pick<BwdFn>* pk = pick_for(kBwd, plan.chunk);
   return launch_slices<BwdFn>(
-      cfg, rows, plan, 1, "softmax_bwd_slice_kernel",
-      [&](unsigned grid, int64_t r0, int n, uint32_t* counters, double* slots, uint32_t total,
-          uint32_t* watchdog) {
+      cfg, rows, plan, 1, 1, "softmax_bwd_slice_kernel",
+      [&](unsigned grid, int64_t r0, int n, const SplitArgs& sa) {
         hipLaunchKernelGGL(pk->fn, dim3(grid), dim3(pk->threads), 0, stream, p + r0 * cols,
                            dy + r0 * cols, dx + r0 * cols, c, static_cast<int>(plan.chunk),
-                           plan.members, n, counters, slots, total, watchdog);
+                           plan.members, n, sa);
       });
 }
 
@@ -694,12 +679,10 @@ extern "C" int credit_softmax_logits_bwd_f32(const float* logits, const float* d
   }
   const Pick<BwdFn>* pk = pick_for(kLogits, plan.chunk);
   return launch_slices<BwdFn>(
-      cfg, rows, plan, 2, "softmax_logits_bwd_slice_kernel",
-      [&](unsigned grid, int64_t r0, int n, uint32_t* counters, double* slots, uint32_t total,
-          uint32_t* watchdog) {
+      cfg, rows, plan, 2, 2, "softmax_logits_bwd_slice_kernel",
+      [&](unsigned grid, int64_t r0, int n, const SplitArgs& sa) {
         hipLaunchKernelGGL(pk->fn, dim3(grid), dim3(pk->threads), 0, stream,
                            logits + r0 * cols, dy + r0 * cols, dx + r0 * cols, c,
-                           static_cast<int>(plan.chunk), plan.members, n, counters, slots,
-                           total, watchdog);
+                           static_cast<int>(plan.chunk), plan.members, n, sa);
       });
 }

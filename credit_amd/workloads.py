@@ -219,7 +219,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         reread_bytes_per_element=4.0,
         staged_bytes_per_element=4,
         reductions_per_stage=(1,),
-        staged_max_cols=16384,
+        staged_max_cols=8192,
     ),
     "softmax_fwd": WorkloadSpec(
         name="softmax_fwd",

@@ -180,7 +180,7 @@ int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, f
  * dx = rstd*(g - xhat*c) (bf16), dw[j] = sum_r dy[r,j]*xhat[r,j] (fp32,
  * accumulated in fp64, summed over row blocks in a fixed order, so it is
  * deterministic).  Needs cols % 8 == 0 and 16-byte aligned x, w, dy, dx, dw.
- * Variants: STAGED (cols <= 16384), SPLIT (P >= cols/16384 members per row
+ * Variants: STAGED (cols <= 8192), SPLIT (P >= cols/8192 members per row
  * block, one exchange per row), READ (a streaming row-dot pre-pass, then
  * column tiles).  rows == 0 writes dw = 0.  Always uses the workspace (dw
  * partials). */

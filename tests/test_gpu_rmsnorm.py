@@ -139,7 +139,7 @@ def test_rmsnorm_bwd_shapes(gpu, variant, split, shape):
     check_bwd(x, w, dy, r, *bwd(x, w, dy, r, variant, split, gpu))
 
 
-@pytest.mark.parametrize("variant,split", [("auto", 0), ("split", 8), ("split", 16), ("read", 0)])
+@pytest.mark.parametrize("variant,split", [("auto", 0), ("split", 16), ("split", 24), ("read", 0)])
 def test_rmsnorm_bwd_wide_rows(gpu, variant, split):
     x, w, dy = SPEC.make_inputs(20, 131072, seed=43)
     r = oracle_rstd32(x)
@@ -149,7 +149,7 @@ def test_rmsnorm_bwd_wide_rows(gpu, variant, split):
 def test_rmsnorm_bwd_staged_and_short_split_reject_wide_rows(gpu):
     x, w, dy = SPEC.make_inputs(2, 131072, seed=3)
     r = oracle_rstd32(x)
-    for variant, split in [("staged", 0), ("split", 2)]:
+    for variant, split in [("staged", 0), ("split", 2), ("split", 8)]:
         with pytest.raises(hip_lib.CreditError) as err:
             bwd(x, w, dy, r, variant, split, gpu)
         assert err.value.status == -4
