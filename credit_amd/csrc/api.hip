@@ -145,22 +145,28 @@ __global__ void fill_f32_kernel(float* __restrict__ p, float v, int64_t n) {
   if (i < n) p[i] = v;
 }
 
-uint32_t next_split_epoch() {
-  // Epoch 0 is the zero-filled state, so it is never handed out.
-  static std::atomic<uint32_t> epoch{0};
-  uint32_t e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
-  if (e == 0) e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
-  return e;
+uint32_t next_split_epoch(uint32_t stages) {
+  // Tag 0 is the zero-filled state, so no reserved range may contain it.
+  static std::atomic<uint32_t> next{1};
+  if (stages == 0) stages = 1;
+  for (;;) {
+    uint32_t base = next.load(std::memory_order_relaxed);
+    const uint32_t end = base + stages;  // may wrap; [base, 2^32) ending at 0 is fine
+    const bool wraps = base == 0 || (end < base && end != 0);
+    const uint32_t start = wraps ? 1u : base;
+    if (next.compare_exchange_weak(base, start + stages, std::memory_order_relaxed))
+      return start;
+  }
 }
 
 int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
-                            int k_values, int stages, size_t extra_bytes, SplitWorkspace* out) {
+                            int k_values, int ring, size_t extra_bytes, SplitWorkspace* out) {
   if (members * k_values > kMaxExchangeValues)
     return set_error(CREDIT_ERR_UNSUPPORTED,
                      "split of %d members exchanges %d partials per stage (at most %d)", members,
                      members * k_values, kMaxExchangeValues);
   const size_t slot_bytes =
-      align_up(split_slot_bytes(groups, members, k_values, stages), 256);
+      align_up(split_slot_bytes(groups, members, k_values, ring), 256);
   char* base = nullptr;
   CREDIT_TRY(acquire_workspace(cfg, slot_bytes + extra_bytes, &base));
   out->counters = ws_counters(base);

@@ -98,12 +98,13 @@ inline int64_t padded_groups(int64_t groups) {
 // them, one lane per slot.
 constexpr int kMaxExchangeValues = 64;
 // Bytes of exchange slots a split launch needs: one 64-bit slot per
-// (group, stage, value, member).
-inline size_t split_slot_bytes(int64_t groups, int members, int k_values, int stages) {
-  return static_cast<size_t>(groups) * stages * k_values * members * sizeof(uint64_t);
+// (group, slot row, value, member); `ring` slot rows per group.
+inline size_t split_slot_bytes(int64_t groups, int members, int k_values, int ring) {
+  return static_cast<size_t>(groups) * ring * k_values * members * sizeof(uint64_t);
 }
-// Tag of the next split launch (process-wide counter, never 0).
-uint32_t next_split_epoch();
+// Reserve `stages` consecutive exchange tags for one split launch and
+// return the first (a process-wide counter; the range never contains 0).
+uint32_t next_split_epoch(uint32_t stages);
 int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base);
 
 // Workspace of a ticketed split launch: the counter area, the partial slots
@@ -115,13 +116,13 @@ struct SplitWorkspace {
   uint64_t* slots = nullptr;
   char* extra = nullptr;
 };
-inline size_t split_workspace_bytes(int64_t groups, int members, int k_values, int stages,
+inline size_t split_workspace_bytes(int64_t groups, int members, int k_values, int ring,
                                     size_t extra_bytes) {
-  const size_t slots = (split_slot_bytes(groups, members, k_values, stages) + 255) / 256 * 256;
+  const size_t slots = (split_slot_bytes(groups, members, k_values, ring) + 255) / 256 * 256;
   return slots + extra_bytes;
 }
 int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
-                            int k_values, int stages, size_t extra_bytes, SplitWorkspace* out);
+                            int k_values, int ring, size_t extra_bytes, SplitWorkspace* out);
 inline uint32_t* ws_watchdog(char* base) { return reinterpret_cast<uint32_t*>(base); }
 inline uint32_t* ws_counters(char* base) {
   return reinterpret_cast<uint32_t*>(base + kWorkspaceHeader);

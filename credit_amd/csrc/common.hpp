@@ -176,6 +176,38 @@ __device__ __forceinline__ void store_nt(u32x4* p, u32x4 v) {
   __builtin_nontemporal_store(v, p);
 }
 
+// Raw buffer access (gfx9 buffer resource: base, stride 0, num_records
+// bytes, dword3 = DATA_FORMAT 32).  A load beyond num_records returns 0
+// and a store beyond it is dropped, in hardware: bounds and tail conditions
+// fold into the resource (scalar registers) instead of branches, which
+// matters for the waitcnt pass -- a load or store under a branch makes the
+// number of operations in flight path-dependent, and the wait after the
+// join then drains everything (vmcnt(0)).
+constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr int kBufferNt = 2;  // cache-policy operand: nontemporal ("nt")
+using buffer_rsrc_t = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           kBufferRsrcWord3);
+}
+__device__ __forceinline__ u32x4 buffer_load_nt(buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kBufferNt);
+}
+__device__ __forceinline__ u32x4 buffer_load(buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+}
+__device__ __forceinline__ void buffer_store_nt(buffer_rsrc_t r, uint32_t offset, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, offset, 0, kBufferNt);
+}
+__device__ __forceinline__ void buffer_store(buffer_rsrc_t r, uint32_t offset, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, offset, 0, 0);
+}
+
+// *p += v on an LDS double that only this lane updates (ds_add_f64).
+__device__ __forceinline__ void lds_add(double* p, double v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 __global__ void fill_f32_kernel(float* __restrict__ p, float v, int64_t n);
 
 // ------------------------------------- cross-workgroup exchange (L2/MALL) --
@@ -254,15 +286,18 @@ __device__ __forceinline__ uint32_t counter_read(const uint32_t* counter) {
 //
 // Exchange protocol: tagged slots, no counters.  Every (group, stage, value
 // k, member) has its own 64-bit slot: the partial's fp32 bits in the low
-// word and the launch's epoch (a host counter, different for every split
-// launch) in the high word, written by ONE device-scope atomic store.  So a
-// publisher never waits for anything (no fence, no vmcnt drain of its own
-// loads and stores), and a reader that sees the epoch in a slot sees that
-// launch's value.  Stage s of a group only ever uses its own slots, so no
-// slot is rewritten within a launch.  One wave of each member polls the
-// group's P*K slots of the stage (contiguous: one request per poll) until
-// every tag matches, puts the values in LDS, and after a barrier every
-// thread combines them in member order: all members, and every run, get
+// word and a tag in the high word, written by ONE device-scope atomic store.
+// The tag of stage s is epoch + s, where the host reserves a fresh range of
+// tags [epoch, epoch + stages) for every split launch (never containing 0,
+// the zero-filled state), so a publisher never waits for anything (no
+// fence, no vmcnt drain of its own loads and stores), and a reader that sees
+// the tag in a slot sees that launch's value of that stage.  Stages use
+// slot rows modulo `ring`: a kernel whose members run many stages reuses a
+// slot row only once every member has polled it (the kernels guarantee
+// that by their step structure).  One wave of each member polls the group's
+// P*K slots of the stage (contiguous: one request per poll) until every tag
+// matches, puts the values in LDS, and after a barrier every thread
+// combines them in member order: all members, and every run, get
 // bit-identical results.  Partials travel as fp32 (the block reductions
 // before them are fp64); the combination is fp64.  The poll is bounded: on
 // expiry it raises *watchdog and continues, so a broken launch ends with a
@@ -274,11 +309,11 @@ static_assert(kMaxExchange <= kWave, "one wave polls a stage's slots");
 // Split-launch arguments, passed by value to every split kernel.
 struct SplitArgs {
   uint32_t* counters;  // workspace counter area (dispensers)
-  uint64_t* slots;     // workspace slots, [group][stage][k][member]
+  uint64_t* slots;     // workspace slots, [group][stage % ring][k][member]
   uint32_t* watchdog;
   uint32_t grid;       // gridDim.x, a multiple of kDispensers * members
-  uint32_t epoch;      // tag of this launch, never 0
-  int stages;          // exchange stages per group
+  uint32_t epoch;      // tag of stage 0; stage s carries epoch + s
+  int ring;            // slot rows per group (stages modulo ring)
 };
 
 struct SplitGroup {
@@ -287,6 +322,7 @@ struct SplitGroup {
   int members;
   int k_values;
   int stage;
+  int ring;
   uint32_t epoch;
   uint64_t* slots;    // this group's slots
   uint32_t* watchdog;
@@ -306,7 +342,9 @@ __device__ __forceinline__ SplitGroup split_join(const SplitArgs& a, int members
     ticket_s = t;
   }
   __syncthreads();
-  const uint32_t t = ticket_s;
+  // readfirstlane: the ticket is workgroup-uniform, and saying so keeps the
+  // group/member arithmetic (and everything addressed by it) scalar.
+  const uint32_t t = __builtin_amdgcn_readfirstlane(ticket_s);
   const uint32_t p = static_cast<uint32_t>(members);
   SplitGroup g;
   g.group = static_cast<int>(subset * (per_subset / p) + t / p);
@@ -314,18 +352,63 @@ __device__ __forceinline__ SplitGroup split_join(const SplitArgs& a, int members
   g.members = members;
   g.k_values = k_values;
   g.stage = 0;
+  g.ring = a.ring;
   g.epoch = a.epoch;
-  g.slots = a.slots + static_cast<size_t>(g.group) * a.stages * k_values * members;
+  g.slots = a.slots + static_cast<size_t>(g.group) * a.ring * k_values * members;
   g.watchdog = a.watchdog;
   return g;
 }
 
+// One thread: publish this member's k-th partial of exchange stage `stage`.
+__device__ __forceinline__ void split_publish_at(const SplitGroup& g, int stage, int k, double v) {
+  const uint64_t word = (static_cast<uint64_t>(g.epoch + static_cast<uint32_t>(stage)) << 32) |
+                        __builtin_bit_cast(uint32_t, static_cast<float>(v));
+  const int row = stage % g.ring;
+  uint64_t* slot = g.slots + (static_cast<size_t>(row) * g.k_values + k) * g.members + g.member;
+  __hip_atomic_store(slot, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Thread 0 only: publish this member's k-th partial of the current stage.
 __device__ __forceinline__ void split_publish(const SplitGroup& g, int k, double v) {
-  const uint64_t word = (static_cast<uint64_t>(g.epoch) << 32) |
-                        __builtin_bit_cast(uint32_t, static_cast<float>(v));
-  uint64_t* slot = g.slots + (static_cast<size_t>(g.stage) * g.k_values + k) * g.members + g.member;
-  __hip_atomic_store(slot, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  split_publish_at(g, g.stage, k, v);
+}
+
+// One whole wave: wait until partials 0..values-1 of every member at
+// exchange stage `stage` carry this launch's epoch.  Lane k*P + m returns
+// member m's partial k as fp32 bits (0 on lanes beyond values*P).  The
+// poll is bounded: on expiry it raises *watchdog and returns what it has.
+__device__ __forceinline__ uint32_t split_poll(const SplitGroup& g, int stage, int values) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n = g.members * values;
+  const uint64_t* base = g.slots + static_cast<size_t>(stage % g.ring) * g.k_values * g.members;
+  const uint32_t tag = g.epoch + static_cast<uint32_t>(stage);
+  uint64_t word = 0;
+  uint32_t spins = 0;
+  for (;;) {
+    bool ok = true;
+    if (lane < n) {
+      word = __hip_atomic_load(base + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = static_cast<uint32_t>(word >> 32) == tag;
+    }
+    if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+    if (++spins > kSpinLimit) {
+      if (lane == 0)
+        __hip_atomic_store(g.watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return lane < n ? static_cast<uint32_t>(word) : 0u;
+}
+
+// One whole wave, after split_poll: sum of partial k over the members in
+// member order (fp64), the same value in every lane.
+__device__ __forceinline__ double split_wave_sum(uint32_t bits, int members, int k) {
+  double s = 0.0;
+  for (int m = 0; m < members; ++m)
+    s += static_cast<double>(
+        __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, k * members + m)));
+  return s;
 }
 
 // LDS copy of the current stage's partials, double-buffered by stage parity
@@ -342,26 +425,9 @@ __device__ __forceinline__ float* split_lds(int stage) {
 __device__ __forceinline__ void split_exchange(SplitGroup& g, int values = 0) {
   float* xch = split_lds(g.stage);
   if (threadIdx.x < kWave) {
-    const int lane = threadIdx.x;
-    const int n = g.members * (values > 0 ? values : g.k_values);
-    const uint64_t* base = g.slots + static_cast<size_t>(g.stage) * g.k_values * g.members;
-    uint64_t word = 0;
-    uint32_t spins = 0;
-    for (;;) {
-      bool ok = true;
-      if (lane < n) {
-        word = __hip_atomic_load(base + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ok = static_cast<uint32_t>(word >> 32) == g.epoch;
-      }
-      if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
-      if (++spins > kSpinLimit) {
-        if (lane == 0)
-          __hip_atomic_store(g.watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (lane < n) xch[lane] = __builtin_bit_cast(float, static_cast<uint32_t>(word));
+    const int v = values > 0 ? values : g.k_values;
+    const uint32_t bits = split_poll(g, g.stage, v);
+    if (static_cast<int>(threadIdx.x) < g.members * v) xch[threadIdx.x] = __builtin_bit_cast(float, bits);
   }
   __syncthreads();
   g.stage += 1;

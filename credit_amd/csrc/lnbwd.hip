@@ -337,7 +337,7 @@ int layernorm_bwd(const T* x, const T* dy, const T* gamma, T* dx, int64_t rows, 
     hipLaunchKernelGGL(pk->fn, dim3(total), dim3(pk->threads), 0, stream, x + r0 * cols,
                        dy + r0 * cols, gamma, dx + r0 * cols, c, static_cast<int>(plan.chunk),
                        plan.members, static_cast<int>(n), eps,
-                       SplitArgs{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(), 2});
+                       SplitArgs{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(2), 2});
     CREDIT_TRY(check_launch("layernorm_bwd_slice_kernel(split)"));
   }
   return CREDIT_OK;

@@ -423,7 +423,7 @@ int control_overhead(int64_t rows, int split, int barriers, int warmup, int iter
   };
   int members = split;
   auto timed = [&](int) -> int {
-    SplitArgs sa{counters, slots, watchdog, total, next_split_epoch(), stages};
+    SplitArgs sa{counters, slots, watchdog, total, next_split_epoch(stages), stages};
     if (cooperative) {
       void* args[] = {&sa, &members, &barriers, &valid, &sinkp};
       CREDIT_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mb_barrier_kernel),

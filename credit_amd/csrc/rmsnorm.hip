@@ -298,6 +298,190 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
   }
 }
 
+// SPLIT variant.  The workgroup is THREADS data lanes (VPT dwordx4 of x
+// and of dy per lane and row) plus one communication wave.  Member `member`
+// of the group covers rows [group*R, group*R + R) and vectors
+// [member*chunk, member*chunk + THREADS*VPT) of each.
+//
+// No workgroup barrier in the row loop.  In the step of row i each data
+// wave issues the loads of row i+3, reduces row i+2 (loaded a step
+// earlier) to a wave partial in LDS and counts itself in with an LDS
+// atomic; the wave that arrives last sums the partials in wave order and
+// publishes the member's partial of row i+2.  The communication wave runs
+// ahead on its own: it polls each row's exchange, writes the group total
+// into a 4-entry LDS ring and advances an LDS ready count.  A data wave
+// waits (LDS spin) for row i's total, writes dx of row i and folds row i
+// into its dw accumulators.  Row i is published two steps before it is
+// needed, so the exchange round trip (~2000 cycles) overlaps the data
+// waves' work, and no wave waits for another wave's loads.  The ring,
+// partial and counter slots of row k are reused by row k+4 only: a wave
+// reaches the step that rewrites them after row k+3's total is ready,
+// which orders it after every access to them for row k.  Every wait ends:
+// the poll is bounded (watchdog), and the ready count then still advances.
+//
+// The data loop has no branches around its row traffic: every load and
+// store goes through a buffer resource whose num_records covers the
+// member's slice, or 0 for a row beyond the group, so lanes out of range
+// read zeros and drop their stores; the waitcnt pass then waits for row
+// i+2 while row i+3's loads stay in flight (on gfx9 one vmcnt counts loads
+// and stores in order; a load under a branch makes the count
+// path-dependent and the wait after the join a full drain).  dw
+// accumulators: fp64 in LDS, [8*VPT][THREADS], one owner lane each.
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS + kWave)
+__attribute__((amdgpu_waves_per_eu(VPT == 1 ? 4 : 3, 8))) void rmsnorm_bwd_group_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ dy, const float* __restrict__ rstd, uint16_t* __restrict__ dx,
+    double* __restrict__ dw_part, int rows, int cols, int chunk, int members,
+    int rows_per_group, SplitArgs sa) {
+  constexpr int NW = THREADS / kWave;
+  constexpr int kSlots = 8 * VPT;
+  extern __shared__ double dw_lds[];  // [kSlots][THREADS]
+  __shared__ double red[4][NW];       // wave partials of row k at [(k - r0) & 3]
+  __shared__ double ring[4];          // group totals of row k at [(k - r0) & 3]
+  __shared__ uint32_t arrivals[4];
+  __shared__ uint32_t ready;          // rows r0 .. r0 + ready - 1 have totals
+  const int tid = threadIdx.x;
+  if (tid < 4) arrivals[tid] = 0;
+  if (tid == 0) ready = 0;
+  const SplitGroup g = split_join(sa, members, 1);  // its barrier covers the stores above
+  const int r0 = g.group * rows_per_group;
+  if (r0 >= rows) return;  // padding group
+  const int r1 = r0 + rows_per_group < rows ? r0 + rows_per_group : rows;
+  const int nvec = cols >> 3;
+  const int v0 = g.member * chunk;
+  const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  const uint32_t slice_bytes = static_cast<uint32_t>(vlen) * 16u;
+
+  if (__builtin_amdgcn_readfirstlane(tid) >= THREADS) {
+    // ---- communication wave: poll every row's exchange in order ----
+    for (int k = r0; k < r1; ++k) {
+      const uint32_t bits = split_poll(g, k - r0, 1);
+      const double dot = split_wave_sum(bits, members, 0);
+      if (tid == THREADS) {
+        ring[(k - r0) & 3] = dot;
+        __hip_atomic_store(&ready, static_cast<uint32_t>(k - r0 + 1), __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+    return;
+  }
+
+  // ---- data waves ----
+  const int wid = tid / kWave;
+  const bool lead = (tid & (kWave - 1)) == 0;
+  const uint32_t lane_off = static_cast<uint32_t>(tid) * 16u;
+  constexpr uint32_t kStride = THREADS * 16u;  // bytes between a lane's vectors
+  struct Row {
+    u32x4 x[VPT], d[VPT];
+  };
+  Row b0, b1, b2, b3;
+  // Row r's slice, or zeros (no traffic) when r is beyond the group.
+  auto load_row = [&](Row& b, int r) {
+    const bool live = r < r1;
+    const size_t off = static_cast<size_t>(live ? r : r0) * cols + 8 * static_cast<size_t>(v0);
+    const buffer_rsrc_t xs = make_rsrc(x + off, live ? slice_bytes : 0u);
+    const buffer_rsrc_t ds = make_rsrc(dy + off, live ? slice_bytes : 0u);
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      b.x[k] = buffer_load_nt(xs, lane_off + k * kStride);
+      b.d[k] = buffer_load_nt(ds, lane_off + k * kStride);
+    }
+  };
+  // The member's weight slice stays in registers for the whole loop.
+  const buffer_rsrc_t wrs = make_rsrc(w + 8 * static_cast<size_t>(v0), slice_bytes);
+  u32x4 wk[VPT];
+#pragma unroll
+  for (int q = 0; q < VPT; ++q) wk[q] = buffer_load(wrs, lane_off + q * kStride);
+  // Reduce row k to a wave partial; the last wave in publishes the member's.
+  auto publish_row = [&](const Row& b, int k) {
+    float part = 0.0f;
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) part += gx8(b.x[q], b.d[q], wk[q]);
+    const double v = wave_reduce_sum_f64(static_cast<double>(part));
+    const int slot = (k - r0) & 3;
+    if (lead) {
+      red[slot][wid] = v;
+      const uint32_t t = __hip_atomic_fetch_add(&arrivals[slot], 1u, __ATOMIC_ACQ_REL,
+                                                __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (t == NW - 1) {
+        double s = red[slot][0];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) s += red[slot][q];
+        arrivals[slot] = 0;
+        split_publish_at(g, k - r0, 0, s);
+      }
+    }
+  };
+  auto wait_total = [&](int i) {
+    const uint32_t need = static_cast<uint32_t>(i - r0 + 1);
+    while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < need)
+      __builtin_amdgcn_s_sleep(1);
+    return ring[(i - r0) & 3];
+  };
+  const double inv_cols = 1.0 / cols;
+  auto finish_row = [&](const Row& b, int r, double dot) {
+    const float rs = rstd[r];
+    // c = mean(g * xhat) = rs * sum(dy*w*x) / cols
+    const float c = static_cast<float>(dot * (rs * inv_cols));
+    const double rsd = static_cast<double>(rs);
+    const size_t off = static_cast<size_t>(r) * cols + 8 * static_cast<size_t>(v0);
+    const buffer_rsrc_t out = make_rsrc(dx + off, slice_bytes);
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) {
+      buffer_store_nt(out, lane_off + q * kStride, dx8(b.x[q], b.d[q], wk[q], rs, c));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // dy*x is exact in fp32 (bf16 x bf16); times rstd it is exact in
+        // fp64.  Lanes beyond the slice hold zeros and add nothing.  Each
+        // lane owns its accumulators, so the add is an uncontended LDS fp64
+        // atomic (ds_add_f64): no read-back registers, half the LDS
+        // traffic, and the same rounding and order as a read-add-write.
+        double* a = dw_lds + (q * 8 + 2 * i) * THREADS + tid;
+        lds_add(a, static_cast<double>(bf16_lo(b.d[q][i]) * bf16_lo(b.x[q][i])) * rsd);
+        lds_add(a + THREADS, static_cast<double>(bf16_hi(b.d[q][i]) * bf16_hi(b.x[q][i])) * rsd);
+      }
+    }
+  };
+  // Step of row i: cur = row i, r2 = row i+2 (loaded), fut receives row i+3.
+  auto step = [&](Row& cur, Row& r2, Row& fut, int i) {
+    load_row(fut, i + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 2 < r1) publish_row(r2, i + 2);
+    finish_row(cur, i, wait_total(i));
+  };
+
+#pragma unroll
+  for (int q = 0; q < kSlots; ++q) dw_lds[q * THREADS + tid] = 0.0;
+  load_row(b0, r0);
+  load_row(b1, r0 + 1);
+  load_row(b2, r0 + 2);
+  publish_row(b0, r0);
+  if (r0 + 1 < r1) publish_row(b1, r0 + 1);
+  // Rotate the four buffers through statically named registers.
+  int i = r0;
+  for (; i + 3 < r1; i += 4) {
+    step(b0, b2, b3, i);
+    step(b1, b3, b0, i + 1);
+    step(b2, b0, b1, i + 2);
+    step(b3, b1, b2, i + 3);
+  }
+  if (i < r1) step(b0, b2, b3, i);
+  if (i + 1 < r1) step(b1, b3, b0, i + 1);
+  if (i + 2 < r1) step(b2, b0, b1, i + 2);
+  // One fp64 partial row per group member slice (own lanes' accumulators).
+  const buffer_rsrc_t prs =
+      make_rsrc(dw_part + static_cast<size_t>(g.group) * cols + 8 * static_cast<size_t>(v0),
+                slice_bytes * 4u);
+#pragma unroll
+  for (int v = 0; v < VPT; ++v)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      buffer_store(prs, (lane_off + v * kStride) * 4u + 16u * q,
+                   __builtin_bit_cast(u32x4, f64x2{dw_lds[(v * 8 + 2 * q) * THREADS + tid],
+                                                   dw_lds[(v * 8 + 2 * q + 1) * THREADS + tid]}));
+}
+
 // READ variant pre-pass: rowdot[r] = sum_j dy*w*x over the row, streamed.
 template <int THREADS>
 __global__ __launch_bounds__(THREADS) void rmsnorm_bwd_rowdot_kernel(
@@ -352,10 +536,21 @@ struct FwdPick {
   int threads;
   int capacity;  // dwordx4 per workgroup
 };
+using BwdGroupFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, const float*,
+                            uint16_t*, double*, int, int, int, int, int, SplitArgs);
 struct BwdPick {
   BwdSliceFn fn;
   int threads;
   int capacity;
+  int lds_bytes() const { return capacity * 8 * static_cast<int>(sizeof(double)); }
+};
+// SPLIT: THREADS data lanes + one communication wave; per_cu is the
+// residency its VGPR and LDS use allows (sizes the row groups).
+struct BwdGroupPick {
+  BwdGroupFn fn;
+  int threads;
+  int capacity;
+  int per_cu;
   int lds_bytes() const { return capacity * 8 * static_cast<int>(sizeof(double)); }
 };
 
@@ -379,8 +574,22 @@ const BwdPick kBwd[] = {
     {rmsnorm_bwd_slice_kernel<256, 2>, 256, 512},
     {rmsnorm_bwd_slice_kernel<512, 2>, 512, 1024},
 };
+// Group kernels: four row buffers per lane.  At one dwordx4 per lane
+// (~104 VGPRs: 4 waves per SIMD, 16 per CU; 64 bytes of LDS dw
+// accumulators per lane) 448 data lanes + 1 wave = 8 waves give two
+// workgroups per CU and 960 + 1 = 16 waves one; two dwordx4 per lane (3
+// waves per SIMD) hold the widest slice, 1024 vectors, one workgroup per CU.
+const BwdGroupPick kBwdGroup[] = {
+    {rmsnorm_bwd_group_kernel<64, 1>, 64, 64, 8},
+    {rmsnorm_bwd_group_kernel<128, 1>, 128, 128, 5},
+    {rmsnorm_bwd_group_kernel<192, 1>, 192, 192, 4},
+    {rmsnorm_bwd_group_kernel<448, 1>, 448, 448, 2},
+    {rmsnorm_bwd_group_kernel<960, 1>, 960, 960, 1},
+    {rmsnorm_bwd_group_kernel<512, 2>, 512, 1024, 1},
+};
 constexpr int kFwdMaxCapacity = 8192;
-constexpr int kBwdMaxCapacity = 1024;
+constexpr int kBwdMaxCapacity = 1024;      // slice kernels (STAGED, READ tiles)
+constexpr int kBwdGroupCapacity = 1024;    // group kernel (SPLIT): largest member slice
 
 template <class Pick, int N>
 const Pick* pick_for(const Pick (&table)[N], int64_t chunk) {
@@ -454,14 +663,28 @@ struct BwdPlan {
   int64_t groups;
 };
 
-int rows_per_group_for(int64_t rows, int members, int cu_count) {
-  // Aim for about two workgroups per CU in total; more rows per group cut
-  // the dw partial traffic (one fp64 row per group).
-  const int64_t target_groups = (2 * static_cast<int64_t>(cu_count) + members - 1) / members;
+int rows_per_group_for(int64_t rows, int members, int cu_count, int per_cu) {
+  // Slice kernels (no exchange): aim for one resident wave of groups; more
+  // rows per group cut the dw partial traffic (one fp64 row per group).
+  const int64_t target_groups =
+      (static_cast<int64_t>(per_cu) * cu_count + members - 1) / members;
   int64_t r = (rows + target_groups - 1) / (target_groups > 0 ? target_groups : 1);
   if (r < 1) r = 1;
   if (r > 64) r = 64;
   return static_cast<int>(r);
+}
+
+// Group kernel (SPLIT): every member of every group must be running at
+// once.  A member of a group waits for the others every row, and the
+// hardware dispatcher does not reliably start a pending workgroup on a CU
+// freed by a finished group while workgroups it would complete are
+// spinning (measured: pending members started seconds late).  So the grid
+// is at most one resident wave -- G groups, G a multiple of kDispensers
+// (one dispenser subset per XCD) and G * P <= workgroups resident at once
+// -- and each group loops over ceil(rows / G) rows.
+int64_t coresident_groups(int members, int cu_count, int per_cu) {
+  const int64_t resident = static_cast<int64_t>(per_cu) * cu_count;
+  return resident / (static_cast<int64_t>(kDispensers) * members) * kDispensers;
 }
 
 int resolve_bwd(const credit_cfg* cfg, int64_t rows, int64_t cols, bool vec, int cu_count,
@@ -473,8 +696,18 @@ int resolve_bwd(const credit_cfg* cfg, int64_t rows, int64_t cols, bool vec, int
   const int64_t nvec = cols / 8;
   int p = 0;
   int v = variant;
-  if (v == CREDIT_VARIANT_AUTO) v = nvec <= kBwdMaxCapacity ? CREDIT_VARIANT_STAGED
-                                                            : CREDIT_VARIANT_SPLIT;
+  if (v == CREDIT_VARIANT_AUTO) {
+    // SPLIT when a power-of-two group of members with slices of at most
+    // kBwdGroupCapacity vectors fits the device kDispensers times over.
+    int p2 = 2;
+    while (p2 * int64_t{kBwdGroupCapacity} < nvec) p2 *= 2;
+    const int64_t chunk = (nvec + p2 - 1) / p2;
+    const bool fits = p2 <= kMaxExchangeValues &&
+                      coresident_groups(p2, cu_count, pick_for(kBwdGroup, chunk)->per_cu) > 0;
+    v = nvec <= kBwdMaxCapacity ? CREDIT_VARIANT_STAGED
+        : fits                  ? CREDIT_VARIANT_SPLIT
+                                : CREDIT_VARIANT_READ;
+  }
   if (v == CREDIT_VARIANT_STAGED) {
     if (nvec > kBwdMaxCapacity)
       return set_error(CREDIT_ERR_UNSUPPORTED,
@@ -482,12 +715,16 @@ int resolve_bwd(const credit_cfg* cfg, int64_t rows, int64_t cols, bool vec, int
     p = 1;
   } else if (v == CREDIT_VARIANT_SPLIT) {
     p = cfg_split(cfg);
-    const int need = static_cast<int>((nvec + kBwdMaxCapacity - 1) / kBwdMaxCapacity);
-    if (p == 0) p = need < 2 ? 2 : need;
+    const int need = static_cast<int>((nvec + kBwdGroupCapacity - 1) / kBwdGroupCapacity);
+    if (p == 0) {
+      // A power of two: then G groups of P fill every resident slot.
+      p = 2;
+      while (p < need) p *= 2;
+    }
     if (p < need)
       return set_error(CREDIT_ERR_UNSUPPORTED,
                        "rmsnorm_bwd split %d leaves more than %d vectors per member", p,
-                       kBwdMaxCapacity);
+                       kBwdGroupCapacity);
     if (p > nvec) p = static_cast<int>(nvec);
   } else {  // READ: column tiles of the largest slice, c from the pre-pass
     p = static_cast<int>((nvec + kBwdMaxCapacity - 1) / kBwdMaxCapacity);
@@ -497,10 +734,33 @@ int resolve_bwd(const credit_cfg* cfg, int64_t rows, int64_t cols, bool vec, int
   plan->members = sp.members;
   plan->chunk = sp.chunk;
   if (v == CREDIT_VARIANT_SPLIT && plan->members < 2) plan->variant = CREDIT_VARIANT_STAGED;
-  plan->rows_per_group = rows_per_group_for(rows, plan->members, cu_count);
+  if (plan->variant == CREDIT_VARIANT_SPLIT) {
+    if (plan->members > kMaxExchangeValues)
+      return set_error(CREDIT_ERR_UNSUPPORTED, "rmsnorm_bwd split %d exceeds %d members",
+                       plan->members, kMaxExchangeValues);
+    const int64_t g = coresident_groups(plan->members, cu_count,
+                                        pick_for(kBwdGroup, plan->chunk)->per_cu);
+    if (g == 0)
+      return set_error(CREDIT_ERR_UNSUPPORTED,
+                       "rmsnorm_bwd split %d: %d groups of it do not fit the device at once",
+                       plan->members, kDispensers);
+    const int64_t r = (rows + g - 1) / g;
+    if (r > (int64_t{1} << 30))
+      return set_error(CREDIT_ERR_BAD_SHAPE, "rmsnorm_bwd: %lld rows per group",
+                       static_cast<long long>(r));
+    plan->rows_per_group = static_cast<int>(r < 1 ? 1 : r);
+  } else {
+    plan->rows_per_group = rows_per_group_for(rows, plan->members, cu_count, 2);
+  }
   plan->groups = (rows + plan->rows_per_group - 1) / plan->rows_per_group;
   return CREDIT_OK;
 }
+
+// Slot rows per group of the group kernel: a member publishes row k two
+// steps before it needs row k's total, and a member reaches row k + 16 only
+// after every member has polled row k, so 16 rows of slots suffice.
+constexpr int kBwdRing = 16;
+int bwd_ring(const BwdPlan& p) { return p.variant == CREDIT_VARIANT_SPLIT ? kBwdRing : 1; }
 
 size_t bwd_extra_bytes(const BwdPlan& p, int64_t rows, int64_t cols) {
   size_t b = align_up(static_cast<size_t>(p.groups) * cols * sizeof(double), 256);
@@ -524,7 +784,7 @@ size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
   credit_cfg c{nullptr, variant, split, nullptr, 0};
   BwdPlan p;
   if (resolve_bwd(&c, rows, cols, cols % 8 == 0, cu_count, &p) != CREDIT_OK) return 0;
-  return split_workspace_bytes(padded_groups(p.groups), p.members, 1, p.rows_per_group,
+  return split_workspace_bytes(padded_groups(p.groups), p.members, 1, bwd_ring(p),
                                bwd_extra_bytes(p, rows, cols));
 }
 
@@ -572,7 +832,7 @@ extern "C" int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uin
   for (int64_t r0 = 0; r0 < rows; r0 += launch_groups) {
     const int64_t n = rows - r0 < launch_groups ? rows - r0 : launch_groups;
     const uint32_t total = static_cast<uint32_t>(padded_groups(n) * plan.members);
-    const SplitArgs sa{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(), 1};
+    const SplitArgs sa{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(1), 1};
     hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), 0, stream, x + r0 * cols, w,
                        y + r0 * cols, rstd + r0, c, static_cast<int>(plan.chunk), plan.members,
                        static_cast<int>(n), eps, sa);
@@ -613,11 +873,10 @@ extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
                      static_cast<long long>(plan.groups), kMaxGroupsPerLaunch);
   SplitWorkspace ws;
   CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(plan.groups), plan.members, 1,
-                                     plan.rows_per_group, bwd_extra_bytes(plan, rows, cols), &ws));
+                                     bwd_ring(plan), bwd_extra_bytes(plan, rows, cols), &ws));
   double* dw_part = reinterpret_cast<double*>(ws.extra);
   float* rowdot = reinterpret_cast<float*>(
       ws.extra + align_up(static_cast<size_t>(plan.groups) * cols * sizeof(double), 256));
-  const BwdPick* pick = pick_for(kBwd, plan.chunk);
   const int c = static_cast<int>(cols);
   int mode = kBwdWhole;
   if (plan.variant == CREDIT_VARIANT_SPLIT) mode = kBwdExchange;
@@ -630,14 +889,24 @@ extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
         <<<dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream>>>(x, w, dy, rowdot, c);
     CREDIT_TRY(check_launch("rmsnorm_bwd_rowdot_kernel"));
   }
-  if (pick->lds_bytes() > 65536)
-    return set_error(CREDIT_ERR_UNSUPPORTED, "rmsnorm_bwd: slice needs too much LDS");
-  hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), pick->lds_bytes(), stream, x,
-                     w, dy, rstd, rowdot, dx, dw_part, static_cast<int>(rows), c,
-                     static_cast<int>(plan.chunk), plan.members, plan.rows_per_group, mode,
-                     SplitArgs{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(),
-                               plan.rows_per_group});
-  CREDIT_TRY(check_launch("rmsnorm_bwd_slice_kernel"));
+  if (mode == kBwdExchange) {
+    const BwdGroupPick* pick = pick_for(kBwdGroup, plan.chunk);
+    hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads + kWave),
+                       pick->lds_bytes(), stream, x, w, dy, rstd, dx, dw_part,
+                       static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members,
+                       plan.rows_per_group,
+                       SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
+                                 next_split_epoch(static_cast<uint32_t>(plan.rows_per_group)),
+                                 kBwdRing});
+    CREDIT_TRY(check_launch("rmsnorm_bwd_group_kernel"));
+  } else {
+    const BwdPick* pick = pick_for(kBwd, plan.chunk);
+    hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), pick->lds_bytes(), stream, x,
+                       w, dy, rstd, rowdot, dx, dw_part, static_cast<int>(rows), c,
+                       static_cast<int>(plan.chunk), plan.members, plan.rows_per_group, mode,
+                       SplitArgs{});
+    CREDIT_TRY(check_launch("rmsnorm_bwd_slice_kernel"));
+  }
   const unsigned reduce_blocks = static_cast<unsigned>((cols / 2 + 255) / 256);
   rmsnorm_dw_reduce_kernel<<<dim3(reduce_blocks), dim3(256), 0, stream>>>(
       dw_part, dw, static_cast<int>(plan.groups), c);

@@ -557,7 +557,7 @@ int launch_slices(const credit_cfg* cfg, int64_t rows, const Plan& plan, int k_v
     const int64_t n = rows - r0 < groups ? rows - r0 : groups;
     const uint32_t total = static_cast<uint32_t>(padded_groups(n) * plan.members);
     launch(total, r0, static_cast<int>(n),
-           SplitArgs{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(), stages});
+           SplitArgs{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(stages), stages});
     CREDIT_TRY(check_launch(name));
   }
   return CREDIT_OK;

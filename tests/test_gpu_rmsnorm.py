@@ -199,3 +199,24 @@ def test_rmsnorm_bwd_full_config(gpu, c3_case, variant, split):
     dx, dw = bwd(x, w, dy, r32, variant, split, gpu)
     np.testing.assert_allclose(dw, edw, **FP32)
     np.testing.assert_allclose(dx, edx, **BF16)
+
+
+@pytest.mark.parametrize("variant,split", [("auto", 0), ("split", 18), ("split", 37)])
+def test_rmsnorm_bwd_back_to_back_launches(gpu, c3_case, variant, split):
+    """Launches queued with no host synchronisation between them (as a
+    training step issues them): every group of the split kernel must be
+    resident at once, or a group whose last members wait for dispatch
+    stalls until the exchange watchdog expires.  The grid is sized to one
+    resident wave; this checks no launch raises the watchdog and the last
+    result is still exact."""
+    x, w, dy, _, _, r32, edx, edw = c3_case
+    ins = [t.to(gpu) for t in (x, w, dy)] + [torch.from_numpy(r32).to(gpu)]
+    dx = torch.empty_like(ins[0])
+    dw = torch.empty(x.shape[1], dtype=torch.float32, device=gpu)
+    cfg = hip_lib.make_cfg(variant, split)
+    for _ in range(6):
+        hip_lib.rmsnorm_bwd(*ins, dx, dw, cfg)
+    torch.cuda.synchronize()
+    hip_lib.check_watchdog()
+    np.testing.assert_allclose(dw.cpu().numpy(), edw, **FP32)
+    np.testing.assert_allclose(dx.float().cpu().numpy(), edx, **BF16)
