@@ -176,6 +176,39 @@ int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
   return CREDIT_OK;
 }
 
+int coresident_groups(const void* kernel, int threads, size_t dynamic_lds, int members,
+                      int64_t* groups) {
+  struct Entry {
+    int device;
+    const void* kernel;
+    int threads;
+    size_t lds;
+    int per_cu;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  int dev = 0;
+  CREDIT_HIP(hipGetDevice(&dev));
+  int per_cu = -1;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : cache)
+      if (e.device == dev && e.kernel == kernel && e.threads == threads && e.lds == dynamic_lds)
+        per_cu = e.per_cu;
+  }
+  if (per_cu < 0) {
+    CREDIT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads,
+                                                            dynamic_lds));
+    std::lock_guard<std::mutex> lock(mu);
+    cache.push_back(Entry{dev, kernel, threads, dynamic_lds, per_cu});
+  }
+  const DeviceProps* props = nullptr;
+  CREDIT_TRY(current_device_props(&props));
+  const int64_t resident = static_cast<int64_t>(per_cu) * props->cu_count;
+  *groups = resident / (static_cast<int64_t>(kDispensers) * members) * kDispensers;
+  return CREDIT_OK;
+}
+
 int cu_count_or_default() {
   int count = 0;
   if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
@@ -257,16 +290,16 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
       body = row_sum_max_workspace(rows, cols, variant, split, cus);
       break;
     case CREDIT_OP_RMSNORM_FWD:
-      body = rmsnorm_fwd_workspace(rows, cols, variant, split);
+      body = rmsnorm_fwd_workspace(rows, cols, variant, split, cus);
       break;
     case CREDIT_OP_RMSNORM_BWD:
       body = rmsnorm_bwd_workspace(rows, cols, variant, split, cus);
       break;
     case CREDIT_OP_LAYERNORM_BWD:
-      body = layernorm_bwd_workspace(rows, cols, variant, split, 4);
+      body = layernorm_bwd_workspace(rows, cols, variant, split, 4, cus);
       break;
     case CREDIT_OP_LAYERNORM_BWD_BF16:
-      body = layernorm_bwd_workspace(rows, cols, variant, split, 2);
+      body = layernorm_bwd_workspace(rows, cols, variant, split, 2, cus);
       break;
     case CREDIT_OP_FFN:  // cols = the FFN hidden width f
       body = ffn_workspace(rows, cols);
@@ -274,7 +307,7 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
     case CREDIT_OP_SOFTMAX_FWD:
     case CREDIT_OP_SOFTMAX_BWD:
     case CREDIT_OP_SOFTMAX_LOGITS_BWD:
-      body = softmax_workspace(op, rows, cols, variant, split);
+      body = softmax_workspace(op, rows, cols, variant, split, cus);
       break;
     default:
       body = 0;

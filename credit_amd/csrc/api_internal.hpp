@@ -123,6 +123,27 @@ inline size_t split_workspace_bytes(int64_t groups, int members, int k_values, i
 }
 int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
                             int k_values, int ring, size_t extra_bytes, SplitWorkspace* out);
+
+// Split launches wait inside a group for all of its members, and the
+// dispatcher does not reliably start a pending workgroup on a CU that a
+// finished group freed while resident workgroups spin (measured on MI355X:
+// pending members started seconds late when launches were queued back to
+// back).  So a split launch is one resident wave: G groups of P members,
+// G a multiple of kDispensers (one dispenser subset per XCD), G*P no more
+// than the workgroups of the kernel resident at once on the device, and
+// each group loops over its rows.  *groups = G (0: not even kDispensers
+// groups fit).
+int coresident_groups(const void* kernel, int threads, size_t dynamic_lds, int members,
+                      int64_t* groups);
+// Upper bound of G for workspace sizing without a device query.
+inline int64_t coresident_groups_bound(int members, int cu_count) {
+  const int64_t resident = static_cast<int64_t>(cu_count) * 32;  // >= blocks per CU
+  return (resident / members + kDispensers - 1) / kDispensers * kDispensers;
+}
+// Slot rows per group of the barrier-synchronised split kernels: every
+// exchange ends with a workgroup barrier, so no member publishes stage s+2
+// before every member has polled stage s.  Four rows leave margin.
+constexpr int kSplitRing = 4;
 inline uint32_t* ws_watchdog(char* base) { return reinterpret_cast<uint32_t*>(base); }
 inline uint32_t* ws_counters(char* base) {
   return reinterpret_cast<uint32_t*>(base + kWorkspaceHeader);
@@ -139,9 +160,10 @@ size_t row_sum_max_workspace(int64_t rows, int64_t cols, int variant, int split,
                              int cu_count);
 size_t ffn_workspace(int64_t rows, int64_t ffn_dim);
 size_t layernorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
-                               int elem_bytes);
-size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int split);
-size_t rmsnorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split);
+                               int elem_bytes, int cu_count);
+size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int split,
+                         int cu_count);
+size_t rmsnorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split, int cu_count);
 size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
                              int cu_count);
 

@@ -203,6 +203,15 @@ __device__ __forceinline__ void buffer_store(buffer_rsrc_t r, uint32_t offset, u
   __builtin_amdgcn_raw_buffer_store_b128(v, r, offset, 0, 0);
 }
 
+// The lane index, re-defined opaquely: per-lane addresses and predicates
+// derived from it inside a loop cannot be hoisted out of the loop (where
+// they would stay live across iterations and raise register pressure).
+__device__ __forceinline__ int opaque_lane_index() {
+  int t = static_cast<int>(threadIdx.x);
+  __asm__ volatile("" : "+v"(t));
+  return t;
+}
+
 // *p += v on an LDS double that only this lane updates (ds_add_f64).
 __device__ __forceinline__ void lds_add(double* p, double v) {
   __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);

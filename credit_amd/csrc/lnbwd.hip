@@ -76,33 +76,38 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
   __shared__ double red[4][NW];
   const int tid = threadIdx.x;
   SplitGroup g;
-  int row = blockIdx.x, member = 0;
+  // members == 1: one workgroup per row.  members > 1: a co-resident grid
+  // of G groups; the member covers its slice of rows group, group + G, ...
+  int row0 = blockIdx.x, step = gridDim.x, member = 0;
   if (members > 1) {
     g = split_join(sa, members, 2);
-    row = g.group;
+    row0 = g.group;
+    step = static_cast<int>(sa.grid) / members;
     member = g.member;
-    if (row >= rows) return;  // padding group
   }
   const int nvec = cols / E;
   const int v0 = member * chunk;
   const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  for (int row = row0; row < rows; row += step) {
+  const int tid = opaque_lane_index();
   const size_t off = static_cast<size_t>(row) * cols;
   const raw* xr = reinterpret_cast<const raw*>(x + off) + v0;
   const raw* dr = reinterpret_cast<const raw*>(dy + off) + v0;
   const raw* gr = reinterpret_cast<const raw*>(gamma) + v0;
   raw xv[VPT], dv[VPT];
+  // (p + k*THREADS)[tid]: a uniform base per k and one lane offset, so no
+  // per-k lane address stays live across the row loop.
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    const bool in = idx < vlen;
-    xv[k] = in ? load_nt(xr + idx) : raw{};
-    dv[k] = in ? load_nt(dr + idx) : raw{};
+    const bool in = tid < vlen - k * THREADS;
+    xv[k] = in ? load_nt(&(xr + k * THREADS)[tid]) : raw{};
+    dv[k] = in ? load_nt(&(dr + k * THREADS)[tid]) : raw{};
   }
   const float x0 = V::scalar(x + off);
   float a1 = 0.0f, a2 = 0.0f;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
-    if (tid + k * THREADS < vlen) {
+    if (tid < vlen - k * THREADS) {
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const float d = V::get(xv[k], e) - x0;
@@ -126,9 +131,8 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
   float b1 = 0.0f, b2 = 0.0f;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    if (idx < vlen) {
-      const raw gv = gr[idx];
+    if (tid < vlen - k * THREADS) {
+      const raw gv = (gr + k * THREADS)[tid];
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const float gg = V::get(dv[k], e) * V::get(gv, e);
@@ -153,17 +157,17 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
   raw* outr = reinterpret_cast<raw*>(dx + off) + v0;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    if (idx < vlen) {
-      const raw gv = gr[idx];
+    if (tid < vlen - k * THREADS) {
+      const raw gv = (gr + k * THREADS)[tid];
       float o[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const float xh = (V::get(xv[k], e) - st.mean) * st.rstd;
         o[e] = (V::get(dv[k], e) * V::get(gv, e) - mg - xh * mgx) * st.rstd;
       }
-      store_nt(outr + idx, V::pack(o));
+      store_nt(&(outr + k * THREADS)[tid], V::pack(o));
     }
+  }
   }
 }
 
@@ -328,32 +332,38 @@ int layernorm_bwd(const T* x, const T* dy, const T* gamma, T* dx, int64_t rows, 
                        static_cast<int>(rows), eps, SplitArgs{});
     return check_launch("layernorm_bwd_slice_kernel");
   }
-  const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
+  int64_t groups = 0;
+  CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(pk->fn), pk->threads, 0,
+                               plan.members, &groups));
+  if (groups == 0)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "layernorm_bwd: %d groups of %d members do not fit the device", kDispensers,
+                     plan.members);
+  if (groups > padded_groups(rows)) groups = padded_groups(rows);
+  const int64_t per_group = (rows + groups - 1) / groups;
   SplitWorkspace ws;
-  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(groups), plan.members, 2, 2, 0, &ws));
-  for (int64_t r0 = 0; r0 < rows; r0 += groups) {
-    const int64_t n = rows - r0 < groups ? rows - r0 : groups;
-    const uint32_t total = static_cast<uint32_t>(padded_groups(n) * plan.members);
-    hipLaunchKernelGGL(pk->fn, dim3(total), dim3(pk->threads), 0, stream, x + r0 * cols,
-                       dy + r0 * cols, gamma, dx + r0 * cols, c, static_cast<int>(plan.chunk),
-                       plan.members, static_cast<int>(n), eps,
-                       SplitArgs{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(2), 2});
-    CREDIT_TRY(check_launch("layernorm_bwd_slice_kernel(split)"));
-  }
-  return CREDIT_OK;
+  CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 2, kSplitRing, 0, &ws));
+  const uint32_t total = static_cast<uint32_t>(groups * plan.members);
+  hipLaunchKernelGGL(pk->fn, dim3(total), dim3(pk->threads), 0, stream, x, dy, gamma, dx, c,
+                     static_cast<int>(plan.chunk), plan.members, static_cast<int>(rows), eps,
+                     SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
+                               next_split_epoch(static_cast<uint32_t>(per_group * 2)),
+                               kSplitRing});
+  return check_launch("layernorm_bwd_slice_kernel(split)");
 }
 
 }  // namespace
 
 size_t layernorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
-                               int elem_bytes) {
+                               int elem_bytes, int cu_count) {
   credit_cfg c{nullptr, variant, split, nullptr, 0};
   Plan p;
   const int64_t e = 16 / elem_bytes;
   const int64_t cap = elem_bytes == 4 ? Slices<float>::capacity : Slices<uint16_t>::capacity;
   if (resolve(&c, cols / e, cols % e == 0, cap, &p) != CREDIT_OK || p.members <= 1) return 0;
-  const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
-  return split_workspace_bytes(padded_groups(groups), p.members, 2, 2, 0);
+  int64_t groups = coresident_groups_bound(p.members, cu_count);
+  if (groups > padded_groups(rows)) groups = padded_groups(rows);
+  return split_workspace_bytes(groups, p.members, 2, kSplitRing, 0);
 }
 
 }  // namespace credit

@@ -171,19 +171,22 @@ __global__ void mb_pingpong_kernel(uint32_t* flag, int peer, int rounds, uint64_
 }
 
 // ------------------------------------------ arrival barrier cost (H3/H4) --
-// `groups` ticketed groups of `members` workgroups; each group meets at
-// `barriers` split barriers in a row (publish, arrive, wait, read the
+// A co-resident grid of ticketed groups of `members` workgroups, shaped
+// like the split kernels' launches: each group takes rows group, group + G,
+// ... of `rows` and meets `barriers` times per row (publish, poll, read the
 // partials): the un-overlapped cost of the exchange the split kernels use.
 __global__ __launch_bounds__(256) void mb_barrier_kernel(SplitArgs sa, int members,
-                                                         int barriers, int groups,
+                                                         int barriers, int rows,
                                                          double* sink) {
   SplitGroup g = split_join(sa, members, 1);
-  if (g.group >= groups) return;  // padding group
+  const int step = static_cast<int>(sa.grid) / members;
   double acc = 0.0;
-  for (int k = 0; k < barriers; ++k) {
-    if (threadIdx.x == 0) split_publish(g, 0, static_cast<double>(g.member + k));
-    split_exchange(g);
-    acc += split_sum(g, 0);
+  for (int row = g.group; row < rows; row += step) {
+    for (int k = 0; k < barriers; ++k) {
+      if (threadIdx.x == 0) split_publish(g, 0, static_cast<double>(g.member + k));
+      split_exchange(g);
+      acc += split_sum(g, 0);
+    }
   }
   if (acc == -1.0 && threadIdx.x == 0) sink[0] = acc;  // keeps the reads alive
 }
@@ -393,37 +396,35 @@ int control_overhead(int64_t rows, int split, int barriers, int warmup, int iter
   const DeviceProps* props = nullptr;
   CREDIT_TRY(current_device_props(&props));
   if (split < 1 || split > 64) return set_error(CREDIT_ERR_BAD_CONFIG, "split %d", split);
-  int64_t groups = rows;
-  if (groups > kMaxGroupsPerLaunch) groups = kMaxGroupsPerLaunch;
-  if (cooperative) {
-    // A cooperative launch must fit the device at once.
-    int per_cu = 0;
-    CREDIT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mb_barrier_kernel, 256, 0));
-    const int64_t cap = static_cast<int64_t>(per_cu) * props->cu_count;
-    if (groups * split > cap) groups = cap / split;
-  }
-  if (cooperative) groups = groups / kDispensers * kDispensers;
+  if (rows < 1) return set_error(CREDIT_ERR_BAD_CONFIG, "rows must be >= 1");
+  int64_t groups = 0;
+  CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(mb_barrier_kernel), 256, 0, split,
+                               &groups));
   if (groups < 1) return set_error(CREDIT_ERR_UNSUPPORTED, "split %d does not fit", split);
-  const int64_t grid_groups = padded_groups(groups);
+  if (groups > padded_groups(rows)) groups = padded_groups(rows);
+  const int64_t per_group = (rows + groups - 1) / groups;
   DevBuf ws, sink;
-  const int stages = barriers > 0 ? barriers : 1;
-  CREDIT_TRY(ws.alloc(kScratchOffset + split_slot_bytes(grid_groups, split, 1, stages)));
+  CREDIT_TRY(ws.alloc(kScratchOffset + split_slot_bytes(groups, split, 1, kSplitRing)));
   CREDIT_TRY(sink.alloc(256));
   char* base = static_cast<char*>(ws.p);
   uint32_t* counters = ws_counters(base);
   uint32_t* watchdog = ws_watchdog(base);
   uint64_t* slots = reinterpret_cast<uint64_t*>(ws_scratch(base));
   double* sinkp = static_cast<double*>(sink.p);
-  const unsigned grid = static_cast<unsigned>(grid_groups * split);
-  uint32_t total = grid;
-  int valid = static_cast<int>(groups);
+  const unsigned grid = static_cast<unsigned>(groups * split);
+  // The plain reference launches one workgroup per (row, member): the work
+  // items a split launch covers, with no exchange.
+  const unsigned plain_grid = static_cast<unsigned>(rows * split);
+  const uint32_t total = grid;
+  int valid = static_cast<int>(rows);
+  const uint32_t stages = static_cast<uint32_t>(per_group * (barriers > 0 ? barriers : 1));
   auto plain = [&](int) -> int {
-    mb_plain_kernel<<<grid, 256>>>(static_cast<int*>(sink.p));
+    mb_plain_kernel<<<plain_grid, 256>>>(static_cast<int*>(sink.p));
     return check_launch("mb_plain_kernel");
   };
   int members = split;
   auto timed = [&](int) -> int {
-    SplitArgs sa{counters, slots, watchdog, total, next_split_epoch(stages), stages};
+    SplitArgs sa{counters, slots, watchdog, total, next_split_epoch(stages), kSplitRing};
     if (cooperative) {
       void* args[] = {&sa, &members, &barriers, &valid, &sinkp};
       CREDIT_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mb_barrier_kernel),

@@ -86,23 +86,27 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
   __shared__ double red[NW];
   const int tid = threadIdx.x;
   SplitGroup g;
-  int row = blockIdx.x, member = 0;
+  // members == 1: one workgroup per row.  members > 1: a co-resident grid
+  // of G groups; the member covers its slice of rows group, group + G, ...
+  int row0 = blockIdx.x, step = gridDim.x, member = 0;
   if (members > 1) {
     g = split_join(sa, members, 1);
-    row = g.group;
+    row0 = g.group;
+    step = static_cast<int>(sa.grid) / members;
     member = g.member;
-    if (row >= rows) return;  // padding group
   }
   const int nvec = cols >> 3;
   const int v0 = member * chunk;
   const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  for (int row = row0; row < rows; row += step) {
+  const int tid = opaque_lane_index();
   const u32x4* xr = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(row) * cols) + v0;
   u32x4 v[VPT];
+  // (p + k*THREADS)[tid]: a uniform base per k and one lane offset, so no
+  // per-k lane address stays live across the row loop.
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    v[k] = idx < vlen ? load_nt(xr + idx) : u32x4{0, 0, 0, 0};
-  }
+  for (int k = 0; k < VPT; ++k)
+    v[k] = tid < vlen - k * THREADS ? load_nt(&(xr + k * THREADS)[tid]) : u32x4{0, 0, 0, 0};
   float ss = 0.0f;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) ss += sumsq8(v[k]);
@@ -116,11 +120,11 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
   const u32x4* wr = reinterpret_cast<const u32x4*>(w) + v0;
   u32x4* yr = reinterpret_cast<u32x4*>(y + static_cast<size_t>(row) * cols) + v0;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    if (idx < vlen) store_nt(yr + idx, scale8(v[k], wr[idx], rs));
-  }
+  for (int k = 0; k < VPT; ++k)
+    if (tid < vlen - k * THREADS)
+      store_nt(&(yr + k * THREADS)[tid], scale8(v[k], (wr + k * THREADS)[tid], rs));
   if (member == 0 && tid == 0) rstd_out[row] = rs;
+  }
 }
 
 // Streaming forward: pass 1 sum of squares, pass 2 output.  VEC: rows are
@@ -770,13 +774,15 @@ size_t bwd_extra_bytes(const BwdPlan& p, int64_t rows, int64_t cols) {
 
 }  // namespace
 
-size_t rmsnorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split) {
+size_t rmsnorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split,
+                             int cu_count) {
   credit_cfg c{nullptr, variant, split, nullptr, 0};
   Plan p;
   if (resolve_fwd(&c, cols, cols % 8 == 0, &p) != CREDIT_OK) return 0;
   if (p.variant != CREDIT_VARIANT_SPLIT) return 0;
-  const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
-  return split_workspace_bytes(padded_groups(groups), p.members, 1, 1, 0);
+  int64_t groups = coresident_groups_bound(p.members, cu_count);
+  if (groups > padded_groups(rows)) groups = padded_groups(rows);
+  return split_workspace_bytes(groups, p.members, 1, kSplitRing, 0);
 }
 
 size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
@@ -825,20 +831,24 @@ extern "C" int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uin
                        static_cast<int>(rows), eps, SplitArgs{});
     return check_launch("rmsnorm_fwd_slice_kernel");
   }
-  const int64_t launch_groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
+  int64_t groups = 0;
+  CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(pick->fn), pick->threads, 0,
+                               plan.members, &groups));
+  if (groups == 0)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "rmsnorm_fwd: %d groups of %d members do not fit the device", kDispensers,
+                     plan.members);
+  if (groups > padded_groups(rows)) groups = padded_groups(rows);
+  const int64_t per_group = (rows + groups - 1) / groups;
   SplitWorkspace ws;
-  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(launch_groups), plan.members, 1, 1, 0,
-                                     &ws));
-  for (int64_t r0 = 0; r0 < rows; r0 += launch_groups) {
-    const int64_t n = rows - r0 < launch_groups ? rows - r0 : launch_groups;
-    const uint32_t total = static_cast<uint32_t>(padded_groups(n) * plan.members);
-    const SplitArgs sa{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(1), 1};
-    hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), 0, stream, x + r0 * cols, w,
-                       y + r0 * cols, rstd + r0, c, static_cast<int>(plan.chunk), plan.members,
-                       static_cast<int>(n), eps, sa);
-    CREDIT_TRY(check_launch("rmsnorm_fwd_slice_kernel(split)"));
-  }
-  return CREDIT_OK;
+  CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 1, kSplitRing, 0, &ws));
+  const uint32_t total = static_cast<uint32_t>(groups * plan.members);
+  const SplitArgs sa{ws.counters, ws.slots, ws.watchdog, total,
+                     next_split_epoch(static_cast<uint32_t>(per_group)), kSplitRing};
+  hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), 0, stream, x, w, y, rstd, c,
+                     static_cast<int>(plan.chunk), plan.members, static_cast<int>(rows), eps,
+                     sa);
+  return check_launch("rmsnorm_fwd_slice_kernel(split)");
 }
 
 extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
@@ -891,6 +901,14 @@ extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
   }
   if (mode == kBwdExchange) {
     const BwdGroupPick* pick = pick_for(kBwdGroup, plan.chunk);
+    int64_t fit = 0;
+    CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(pick->fn), pick->threads + kWave,
+                                 pick->lds_bytes(), plan.members, &fit));
+    if (padded_groups(plan.groups) > fit)
+      return set_error(CREDIT_ERR_UNSUPPORTED,
+                       "rmsnorm_bwd: %lld groups of %d members exceed the %lld resident at once",
+                       static_cast<long long>(padded_groups(plan.groups)), plan.members,
+                       static_cast<long long>(fit));
     hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads + kWave),
                        pick->lds_bytes(), stream, x, w, dy, rstd, dx, dw_part,
                        static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members,

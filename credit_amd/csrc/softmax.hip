@@ -97,19 +97,21 @@ __device__ __forceinline__ void split_merge_maxsum(const SplitGroup& g, float* m
 }
 
 struct Slice {
-  int row, member, v0, vlen;
+  int row, step, member, v0, vlen;
 };
 
-// Row and slice of this workgroup: ticketed member of a group when
-// members > 1, otherwise row = blockIdx.x holding the whole row.
+// Rows and slice of this workgroup.  members == 1: the grid has one
+// workgroup per row (row = blockIdx.x, one pass).  members > 1: a
+// co-resident grid of G groups; the ticketed member covers the same slice of
+// rows group, group + G, group + 2G, ... (padding groups have group >= rows
+// and do no pass).
 __device__ __forceinline__ Slice slice_of(SplitGroup* g, int members, int k_values, int chunk,
                                           int nvec, const SplitArgs& sa) {
-  // s.row >= rows marks a padding group of a ticketed launch: the caller
-  // returns at once.
-  Slice s{static_cast<int>(blockIdx.x), 0, 0, 0};
+  Slice s{static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), 0, 0, 0};
   if (members > 1) {
     *g = split_join(sa, members, k_values);
     s.row = g->group;
+    s.step = static_cast<int>(sa.grid) / members;
     s.member = g->member;
   }
   s.v0 = s.member * chunk;
@@ -128,14 +130,16 @@ __global__ __launch_bounds__(THREADS) void softmax_fwd_slice_kernel(
   const int tid = threadIdx.x;
   SplitGroup g;
   const Slice sl = slice_of(&g, members, 2, chunk, cols >> 2, sa);
-  if (sl.row >= rows) return;
-  const f32x4* xr = reinterpret_cast<const f32x4*>(x + static_cast<size_t>(sl.row) * cols) + sl.v0;
+  for (int row = sl.row; row < rows; row += sl.step) {
+  const int tid = opaque_lane_index();
+  const f32x4* xr = reinterpret_cast<const f32x4*>(x + static_cast<size_t>(row) * cols) + sl.v0;
   f32x4 v[VPT];
+  // (xr + k*THREADS)[tid]: a uniform base per k and one lane offset, so no
+  // per-k lane address stays live across the row loop.
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    v[k] = idx < sl.vlen ? load_nt(xr + idx) : f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
-  }
+  for (int k = 0; k < VPT; ++k)
+    v[k] = tid < sl.vlen - k * THREADS ? load_nt(&(xr + k * THREADS)[tid])
+                                       : f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
   float lm = kNegInf;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) lm = fmax_nan(lm, max4(v[k]));
@@ -157,15 +161,14 @@ __global__ __launch_bounds__(THREADS) void softmax_fwd_slice_kernel(
     split_merge_maxsum(g, &m, &s);
   }
   const float inv_s = static_cast<float>(1.0 / s);
-  f32x4* pr = reinterpret_cast<f32x4*>(p + static_cast<size_t>(sl.row) * cols) + sl.v0;
+  f32x4* pr = reinterpret_cast<f32x4*>(p + static_cast<size_t>(row) * cols) + sl.v0;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    if (idx < sl.vlen) store_nt(pr + idx, prob4(v[k], m, inv_s));
-  }
+  for (int k = 0; k < VPT; ++k)
+    if (tid < sl.vlen - k * THREADS) store_nt(&(pr + k * THREADS)[tid], prob4(v[k], m, inv_s));
   if (sl.member == 0 && tid == 0) {
-    rowmax[sl.row] = m;
-    lse[sl.row] = static_cast<float>(static_cast<double>(m) + ::log(s));
+    rowmax[row] = m;
+    lse[row] = static_cast<float>(static_cast<double>(m) + ::log(s));
+  }
   }
 }
 
@@ -244,17 +247,17 @@ __global__ __launch_bounds__(THREADS) void softmax_bwd_slice_kernel(
   const int tid = threadIdx.x;
   SplitGroup g;
   const Slice sl = slice_of(&g, members, 1, chunk, cols >> 2, sa);
-  if (sl.row >= rows) return;
-  const size_t off = static_cast<size_t>(sl.row) * cols;
+  for (int row = sl.row; row < rows; row += sl.step) {
+  const int tid = opaque_lane_index();
+  const size_t off = static_cast<size_t>(row) * cols;
   const f32x4* pr = reinterpret_cast<const f32x4*>(p + off) + sl.v0;
   const f32x4* dr = reinterpret_cast<const f32x4*>(dy + off) + sl.v0;
   f32x4 pv[VPT], dv[VPT];
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    const bool in = idx < sl.vlen;
-    pv[k] = in ? load_nt(pr + idx) : f32x4{0, 0, 0, 0};
-    dv[k] = in ? load_nt(dr + idx) : f32x4{0, 0, 0, 0};
+    const bool in = tid < sl.vlen - k * THREADS;
+    pv[k] = in ? load_nt(&(pr + k * THREADS)[tid]) : f32x4{0, 0, 0, 0};
+    dv[k] = in ? load_nt(&(dr + k * THREADS)[tid]) : f32x4{0, 0, 0, 0};
   }
   float ld = 0.0f;
 #pragma unroll
@@ -268,9 +271,8 @@ __global__ __launch_bounds__(THREADS) void softmax_bwd_slice_kernel(
   const float d = static_cast<float>(dot);
   f32x4* xr = reinterpret_cast<f32x4*>(dx + off) + sl.v0;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    if (idx < sl.vlen) store_nt(xr + idx, grad4(pv[k], dv[k], d));
+  for (int k = 0; k < VPT; ++k)
+    if (tid < sl.vlen - k * THREADS) store_nt(&(xr + k * THREADS)[tid], grad4(pv[k], dv[k], d));
   }
 }
 
@@ -329,17 +331,17 @@ __global__ __launch_bounds__(THREADS) void softmax_logits_bwd_slice_kernel(
   const int tid = threadIdx.x;
   SplitGroup g;
   const Slice sl = slice_of(&g, members, 2, chunk, cols >> 2, sa);
-  if (sl.row >= rows) return;
-  const size_t off = static_cast<size_t>(sl.row) * cols;
+  for (int row = sl.row; row < rows; row += sl.step) {
+  const int tid = opaque_lane_index();
+  const size_t off = static_cast<size_t>(row) * cols;
   const f32x4* lr = reinterpret_cast<const f32x4*>(logits + off) + sl.v0;
   const f32x4* dr = reinterpret_cast<const f32x4*>(dy + off) + sl.v0;
   f32x4 v[VPT], dv[VPT];
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    const bool in = idx < sl.vlen;
-    v[k] = in ? load_nt(lr + idx) : f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
-    dv[k] = in ? load_nt(dr + idx) : f32x4{0, 0, 0, 0};
+    const bool in = tid < sl.vlen - k * THREADS;
+    v[k] = in ? load_nt(&(lr + k * THREADS)[tid]) : f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+    dv[k] = in ? load_nt(&(dr + k * THREADS)[tid]) : f32x4{0, 0, 0, 0};
   }
   float lm = kNegInf;
 #pragma unroll
@@ -377,9 +379,8 @@ __global__ __launch_bounds__(THREADS) void softmax_logits_bwd_slice_kernel(
   const float d = static_cast<float>(dot);
   f32x4* xr = reinterpret_cast<f32x4*>(dx + off) + sl.v0;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int idx = tid + k * THREADS;
-    if (idx < sl.vlen) store_nt(xr + idx, grad4(v[k], dv[k], d));
+  for (int k = 0; k < VPT; ++k)
+    if (tid < sl.vlen - k * THREADS) store_nt(&(xr + k * THREADS)[tid], grad4(v[k], dv[k], d));
   }
 }
 
@@ -540,45 +541,50 @@ int resolve(const credit_cfg* cfg, int64_t cols, bool vec, int64_t capacity, con
 constexpr int64_t kFwdCapacity = 16384;
 constexpr int64_t kBwdCapacity = 8192;
 
-// Launch a slice kernel over all rows: a plain grid of rows workgroups
-// (members == 1) or ticketed groups, at most kMaxGroupsPerLaunch per launch.
+// Launch a slice kernel over all rows: a plain grid of one workgroup per
+// row (members == 1), or one co-resident wave of ticketed groups, each
+// looping over its rows (`stages` exchanges per row).
 template <class Fn, class Launch>
-int launch_slices(const credit_cfg* cfg, int64_t rows, const Plan& plan, int k_values,
-                  int stages, const char* name, Launch&& launch) {
+int launch_slices(const credit_cfg* cfg, int64_t rows, const Plan& plan, const Pick<Fn>* pk,
+                  int k_values, int stages, const char* name, Launch&& launch) {
   if (plan.members == 1) {
-    launch(static_cast<unsigned>(rows), int64_t{0}, static_cast<int>(rows), SplitArgs{});
+    launch(static_cast<unsigned>(rows), SplitArgs{});
     return check_launch(name);
   }
-  const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
+  int64_t groups = 0;
+  CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(pk->fn), pk->threads, 0,
+                               plan.members, &groups));
+  if (groups == 0)
+    return set_error(CREDIT_ERR_UNSUPPORTED, "%s: %d groups of %d members do not fit the device",
+                     name, kDispensers, plan.members);
+  if (groups > padded_groups(rows)) groups = padded_groups(rows);
+  const int64_t per_group = (rows + groups - 1) / groups;
   SplitWorkspace ws;
-  CREDIT_TRY(acquire_split_workspace(cfg, padded_groups(groups), plan.members, k_values, stages,
-                                     0, &ws));
-  for (int64_t r0 = 0; r0 < rows; r0 += groups) {
-    const int64_t n = rows - r0 < groups ? rows - r0 : groups;
-    const uint32_t total = static_cast<uint32_t>(padded_groups(n) * plan.members);
-    launch(total, r0, static_cast<int>(n),
-           SplitArgs{ws.counters, ws.slots, ws.watchdog, total, next_split_epoch(stages), stages});
-    CREDIT_TRY(check_launch(name));
-  }
-  return CREDIT_OK;
+  CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, k_values, kSplitRing, 0, &ws));
+  const uint32_t total = static_cast<uint32_t>(groups * plan.members);
+  launch(total, SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
+                          next_split_epoch(static_cast<uint32_t>(per_group * stages)),
+                          kSplitRing});
+  return check_launch(name);
 }
 
-size_t slice_workspace(int64_t rows, const Plan& p, int k_values, int stages) {
+size_t slice_workspace(int64_t rows, const Plan& p, int k_values, int cu_count) {
   if (p.members <= 1) return 0;
-  const int64_t groups = rows < kMaxGroupsPerLaunch ? rows : kMaxGroupsPerLaunch;
-  return split_workspace_bytes(padded_groups(groups), p.members, k_values, stages, 0);
+  int64_t groups = coresident_groups_bound(p.members, cu_count);
+  if (groups > padded_groups(rows)) groups = padded_groups(rows);
+  return split_workspace_bytes(groups, p.members, k_values, kSplitRing, 0);
 }
 
 }  // namespace
 
-size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int split) {
+size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int split,
+                         int cu_count) {
   credit_cfg c{nullptr, variant, split, nullptr, 0};
   Plan p;
   const int64_t cap = op == CREDIT_OP_SOFTMAX_FWD ? kFwdCapacity : kBwdCapacity;
   if (resolve(&c, cols, cols % 4 == 0, cap, "softmax", &p) != CREDIT_OK) return 0;
   const int k = op == CREDIT_OP_SOFTMAX_BWD ? 1 : 2;
-  const int stages = op == CREDIT_OP_SOFTMAX_LOGITS_BWD ? 2 : 1;
-  return slice_workspace(rows, p, k, stages);
+  return slice_workspace(rows, p, k, cu_count);
 }
 
 }  // namespace credit
@@ -610,11 +616,11 @@ extern "C" int credit_softmax_fwd_f32(const float* x, float* p, float* rowmax, f
   }
   const Pick<FwdFn>* pk = pick_for(kFwd, plan.chunk);
   return launch_slices<FwdFn>(
-      cfg, rows, plan, 2, 1, "softmax_fwd_slice_kernel",
-      [&](unsigned grid, int64_t r0, int n, const SplitArgs& sa) {
-        hipLaunchKernelGGL(pk->fn, dim3(grid), dim3(pk->threads), 0, stream, x + r0 * cols,
-                           p + r0 * cols, rowmax + r0, lse + r0, c,
-                           static_cast<int>(plan.chunk), plan.members, n, sa);
+      cfg, rows, plan, pk, 2, 1, "softmax_fwd_slice_kernel",
+      [&](unsigned grid, const SplitArgs& sa) {
+        hipLaunchKernelGGL(pk->fn, dim3(grid), dim3(pk->threads), 0, stream, x, p, rowmax, lse,
+                           c, static_cast<int>(plan.chunk), plan.members,
+                           static_cast<int>(rows), sa);
       });
 }
 
@@ -644,11 +650,11 @@ extern "C" int credit_softmax_bwd_f32(const float* p, const float* dy, float* dx
   }
   const Pick<BwdFn>* pk = pick_for(kBwd, plan.chunk);
   return launch_slices<BwdFn>(
-      cfg, rows, plan, 1, 1, "softmax_bwd_slice_kernel",
-      [&](unsigned grid, int64_t r0, int n, const SplitArgs& sa) {
-        hipLaunchKernelGGL(pk->fn, dim3(grid), dim3(pk->threads), 0, stream, p + r0 * cols,
-                           dy + r0 * cols, dx + r0 * cols, c, static_cast<int>(plan.chunk),
-                           plan.members, n, sa);
+      cfg, rows, plan, pk, 1, 1, "softmax_bwd_slice_kernel",
+      [&](unsigned grid, const SplitArgs& sa) {
+        hipLaunchKernelGGL(pk->fn, dim3(grid), dim3(pk->threads), 0, stream, p, dy, dx, c,
+                           static_cast<int>(plan.chunk), plan.members, static_cast<int>(rows),
+                           sa);
       });
 }
 
@@ -679,10 +685,10 @@ extern "C" int credit_softmax_logits_bwd_f32(const float* logits, const float* d
   }
   const Pick<BwdFn>* pk = pick_for(kLogits, plan.chunk);
   return launch_slices<BwdFn>(
-      cfg, rows, plan, 2, 2, "softmax_logits_bwd_slice_kernel",
-      [&](unsigned grid, int64_t r0, int n, const SplitArgs& sa) {
-        hipLaunchKernelGGL(pk->fn, dim3(grid), dim3(pk->threads), 0, stream,
-                           logits + r0 * cols, dy + r0 * cols, dx + r0 * cols, c,
-                           static_cast<int>(plan.chunk), plan.members, n, sa);
+      cfg, rows, plan, pk, 2, 2, "softmax_logits_bwd_slice_kernel",
+      [&](unsigned grid, const SplitArgs& sa) {
+        hipLaunchKernelGGL(pk->fn, dim3(grid), dim3(pk->threads), 0, stream, logits, dy, dx,
+                           c, static_cast<int>(plan.chunk), plan.members,
+                           static_cast<int>(rows), sa);
       });
 }

@@ -248,9 +248,10 @@ def microbench(name: str, nbytes: int = 0, iters: int = 0, n_results: int = 16) 
 
 def control_overhead(rows: int, split: int, barriers: int, warmup: int = 3, iters: int = 20,
                      cooperative: bool = False) -> tuple[float, float]:
-    """(plain_ms, split_ms): a grid of `rows` ticketed groups of `split`
-    workgroups meeting at `barriers` split barriers, against a plain launch
-    of the same grid (replaces build/cluster_control)."""
+    """(plain_ms, split_ms): `rows` rows covered by a co-resident wave of
+    ticketed groups of `split` workgroups meeting `barriers` times per row,
+    against a plain launch of rows * split workgroups with no exchange
+    (replaces build/cluster_control)."""
     plain = ctypes.c_double()
     split_ms = ctypes.c_double()
     check(load_library().credit_control_overhead(rows, split, barriers, warmup, iters,
