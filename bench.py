@@ -39,7 +39,7 @@ CALL_KERNELS = {
     "softmax_fwd": ["softmax_fwd_slice_kernel<1024, 16>"],
     "softmax_bwd": ["softmax_bwd_slice_kernel<1024, 8>"],
     "softmax_logits_backward": ["softmax_logits_bwd_slice_kernel<1024, 8>"],
-    "ffn": ["ffn_rstd_kernel", "ffn_gemm_kernel<0>", "ffn_gemm_kernel<1>"],
+    "ffn": ["ffn_rstd_kernel", "ffn_gemm256_kernel<0>", "ffn_gemm256_kernel<1>"],
     "layernorm_backward": ["layernorm_bwd_slice_kernel<float, 1024, 8>"],
     "layernorm_backward_bf16": ["layernorm_bwd_slice_kernel<unsigned short, 1024, 4>"],
 }
