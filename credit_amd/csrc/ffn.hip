@@ -374,136 +374,6 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
   }
 }
 
-template <int EPI>
-__global__ __launch_bounds__(kBigThreads) void gemm_8w_g16(
-    const uint16_t* __restrict__ A, const float* __restrict__ scale,
-    const uint16_t* __restrict__ B, const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
-    int M, int N, int K) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves, 128 x 64 each
-
-  // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin,
-  // so XCD x runs ids x, x + 8, ...; give each XCD a contiguous run of the
-  // tile sequence, and walk that run in blocks of kGroupM M-tiles (8 M-tiles
-  // x 4 N-tiles run at once per XCD and share A rows and B columns in its L2;
-  // 4 or 16 M-tiles measured 3-8% slower).
-  const int tiles_m = M / kBig, tiles_n = N / kBig;
-  const int total = tiles_m * tiles_n;
-  const int per_xcd = total / 8;  // host guarantees total % 8 == 0
-  const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  const int group = t / (16 * tiles_n);
-  const int gm = tiles_m - group * 16 < 16 ? tiles_m - group * 16 : 16;
-  const int within = t - group * 16 * tiles_n;
-  const int tm = group * 16 + within % gm;
-  const int tn = within / gm;
-  const int m0 = tm * kBig, n0 = tn * kBig;
-  // Load assignment: instruction i (0..1) of wave w fills LDS rows
-  // (8 i + w) * 16 + lane / 4, swizzled position lane % 4.  Element offsets
-  // fit 32 bits (host checks M*K and N*K < 2^31).
-  uint32_t a_off[2], b_off[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = (8 * i + wave) * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ ((r >> 2) & 3);
-    a_off[i] = static_cast<uint32_t>((m0 + r) * K + c * 8);
-    b_off[i] = static_cast<uint32_t>((n0 + r) * K + c * 8);
-  }
-  auto issue = [&](int ks, int stage) {
-    char* a_base = smem + stage * kBigStage;
-    char* b_base = a_base + kBigTile;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int blk = (8 * i + wave) * 1024;
-      __builtin_amdgcn_global_load_lds(A + a_off[i] + ks * kBigK, (lds_ptr_t)(a_base + blk), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(B + b_off[i] + ks * kBigK, (lds_ptr_t)(b_base + blk), 16, 0, 0);
-    }
-  };
-  // Fragment addresses: row part (lane-dependent) plus the swizzled chunk of
-  // half-step kk; rows i*32 / j*32 further are +2048 bytes.
-  const int sw = ((lane & 31) >> 2) & 3;
-  const int a_row = (wm * 128 + (lane & 31)) * 64;
-  const int b_row = kBigTile + (wn * 64 + (lane & 31)) * 64;
-  const int koff[2] = {((lane >> 5) ^ sw) << 4, ((2 + (lane >> 5)) ^ sw) << 4};
-  struct F8 { bf16x8_t a[4], b[2]; };
-  auto read_frags = [&](int stage, int kk, F8& f) {
-    const char* base = smem + stage * kBigStage;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      f.a[i] = *reinterpret_cast<const bf16x8_t*>(base + a_row + koff[kk] + i * 2048);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      f.b[j] = *reinterpret_cast<const bf16x8_t*>(base + b_row + koff[kk] + j * 2048);
-  };
-  f32x16 acc[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  // 8 MFMAs on `cur` while the 6 fragment reads of `nxt` go out.
-  auto half_step = [&](const F8& cur, F8& nxt, int nstage, int nkk) {
-    read_frags(nstage, nkk, nxt);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur.a[i], cur.b[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int q = 0; q < 6; ++q) {
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
-  };
-  const int ksteps = K / kBigK;  // host guarantees ksteps % kStages == 0
-#pragma unroll
-  for (int s = 0; s < kStages; ++s) issue(s, s);
-  wait_vmcnt<8>();  // steps 0 and 1 landed (this thread's loads)
-  __syncthreads();
-  F8 f0, f1;
-  read_frags(0, 0, f0);
-  for (int ks0 = 0; ks0 < ksteps; ks0 += kStages) {
-#pragma unroll
-    for (int s = 0; s < kStages; ++s) {
-      const int ks = ks0 + s;
-      half_step(f0, f1, s, 1);                  // MFMAs k 0..15; read k 16..31
-      half_step(f1, f0, (s + 1) % kStages, 0);  // MFMAs k 16..31; read next step
-      // Own loads of step ks+2 landed: only step ks+3 may stay in flight.
-      if (ks + 3 < ksteps)
-        wait_vmcnt<4>();
-      else
-        wait_vmcnt<0>();
-      __syncthreads();
-      if (ks + kStages < ksteps) issue(ks + kStages, s);
-    }
-  }
-  // Epilogue.  Accumulator register r of lane l holds row
-  // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of its 32 x 32 tile.
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      const float sc = EPI == kEpiGelu ? scale[m] : 1.0f;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-        const size_t idx = static_cast<size_t>(m) * N + n;
-        float v = acc[i][j][r];
-        if (EPI == kEpiGelu)
-          v = gelu_tanh(v * sc);
-        else
-          v += bf16_to_f32(R[idx]);
-        C[idx] = f32_to_bf16(v);
-      }
-    }
-  }
-}
-
 // dst[c, r] = src[r, c] for a rows x cols bf16 matrix, through a 64 x 64
 // LDS tile.
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src,
