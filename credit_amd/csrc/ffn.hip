@@ -210,8 +210,8 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
 //    wave is done reading stage ks, which the following issue refills; the
 //    next step's first fragments (stage ks+1, published one step earlier)
 //    are read before it.
-//  - The K loop is unrolled over the kStages stages so every stage offset
-//    is a compile-time constant.
+//  - The stage index runs at run time (a scalar add per step), so K needs
+//    only to be a multiple of 32 and at least kStages steps.
 //  - LDS rows are 64 bytes (32 bf16 of K); the 16-byte chunk c of row r sits
 //    at position c ^ ((r >> 2) & 3), so the fragment reads of 16 consecutive
 //    rows (four rows share a 256-byte bank row) hit 16 distinct 4-bank groups
@@ -221,10 +221,14 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
 //   kEpiResidual: C = bf16(acc + R[m, n])
 constexpr int kBig = 256;
 constexpr int kBigK = 32;
-constexpr int kStages = 4;
+// Five K-steps in flight through LDS: the waits at the end of step ks need
+// step ks+2 and let ks+3 and ks+4 stay in flight, three steps of load lead
+// (four stages: two steps, measured 10% slower at C5).
+constexpr int kStages = 5;
 constexpr int kBigTile = kBig * kBigK * 2;   // one operand tile, bytes (16 KiB)
 constexpr int kBigStage = 2 * kBigTile;      // A and B tiles of one stage
-constexpr int kBigLds = kStages * kBigStage; // 128 KiB
+constexpr int kBigLds = kStages * kBigStage; // 160 KiB, the whole LDS
+static_assert(kStages == 5, "the wait counts in ffn_gemm256_kernel assume five stages");
 // Tile blocks within an XCD: 8 M-tiles x 4 N-tiles run concurrently and
 // share their A rows and B columns through that XCD's L2.
 constexpr int kGroupM = 8;
@@ -329,28 +333,30 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     }
     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
   };
-  const int ksteps = K / kBigK;  // host guarantees ksteps % kStages == 0
+  const int ksteps = K / kBigK;  // host guarantees ksteps >= kStages
 #pragma unroll
-  for (int s = 0; s < kStages; ++s) issue(s, s);
-  wait_vmcnt<8>();  // steps 0 and 1 landed (this thread's loads)
+  for (int st = 0; st < kStages; ++st) issue(st, st);
+  wait_vmcnt<4 * (kStages - 2)>();  // steps 0 and 1 landed (this thread's loads)
   __syncthreads();
   F8 f0, f1;
   read_frags(0, 0, f0);
-  for (int ks0 = 0; ks0 < ksteps; ks0 += kStages) {
-#pragma unroll
-    for (int s = 0; s < kStages; ++s) {
-      const int ks = ks0 + s;
-      half_step(f0, f1, s, 1);                  // MFMAs k 0..15; read k 16..31
-      half_step(f1, f0, (s + 1) % kStages, 0);  // MFMAs k 16..31; read next step
-      // Own loads of step ks+2 landed: only step ks+3 may stay in flight.
-      if (ks + 3 < ksteps)
-        wait_vmcnt<4>();
-      else
-        wait_vmcnt<0>();
-      __syncthreads();
-      if (ks + kStages < ksteps) issue(ks + kStages, s);
-    }
+  int s = 0;
+  for (int ks = 0; ks < ksteps; ++ks) {
+    const int sn = s + 1 == kStages ? 0 : s + 1;
+    half_step(f0, f1, s, 1);   // MFMAs k 0..15; read k 16..31
+    half_step(f1, f0, sn, 0);  // MFMAs k 16..31; read next step
+    // Own loads of step ks+2 landed: steps ks+3 and ks+4 may stay in flight.
+    if (ks + 4 < ksteps)
+      wait_vmcnt<8>();
+    else if (ks + 3 < ksteps)
+      wait_vmcnt<4>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
+    if (ks + kStages < ksteps) issue(ks + kStages, s);
+    s = sn;
   }
+
   // Epilogue.  Accumulator register r of lane l holds row
   // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of its 32 x 32 tile.
 #pragma unroll
@@ -395,7 +401,7 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
-// The 256-tile kernels take 128 KiB of dynamic LDS; allow it once per
+// The 256-tile kernels take 160 KiB of dynamic LDS; allow it once per
 // process (the attribute belongs to the kernel, not to a device).
 int enable_big_lds() {
   static int status = [] {
@@ -467,9 +473,8 @@ extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w
   const int M = static_cast<int>(rows), D = static_cast<int>(d), F = static_cast<int>(f);
   ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, D, eps);
   CREDIT_TRY(check_launch("ffn_rstd_kernel"));
-  // The 256-tile kernels: every dimension a multiple of 256 (so K / 32 is a
-  // multiple of kStages), tile counts a multiple of the 8 XCDs, 32-bit
-  // element offsets.
+  // The 256-tile kernels: every dimension a multiple of 256 (so K / 32 >=
+  // kStages), tile counts a multiple of the 8 XCDs, 32-bit element offsets.
   const bool big = M % kBig == 0 && D % kBig == 0 && F % kBig == 0 &&
                    ((M / kBig) * (F / kBig)) % 8 == 0 && ((M / kBig) * (D / kBig)) % 8 == 0 &&
                    static_cast<int64_t>(M) * F < (int64_t{1} << 31) &&
