@@ -72,6 +72,37 @@ def summarize(fetch: str, write: str, copy_fetch: str, copy_write: str,
             "kernels": kernels}
 
 
+def kernel_stats(path: str | Path) -> dict[str, dict[str, float]]:
+    """rocprofv3 ``--stats`` kernel summary (``*_kernel_stats.csv``) by short
+    kernel name: calls and average / min / max duration in microseconds."""
+    out: dict[str, dict[str, float]] = {}
+    with open(path, newline="") as fh:
+        for row in csv.DictReader(fh):
+            out[short_name(row["Name"])] = {
+                "calls": int(row["Calls"]),
+                "avg_us": float(row["AverageNs"]) / 1e3,
+                "min_us": float(row["MinNs"]) / 1e3,
+                "max_us": float(row["MaxNs"]) / 1e3,
+            }
+    return out
+
+
+def markdown_table(stats: dict[str, dict[str, float]], traffic: dict) -> str:
+    """One row per kernel of the trace: calls, durations and, where the PMC
+    runs saw the kernel, its HBM fetch and write in MB per dispatch."""
+    lines = ["| kernel | calls | avg us | min us | max us | HBM fetch MB | HBM write MB |",
+             "|---|---|---|---|---|---|---|"]
+    kern = traffic.get("kernels", {})
+    for name in sorted(stats, key=lambda n: -stats[n]["avg_us"] * stats[n]["calls"]):
+        st = stats[name]
+        tr = kern.get(name)
+        fetch = f"{tr['fetch_bytes'] / 1e6:.1f}" if tr else "-"
+        write = f"{tr['write_bytes'] / 1e6:.1f}" if tr else "-"
+        lines.append(f"| `{name}` | {st['calls']} | {st['avg_us']:.1f} | {st['min_us']:.1f} | "
+                     f"{st['max_us']:.1f} | {fetch} | {write} |")
+    return "\n".join(lines) + "\n"
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--fetch", required=True)
@@ -80,9 +111,15 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-write", required=True)
     ap.add_argument("--copy-bytes", type=int, required=True)
     ap.add_argument("--json", required=True)
+    ap.add_argument("--stats", help="rocprofv3 --stats kernel summary CSV of the same workload")
+    ap.add_argument("--markdown", help="write the per-kernel trace + traffic table here")
     args = ap.parse_args(argv)
     out = summarize(args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_bytes)
     Path(args.json).write_text(json.dumps(out, indent=1) + "\n")
+    if args.markdown:
+        if not args.stats:
+            ap.error("--markdown needs --stats")
+        Path(args.markdown).write_text(markdown_table(kernel_stats(args.stats), out))
     return 0
 
 
