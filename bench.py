@@ -42,6 +42,7 @@ CALL_KERNELS = {
     "ffn": ["ffn_rstd_kernel", "ffn_gemm256_kernel<0>", "ffn_gemm256_kernel<1>"],
     "layernorm_backward": ["layernorm_bwd_slice_kernel<float, 1024, 8>"],
     "layernorm_backward_bf16": ["layernorm_bwd_slice_kernel<unsigned short, 1024, 4>"],
+    "rowwise_quant": ["rowwise_quant_slice_kernel<1024, 16>"],
 }
 
 
@@ -220,6 +221,7 @@ VARIANT_SWEEP = {
     "softmax_logits_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
     "layernorm_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
     "layernorm_backward_bf16": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
+    "rowwise_quant": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
 }
 
 

@@ -309,6 +309,9 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
     case CREDIT_OP_SOFTMAX_LOGITS_BWD:
       body = softmax_workspace(op, rows, cols, variant, split, cus);
       break;
+    case CREDIT_OP_ROWWISE_QUANT:
+      body = rowwise_quant_workspace(rows, cols, variant, split, cus);
+      break;
     default:
       body = 0;
   }

@@ -74,7 +74,6 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
   constexpr int NW = THREADS / kWave;
   constexpr int E = V::kN;
   __shared__ double red[4][NW];
-  const int tid = threadIdx.x;
   SplitGroup g;
   // members == 1: one workgroup per row.  members > 1: a co-resident grid
   // of G groups; the member covers its slice of rows group, group + G, ...

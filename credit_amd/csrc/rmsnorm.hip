@@ -84,7 +84,6 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
     int members, int rows, float eps, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
   __shared__ double red[NW];
-  const int tid = threadIdx.x;
   SplitGroup g;
   // members == 1: one workgroup per row.  members > 1: a co-resident grid
   // of G groups; the member covers its slice of rows group, group + G, ...

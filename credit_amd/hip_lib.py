@@ -52,6 +52,7 @@ OPS = {
     "softmax_logits_backward": 8,
     "ffn": 9,
     "layernorm_backward_bf16": 10,
+    "rowwise_quant": 11,
 }
 
 
@@ -115,6 +116,7 @@ SIGNATURES: dict[str, list] = {
     "credit_softmax_fwd_f32": [_P, _P, _P, _P, _I64, _I64, _CFG],
     "credit_softmax_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_softmax_logits_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
+    "credit_rowwise_quant_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_ffn_rmsnorm_gelu_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
     "credit_layernorm_bwd_f32": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_layernorm_bwd_bf16": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
@@ -365,6 +367,22 @@ def softmax_logits_backward(logits: torch.Tensor, dy: torch.Tensor, dx: torch.Te
     )
 
 
+def rowwise_quant(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor,
+                  cfg: CreditCfg) -> None:
+    """fp32 rows in, int8 codes and one fp32 scale per row out."""
+    rows, cols = _rows_cols(x)
+    if tuple(q.shape) != (rows, cols):
+        raise ValueError(f"q: expected shape {(rows, cols)}, got {tuple(q.shape)}")
+    if scale.numel() != rows:
+        raise ValueError(f"scale: expected {rows} elements, got {scale.numel()}")
+    check(
+        load_library().credit_rowwise_quant_f32(
+            _ptr(x, "x", torch.float32), _ptr(q, "q", torch.int8),
+            _ptr(scale, "scale", torch.float32), rows, cols, ctypes.byref(cfg)),
+        "credit_rowwise_quant_f32",
+    )
+
+
 def layernorm_backward(x: torch.Tensor, dy: torch.Tensor, gamma: torch.Tensor,
                        dx: torch.Tensor, eps: float, cfg: CreditCfg) -> None:
     """fp32 or bf16 (all four tensors the same dtype)."""
@@ -477,6 +495,12 @@ def launch_softmax_logits_backward(inputs, outputs, config: LaunchConfig = Launc
     softmax_logits_backward(logits, dy, dx, make_cfg(config.variant, config.split))
 
 
+def launch_rowwise_quant(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    (x,) = inputs
+    q, scale = outputs
+    rowwise_quant(x, q, scale, make_cfg(config.variant, config.split))
+
+
 FFN_EPS = 1.0e-6
 
 
@@ -507,6 +531,7 @@ HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
     "softmax_fwd": launch_softmax_fwd,
     "softmax_bwd": launch_softmax_bwd,
     "softmax_logits_backward": launch_softmax_logits_backward,
+    "rowwise_quant": launch_rowwise_quant,
 }
 
 
@@ -552,6 +577,8 @@ def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch
         return torch.empty_like(x), torch.empty(x.shape[1], **f32)
     if name == "softmax_fwd":
         return torch.empty_like(x), torch.empty(rows, **f32), torch.empty(rows, **f32)
+    if name == "rowwise_quant":
+        return torch.empty(x.shape, device=x.device, dtype=torch.int8), torch.empty(rows, **f32)
     if name in ("softmax_bwd", "softmax_logits_backward", "ffn", "layernorm_backward",
                 "layernorm_backward_bf16"):
         return (torch.empty_like(x),)

@@ -55,6 +55,7 @@ SWEEP_WORKLOADS = (
     "softmax_logits_backward",
     "layernorm_backward",
     "layernorm_backward_bf16",
+    "rowwise_quant",
 )
 DEFAULT_N_VALUES = (4096, 8192, 16384, 32768, 65536, 131072, 262144)
 DEFAULT_SPLITS = (2, 4, 8, 16)
@@ -180,6 +181,8 @@ def variant_list(spec: WorkloadSpec, cols: int, splits: tuple[int, ...]):
 
 
 def _close(a: torch.Tensor, b: torch.Tensor) -> bool:
+    if not a.is_floating_point():
+        return bool(torch.equal(a, b))
     if a.dtype == torch.bfloat16:
         return bool(torch.allclose(a.float(), b.float(), rtol=1e-2, atol=1e-2, equal_nan=True))
     return bool(torch.allclose(a, b, rtol=1e-5, atol=1e-6, equal_nan=True))
@@ -202,7 +205,7 @@ def measure_point(name: str, spec: WorkloadSpec, rows: int, cols: int, cfg: RunC
         row = {"workload": name, "rows": rows, "cols": cols, "variant": variant, "split": split}
         try:
             for o in outs[0]:
-                o.fill_(float("nan"))
+                o.fill_(float("nan") if o.is_floating_point() else -128)
             launcher(sets[0], outs[0], lc)
             torch.cuda.synchronize()
             hip_lib.check_watchdog()

@@ -151,6 +151,10 @@ def make_softmax_logits_inputs(rows, cols, g):
     )
 
 
+def make_quant_inputs(rows, cols, g):
+    return (_uniform((rows, cols), -1.0, 1.0, g),)
+
+
 # -------------------------------------------------------------- registry --
 
 FP32_TOL = (1.0e-6, 1.0e-5)
@@ -315,6 +319,26 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=8,
         reductions_per_stage=(2, 1),
         staged_max_cols=32768,
+    ),
+    # dsmem_eval/workloads.py:150-154,203-211; metadata
+    # dsmem_eval/workload_metadata.py:32-34.  q is bit-exact; the scale is
+    # one fp32 division (max_abs / 127).
+    "rowwise_quant": WorkloadSpec(
+        name="rowwise_quant",
+        label="Row-wise int8 quantization",
+        category="quantization",
+        rows=4096,
+        cols=65536,
+        input_factory=make_quant_inputs,
+        output_names=("q", "scale"),
+        algorithmic_bytes=lambda r, c: 4 * r * c + r * c + 4 * r,
+        tolerances=(None, (1.0e-6, 1.0e-6)),
+        seed=1234,
+        modeled_bytes_per_element=9.0,
+        reread_bytes_per_element=4.0,
+        staged_bytes_per_element=4,
+        reductions_per_stage=(1,),
+        staged_max_cols=65536,
     ),
 }
 

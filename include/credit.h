@@ -82,6 +82,7 @@ typedef struct credit_cfg {
 #define CREDIT_OP_SOFTMAX_LOGITS_BWD 8
 #define CREDIT_OP_FFN 9
 #define CREDIT_OP_LAYERNORM_BWD_BF16 10
+#define CREDIT_OP_ROWWISE_QUANT 11
 
 /* ------------------------------------------------------------ library --- */
 
@@ -214,6 +215,21 @@ int credit_softmax_bwd_f32(const float* p, const float* dy, float* dx, int64_t r
  * ((max, sum), then sum p*dy); READ streams three passes. */
 int credit_softmax_logits_bwd_f32(const float* logits, const float* dy, float* dx,
                                   int64_t rows, int64_t cols, const credit_cfg* cfg);
+
+/* --------------------------------------- rowwise_quant (reference) -----
+ * q = int8(clamp(rint(x * inv), -127, 127)), inv = (1 / max_j |x_j|) * 127
+ * (0 for an all-zero row), scale = max_j |x_j| / 127, fp32 in: the reference
+ * workload rowwise_quant (dsmem_eval/workloads.py:150-154; kernels
+ * src/workloads/rowwise_quant.cu:260-363, launched per
+ * dsmem_eval/runner.py:280-310).  Bit-exact against the reference's torch
+ * function for finite x (inv rounds the reciprocal first, as torch
+ * evaluates 127.0 / max_abs).  x and q [rows, cols], scale [rows].
+ * Variants: STAGED holds rows <= 65536 columns; SPLIT exchanges the partial
+ * maximum once per row; READ reads x twice and takes any width and
+ * alignment (STAGED/SPLIT need cols % 4 == 0, x 16-byte and q 4-byte
+ * aligned). */
+int credit_rowwise_quant_f32(const float* x, int8_t* q, float* scale, int64_t rows,
+                             int64_t cols, const credit_cfg* cfg);
 
 /* ------------------------------------------ C5: norm-fused FFN ----------
  * out = bf16(x + bf16(GELU_tanh(bf16(x * rstd) @ W1^T)) @ W2^T) with

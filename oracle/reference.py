@@ -179,16 +179,23 @@ def lars_momentum(weight, grad, momentum):
 
 
 def rowwise_quant(x):
-    """(int8 q, fp32 scale), dsmem_eval/workloads.py:150-154.
+    """(int8 q, fp32 scale), dsmem_eval/workloads.py:150-154, for finite x.
 
     Computed in float32 like the reference (its inputs and scale are fp32);
     round-half-to-even as torch.round / nearbyintf
-    (src/workloads/rowwise_quant.cu:239-244).
+    (src/workloads/rowwise_quant.cu:239-244).  The reference's
+    ``127.0 / max_abs`` is a scalar divided by a tensor, which torch
+    evaluates as ``reciprocal(max_abs) * 127`` -- two fp32 roundings, not
+    one correctly rounded division (the CUDA file's ``kQMax / max_abs``,
+    rowwise_quant.cu:277, differs from it in about a quarter of rows) -- so
+    the oracle rounds the reciprocal first.  ``scale = max_abs / 127.0`` is a
+    tensor divided by a scalar: one correctly rounded division.
     """
     x = np.asarray(x, dtype=np.float32)
     max_abs = np.max(np.abs(x), axis=-1, keepdims=True)
     with np.errstate(divide="ignore"):
-        inv = np.where(max_abs > 0, np.float32(127.0) / max_abs, np.float32(0.0)).astype(np.float32)
+        recip = (np.float32(1.0) / max_abs).astype(np.float32)
+        inv = np.where(max_abs > 0, recip * np.float32(127.0), np.float32(0.0)).astype(np.float32)
     q = np.clip(np.rint(x * inv), -127, 127).astype(np.int8)
     return q, (max_abs / np.float32(127.0)).astype(np.float32)[..., 0]
 

@@ -64,6 +64,14 @@ def softmax_logits_backward(logits, dy):
     return p * (dy - (p * dy).sum(dim=-1, keepdim=True))
 
 
+def rowwise_quant(x):
+    """dsmem_eval/workloads.py:150-154 as written."""
+    max_abs = torch.amax(torch.abs(x), dim=-1, keepdim=True)
+    inv_scale = torch.where(max_abs > 0.0, 127.0 / max_abs, torch.zeros_like(max_abs))
+    q = torch.clamp(torch.round(x * inv_scale), -127.0, 127.0).to(torch.int8)
+    return q, (max_abs / 127.0).squeeze(-1)
+
+
 def ffn(x, w1, w2, eps=1.0e-6):
     a = F.rms_norm(x.float(), (x.shape[-1],), None, eps).to(x.dtype)
     h = F.gelu(a @ w1, approximate="tanh")
@@ -82,5 +90,6 @@ FUNCTIONS = {
     "layernorm_backward_bf16": lambda x, dy, g: layernorm_backward(
         x.float(), dy.float(), g.float()).to(x.dtype),
     "softmax_logits_backward": softmax_logits_backward,
+    "rowwise_quant": rowwise_quant,
     "ffn": ffn,
 }

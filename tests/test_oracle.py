@@ -163,6 +163,29 @@ def test_rowwise_quant_brute_force():
     assert np.all(np.abs(q[2] * scale[2] - x[2]) <= scale[2] / 2 + 1e-7)
 
 
+def test_rowwise_quant_matches_torch_operator_semantics():
+    """The reference's torch function (amax, scalar / tensor, round, clamp,
+    int8) on many random rows: q and scale bit-exact.  torch evaluates the
+    scalar / tensor as reciprocal * scalar, which a one-step division would
+    get wrong in about a quarter of the rows."""
+    g = torch.Generator().manual_seed(11)
+    x = (torch.rand(4096, 64, generator=g) * 2 - 1) * torch.rand(4096, 1, generator=g) * 8
+    x[7] = 0.0
+    # Rows whose elements land next to half-integers, (j + 0.5) * m / 127:
+    # there the last bit of the reciprocal decides the rounding (a one-step
+    # division gives a different q for ~12% of these elements).
+    m = torch.rand(2048, 1, generator=g) * 3.5 + 0.5
+    ties = (torch.arange(63, dtype=torch.float32)[None, :] + 0.5) * m / 127.0
+    x = torch.cat([x, torch.cat([ties, m], dim=1)])
+    max_abs = torch.amax(torch.abs(x), dim=-1, keepdim=True)
+    inv = torch.where(max_abs > 0.0, 127.0 / max_abs, torch.zeros_like(max_abs))
+    tq = torch.clamp(torch.round(x * inv), -127.0, 127.0).to(torch.int8)
+    tscale = (max_abs / 127.0).squeeze(-1)
+    q, scale = ref.rowwise_quant(x.numpy())
+    assert np.array_equal(q, tq.numpy())
+    assert np.array_equal(scale, tscale.numpy())
+
+
 def test_weighted_var_backward_matches_autograd():
     x = RNG.uniform(-2, 2, (4, 100))
     w = RNG.uniform(0.5, 1.5, (4, 100))
