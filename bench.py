@@ -36,7 +36,7 @@ CALL_KERNELS = {
     "layernorm_fwd": ["layernorm_fwd_staged_kernel<512, 8>"],
     "rmsnorm_fwd": ["rmsnorm_fwd_slice_kernel<1024, 8>"],
     "rmsnorm_bwd": ["rmsnorm_bwd_group_kernel<512, 2>", "rmsnorm_dw_reduce_kernel"],
-    "softmax_fwd": ["softmax_fwd_slice_kernel<1024, 16>"],
+    "softmax_fwd": ["softmax_fwd_group_kernel<512, 8>"],
     "softmax_bwd": ["softmax_bwd_slice_kernel<1024, 8>"],
     "softmax_logits_backward": ["softmax_logits_bwd_slice_kernel<1024, 8>"],
     "ffn": ["ffn_rstd_kernel", "ffn_gemm256_kernel<0>", "ffn_gemm256_kernel<1>"],
@@ -216,7 +216,7 @@ VARIANT_SWEEP = {
     "layernorm_fwd": [("read", 0), ("staged", 0)],
     "rmsnorm_fwd": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
     "rmsnorm_bwd": [("read", 0), ("split", 16), ("split", 18), ("split", 32), ("split", 37)],
-    "softmax_fwd": [("read", 0), ("split", 4), ("split", 8), ("split", 16)],
+    "softmax_fwd": [("read", 0), ("split", 4), ("split", 8), ("split", 16), ("split", 32)],
     "softmax_bwd": [("read", 0), ("split", 8), ("split", 16)],
     "softmax_logits_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
     "layernorm_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],

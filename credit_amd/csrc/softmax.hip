@@ -151,6 +151,197 @@ __global__ __launch_bounds__(THREADS) void softmax_fwd_slice_kernel(
   }
 }
 
+// One wave merges up to 64 (max, sum) partials, one per lane (`has`
+// false: no partial): M = max m_l, S = sum s_l e^(m_l - M), each term an
+// fp32 rescale summed in fp64 by a fixed tree; S rounded to fp32 once.  The
+// maximum propagates NaN; a lane with s = 0 adds nothing (also when its m
+// is -inf).  Every lane gets the result.
+__device__ __forceinline__ void merge_maxsum_lanes(bool has, float m, float s, float* M_out,
+                                                   float* S_out) {
+  const float M = wave_reduce(has ? m : kNegInf, MaxOp{});
+  const double term = has && s != 0.0f ? static_cast<double>(s) * exp_accurate(m - M) : 0.0;
+  *M_out = M;
+  *S_out = static_cast<float>(wave_reduce_sum_f64(term));
+}
+
+// SPLIT variant for rows wider than one workgroup: a co-resident wave of
+// row groups, each group P members that hold 1/P of every row of a block of
+// rows, pipelined four rows deep.  The workgroup is THREADS data lanes (VPT
+// f32x4 of the member's slice per lane and row) plus one communication wave.
+//
+// In the step of row i each data wave issues the loads of row i+3, reduces
+// row i+2 (loaded a step earlier) to its wave partial (m_w, s_w) -- m_w the
+// wave maximum, s_w = sum e^(x - m_w) -- replacing the row's values by
+// e^(x - m_w) in registers, and counts itself in with an LDS atomic; the
+// wave that arrives last merges the wave partials in wave order and
+// publishes the member's (m, s) of row i+2.  The communication wave polls
+// each row's exchange in order, merges the members' partials in member
+// order into the row's (M, S), writes them into a 4-entry LDS ring and
+// advances an LDS ready count.  A data wave then waits (LDS spin) for row
+// i's (M, S) and writes p = e^(x - m_w) * (e^(m_w - M) / S): one exponential
+// per element, the second pass a multiply.  Row i is published two steps
+// before it is needed, so the exchange round trip overlaps the loads and
+// stores of the rows around it, and no wave ever waits for another wave's
+// loads (vmcnt is per wave: the polling wave issues no row traffic).  LDS
+// slots of row k are reused by row k+4 only, which a wave reaches after row
+// k+3's total is ready, i.e. after every access to them for row k.  Every
+// wait ends: the poll is bounded (watchdog), and the ready count then still
+// advances.
+//
+// Row traffic goes through buffer resources whose num_records covers the
+// member's slice (0 for a row beyond the group): out-of-range lanes read
+// zeros, masked to -inf / 0, and drop their stores; no branch surrounds a
+// load or store, so the waitcnt pass keeps rows i+1..i+3 in flight.
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS + kWave)
+__attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void softmax_fwd_group_kernel(
+    const float* __restrict__ x, float* __restrict__ p, float* __restrict__ rowmax,
+    float* __restrict__ lse, int rows, int cols, int chunk, int members, int rows_per_group,
+    SplitArgs sa) {
+  constexpr int NW = THREADS / kWave;
+  __shared__ float wmax[4][NW];       // wave partials of row k at [(k - r0) & 3]
+  __shared__ double wsum[4][NW];
+  __shared__ float ring_m[4];         // group (M, S) of row k at [(k - r0) & 3]
+  __shared__ float ring_s[4];
+  __shared__ uint32_t arrivals[4];
+  __shared__ uint32_t ready;          // rows r0 .. r0 + ready - 1 have (M, S)
+  const int tid = threadIdx.x;
+  if (tid < 4) arrivals[tid] = 0;
+  if (tid == 0) ready = 0;
+  const SplitGroup g = split_join(sa, members, 2);  // its barrier covers the stores above
+  const int r0 = g.group * rows_per_group;
+  if (r0 >= rows) return;  // padding group
+  const int r1 = r0 + rows_per_group < rows ? r0 + rows_per_group : rows;
+  const int nvec = cols >> 2;
+  const int v0 = g.member * chunk;
+  const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  const uint32_t slice_bytes = static_cast<uint32_t>(vlen) * 16u;
+
+  if (__builtin_amdgcn_readfirstlane(tid) >= THREADS) {
+    // ---- communication wave: merge every row's member partials ----
+    const int lane = tid & (kWave - 1);
+    for (int k = r0; k < r1; ++k) {
+      const uint32_t bits = split_poll(g, k - r0, 2);
+      // Lane m < P holds member m's (m, s): s sits P lanes up.
+      const uint32_t sbits = static_cast<uint32_t>(__shfl(static_cast<int>(bits), lane + members));
+      float M, S;
+      merge_maxsum_lanes(lane < members, __builtin_bit_cast(float, bits),
+                         __builtin_bit_cast(float, sbits), &M, &S);
+      if (tid == THREADS) {
+        ring_m[(k - r0) & 3] = M;
+        ring_s[(k - r0) & 3] = S;
+        __hip_atomic_store(&ready, static_cast<uint32_t>(k - r0 + 1), __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (g.member == 0) {
+          rowmax[k] = M;
+          lse[k] = static_cast<float>(static_cast<double>(M) + ::log(static_cast<double>(S)));
+        }
+      }
+    }
+    return;
+  }
+
+  // ---- data waves ----
+  const int wid = tid / kWave;
+  const bool lead = (tid & (kWave - 1)) == 0;
+  const uint32_t lane_off = static_cast<uint32_t>(tid) * 16u;
+  constexpr uint32_t kStride = THREADS * 16u;  // bytes between a lane's vectors
+  struct Row {
+    f32x4 v[VPT];
+  };
+  Row b0, b1, b2, b3;
+  auto load_row = [&](Row& b, int r) {
+    const bool live = r < r1;
+    const size_t off = static_cast<size_t>(live ? r : r0) * cols + 4 * static_cast<size_t>(v0);
+    const buffer_rsrc_t xs = make_rsrc(x + off, live ? slice_bytes : 0u);
+#pragma unroll
+    for (int q = 0; q < VPT; ++q)
+      b.v[q] = __builtin_bit_cast(f32x4, buffer_load_nt(xs, lane_off + q * kStride));
+  };
+  // Row k -> e^(x - m_w) in place; the last wave in publishes the member's
+  // (m, s) of row k.
+  auto publish_row = [&](Row& b, int k) {
+    float lm = kNegInf;
+#pragma unroll
+    for (int q = 0; q < VPT; ++q)
+      lm = lane_off + q * kStride < slice_bytes ? fmax_nan(lm, max4(b.v[q])) : lm;
+    const float wm = wave_reduce(lm, MaxOp{});
+    float ls = 0.0f;
+    if (wm != kNegInf) {
+#pragma unroll
+      for (int q = 0; q < VPT; ++q) {
+        const f32x4 e = prob4(b.v[q], wm, 1.0f);
+        b.v[q] = lane_off + q * kStride < slice_bytes ? e : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        ls += (b.v[q].x + b.v[q].y) + (b.v[q].z + b.v[q].w);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < VPT; ++q) b.v[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const double ws = wave_reduce_sum_f64(static_cast<double>(ls));
+    const int slot = (k - r0) & 3;
+    uint32_t t = 0;
+    if (lead) {
+      wmax[slot][wid] = wm;
+      wsum[slot][wid] = ws;
+      t = __hip_atomic_fetch_add(&arrivals[slot], 1u, __ATOMIC_ACQ_REL,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (__builtin_amdgcn_readfirstlane(t) == NW - 1) {
+      // Last wave in: lane w merges wave w's partial.
+      const int lane = tid & (kWave - 1);
+      const bool has = lane < NW;
+      float M, S;
+      merge_maxsum_lanes(has, has ? wmax[slot][lane] : kNegInf,
+                         has ? static_cast<float>(wsum[slot][lane]) : 0.0f, &M, &S);
+      if (lead) {
+        arrivals[slot] = 0;
+        split_publish_at(g, k - r0, 0, M);
+        split_publish_at(g, k - r0, 1, S);
+      }
+    }
+  };
+  auto finish_row = [&](const Row& b, int r) {
+    const int slot = (r - r0) & 3;
+    const uint32_t need = static_cast<uint32_t>(r - r0 + 1);
+    while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < need)
+      __builtin_amdgcn_s_sleep(1);
+    const float M = ring_m[slot];
+    const float S = ring_s[slot];
+    // e^(m_w - M) / S; 0/0 (NaN) for a row of -inf, as torch.softmax.
+    const float mw = wmax[slot][wid];
+    const float f = (mw == kNegInf ? 0.0f : exp_accurate(mw - M)) / S;
+    const size_t off = static_cast<size_t>(r) * cols + 4 * static_cast<size_t>(v0);
+    const buffer_rsrc_t out = make_rsrc(p + off, slice_bytes);
+#pragma unroll
+    for (int q = 0; q < VPT; ++q)
+      buffer_store_nt(out, lane_off + q * kStride, __builtin_bit_cast(u32x4, b.v[q] * f));
+  };
+  auto step = [&](Row& cur, Row& r2, Row& fut, int i) {
+    load_row(fut, i + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 2 < r1) publish_row(r2, i + 2);
+    finish_row(cur, i);
+  };
+
+  load_row(b0, r0);
+  load_row(b1, r0 + 1);
+  load_row(b2, r0 + 2);
+  publish_row(b0, r0);
+  if (r0 + 1 < r1) publish_row(b1, r0 + 1);
+  // Rotate the four buffers through statically named registers.
+  int i = r0;
+  for (; i + 3 < r1; i += 4) {
+    step(b0, b2, b3, i);
+    step(b1, b3, b0, i + 1);
+    step(b2, b0, b1, i + 2);
+    step(b3, b1, b2, i + 3);
+  }
+  if (i < r1) step(b0, b2, b3, i);
+  if (i + 1 < r1) step(b1, b3, b0, i + 1);
+  if (i + 2 < r1) step(b2, b0, b1, i + 2);
+}
+
 // Streaming forward: online (max, sum) pass, then the output pass.  VEC:
 // f32x4 loads (cols % 4 == 0, 16-byte aligned rows); else element loads.
 template <int THREADS, bool VEC>
@@ -453,6 +644,71 @@ const Pick<BwdFn> kLogits[] = {
 constexpr int64_t kFwdCapacity = 16384;
 constexpr int64_t kBwdCapacity = 8192;
 
+// Forward group kernel (SPLIT on rows wider than one workgroup): four row
+// buffers of VPT f32x4 per lane; 448-512 data lanes + 1 wave give two
+// workgroups per CU, 960 + 1 one.
+using FwdGroupFn = void (*)(const float*, float*, float*, float*, int, int, int, int, int,
+                            SplitArgs);
+const Pick<FwdGroupFn> kFwdGroup[] = {
+    {softmax_fwd_group_kernel<64, 4>, 64, 256},
+    {softmax_fwd_group_kernel<128, 4>, 128, 512},
+    {softmax_fwd_group_kernel<192, 4>, 192, 768},
+    {softmax_fwd_group_kernel<448, 4>, 448, 1792},
+    {softmax_fwd_group_kernel<512, 4>, 512, 2048},
+    {softmax_fwd_group_kernel<960, 4>, 960, 3840},
+    {softmax_fwd_group_kernel<512, 8>, 512, 4096},
+};
+constexpr int64_t kFwdGroupCapacity = 4096;
+// Slot rows per group: a member publishes row k two steps before it needs
+// row k's total and reaches row k + 16 only after every member has polled
+// row k.
+constexpr int kGroupRing = 16;
+constexpr int kMaxGroupMembers = kMaxExchangeValues / 2;  // (m, s) per member
+
+bool fwd_group_ok(const Plan& plan) {
+  return plan.variant == CREDIT_VARIANT_SPLIT && plan.members <= kMaxGroupMembers &&
+         plan.chunk <= kFwdGroupCapacity;
+}
+
+// Forward plan.  AUTO on a row wider than one workgroup takes the group
+// kernel with the fewest members (a power of two) whose slices fit it:
+// fewer members wait for fewer stragglers at every row (measured at
+// 512 x 262144: 16 members 212 us, 32 members 239 us, the 4-member slice
+// kernel without the pipeline 249 us).
+int resolve_fwd(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
+  const int64_t nvec = cols / 4;
+  if (cfg_variant(cfg) == CREDIT_VARIANT_AUTO && vec && nvec > kFwdCapacity) {
+    int p = 2;
+    while (p * kFwdGroupCapacity < nvec) p *= 2;
+    if (p <= kMaxGroupMembers) {
+      const int64_t chunk = (nvec + p - 1) / p;
+      *plan = Plan{CREDIT_VARIANT_SPLIT, static_cast<int>((nvec + chunk - 1) / chunk), chunk};
+      return CREDIT_OK;
+    }
+  }
+  return resolve(cfg, cols, vec, kFwdCapacity, "softmax_fwd", plan);
+}
+
+// Rows per group and groups of a group-kernel launch: as many groups as
+// fit the device at once (a multiple of kDispensers), each taking a
+// contiguous block of rows.
+int plan_row_groups(const void* fn, int threads, int members, int64_t rows, int* rows_per_group,
+                    int64_t* groups, const char* name) {
+  int64_t fit = 0;
+  CREDIT_TRY(coresident_groups(fn, threads, 0, members, &fit));
+  if (fit == 0)
+    return set_error(CREDIT_ERR_UNSUPPORTED, "%s: %d groups of %d members do not fit the device",
+                     name, kDispensers, members);
+  const int64_t g = fit < padded_groups(rows) ? fit : padded_groups(rows);
+  const int64_t r = (rows + g - 1) / g;
+  if (r > (int64_t{1} << 30))
+    return set_error(CREDIT_ERR_BAD_SHAPE, "%s: %lld rows per group", name,
+                     static_cast<long long>(r));
+  *rows_per_group = static_cast<int>(r);
+  *groups = padded_groups((rows + r - 1) / r);
+  return CREDIT_OK;
+}
+
 }  // namespace
 
 size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int split,
@@ -460,8 +716,15 @@ size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int sp
   credit_cfg c{nullptr, variant, split, nullptr, 0};
   Plan p;
   const int64_t cap = op == CREDIT_OP_SOFTMAX_FWD ? kFwdCapacity : kBwdCapacity;
-  if (resolve(&c, cols, cols % 4 == 0, cap, "softmax", &p) != CREDIT_OK) return 0;
+  const int st = op == CREDIT_OP_SOFTMAX_FWD ? resolve_fwd(&c, cols, cols % 4 == 0, &p)
+                                             : resolve(&c, cols, cols % 4 == 0, cap, "softmax", &p);
+  if (st != CREDIT_OK) return 0;
   const int k = op == CREDIT_OP_SOFTMAX_BWD ? 1 : 2;
+  if (op == CREDIT_OP_SOFTMAX_FWD && fwd_group_ok(p)) {
+    int64_t groups = coresident_groups_bound(p.members, cu_count);
+    if (groups > padded_groups(rows)) groups = padded_groups(rows);
+    return split_workspace_bytes(groups, p.members, 2, kGroupRing, 0);
+  }
   return slice_workspace(rows, p, k, cu_count);
 }
 
@@ -481,7 +744,7 @@ extern "C" int credit_softmax_fwd_f32(const float* x, float* p, float* rowmax, f
   CREDIT_TRY(check_cfg(cfg));
   if (rows == 0) return CREDIT_OK;
   Plan plan;
-  CREDIT_TRY(resolve(cfg, cols, vec_ok(cols, {x, p}), kFwdCapacity, "softmax_fwd", &plan));
+  CREDIT_TRY(resolve_fwd(cfg, cols, vec_ok(cols, {x, p}), &plan));
   hipStream_t stream = cfg_stream(cfg);
   const int c = static_cast<int>(cols);
   const unsigned r = static_cast<unsigned>(rows);
@@ -491,6 +754,22 @@ extern "C" int credit_softmax_fwd_f32(const float* x, float* p, float* rowmax, f
     else
       softmax_fwd_read_kernel<256, false><<<r, 256, 0, stream>>>(x, p, rowmax, lse, c);
     return check_launch("softmax_fwd_read_kernel");
+  }
+  if (fwd_group_ok(plan)) {
+    const Pick<FwdGroupFn>* gk = pick_for(kFwdGroup, plan.chunk);
+    const int threads = gk->threads + kWave;
+    int rpg = 0;
+    int64_t groups = 0;
+    CREDIT_TRY(plan_row_groups(reinterpret_cast<const void*>(gk->fn), threads, plan.members, rows,
+                               &rpg, &groups, "softmax_fwd_group_kernel"));
+    SplitWorkspace ws;
+    CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 2, kGroupRing, 0, &ws));
+    const uint32_t total = static_cast<uint32_t>(groups * plan.members);
+    hipLaunchKernelGGL(gk->fn, dim3(total), dim3(threads), 0, stream, x, p, rowmax, lse,
+                       static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members, rpg,
+                       SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
+                                 next_split_epoch(static_cast<uint32_t>(rpg)), kGroupRing});
+    return check_launch("softmax_fwd_group_kernel");
   }
   const Pick<FwdFn>* pk = pick_for(kFwd, plan.chunk);
   return launch_slices<FwdFn>(
