@@ -43,6 +43,9 @@ CALL_KERNELS = {
     "layernorm_backward": ["layernorm_bwd_slice_kernel<float, 1024, 8>"],
     "layernorm_backward_bf16": ["layernorm_bwd_slice_kernel<unsigned short, 1024, 4>"],
     "rowwise_quant": ["rowwise_quant_slice_kernel<1024, 16>"],
+    "lars_momentum": ["lars_slice_kernel<512, 8>"],
+    "weighted_var_backward": ["wvar_bwd_slice_kernel<1024, 4>"],
+    "pearson_backward": ["pearson_bwd_slice_kernel<512, 8>"],
 }
 
 
@@ -222,6 +225,9 @@ VARIANT_SWEEP = {
     "layernorm_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
     "layernorm_backward_bf16": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
     "rowwise_quant": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
+    "lars_momentum": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
+    "weighted_var_backward": [("read", 0), ("split", 4), ("split", 8), ("split", 12)],
+    "pearson_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
 }
 
 

@@ -312,6 +312,15 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
     case CREDIT_OP_ROWWISE_QUANT:
       body = rowwise_quant_workspace(rows, cols, variant, split, cus);
       break;
+    case CREDIT_OP_LARS_MOMENTUM:
+      body = lars_workspace(rows, cols, variant, split, cus);
+      break;
+    case CREDIT_OP_WEIGHTED_VAR_BWD:
+      body = wvar_bwd_workspace(rows, cols, variant, split, cus);
+      break;
+    case CREDIT_OP_PEARSON_BWD:
+      body = pearson_bwd_workspace(rows, cols, variant, split, cus);
+      break;
     default:
       body = 0;
   }

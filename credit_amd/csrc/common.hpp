@@ -153,6 +153,27 @@ __device__ __forceinline__ double block_reduce_sum_f64(double v, double* slots) 
   return r;
 }
 
+// K sums over the workgroup in one LDS round (one barrier): each wave
+// deposits its K wave sums, then lane w < NW of every wave loads wave w's
+// sum of value k and a second wave reduction folds them -- K LDS reads per
+// lane instead of K*NW, which keeps the register footprint of several
+// simultaneous sums flat in the workgroup size.  Fixed order: the result is
+// deterministic and the same in every lane.  `slots` is [K][NW] and must not
+// be reused before a later barrier.
+template <int NW, int K>
+__device__ __forceinline__ void block_reduce_sum_f64_multi(double (&v)[K], double (*slots)[NW]) {
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int k = 0; k < K; ++k) v[k] = wave_reduce_sum_f64(v[k]);
+  if (lane == 0)
+#pragma unroll
+    for (int k = 0; k < K; ++k) slots[k][wave] = v[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < K; ++k) v[k] = wave_reduce_sum_f64(lane < NW ? slots[k][lane] : 0.0);
+}
+
 // --------------------------------------------------- memory access helpers
 // Native clang vectors: the nontemporal builtins (global_load/store with the
 // nt bit) accept these, not HIP's struct-wrapped float4/uint4.

@@ -36,6 +36,19 @@ __device__ __forceinline__ Slice slice_of(SplitGroup* g, int members, int k_valu
   return s;
 }
 
+// Buffer resource over this member's slice of a row of f32x4 vectors:
+// loads beyond it return zeros and stores beyond it are dropped, so slice
+// kernels need no per-lane bounds branch around their row traffic.
+__device__ __forceinline__ buffer_rsrc_t slice_rsrc(const float* row, const Slice& s) {
+  return make_rsrc(row + 4 * static_cast<size_t>(s.v0), static_cast<uint32_t>(s.vlen) * 16u);
+}
+__device__ __forceinline__ f32x4 slice_load(buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_bit_cast(f32x4, buffer_load_nt(r, offset));
+}
+__device__ __forceinline__ void slice_store(buffer_rsrc_t r, uint32_t offset, f32x4 v) {
+  buffer_store_nt(r, offset, __builtin_bit_cast(u32x4, v));
+}
+
 template <class Fn>
 struct Pick {
   Fn fn;
@@ -63,10 +76,12 @@ struct Plan {
   int64_t chunk;
 };
 
-// Variant resolution shared by the three operations; `capacity` is the
-// widest slice (f32x4) one workgroup holds.
+// Variant resolution shared by the slice operations; `capacity` is the
+// widest slice (f32x4) one workgroup holds.  AUTO on a row wider than that
+// splits it into slices of at most `auto_capacity` (default: capacity):
+// smaller slices run on smaller workgroups, two of which share a CU.
 inline int resolve(const credit_cfg* cfg, int64_t cols, bool vec, int64_t capacity, const char* op,
-            Plan* plan) {
+                   Plan* plan, int64_t auto_capacity = 0) {
   const int variant = cfg_variant(cfg);
   const int64_t nvec = cols / 4;
   if (variant == CREDIT_VARIANT_READ || (!vec && variant == CREDIT_VARIANT_AUTO)) {
@@ -85,7 +100,8 @@ inline int resolve(const credit_cfg* cfg, int64_t cols, bool vec, int64_t capaci
                        op, static_cast<long long>(capacity * 4));
     p = 1;
   } else if (variant == CREDIT_VARIANT_AUTO) {
-    p = need;
+    const int64_t cap = auto_capacity > 0 && need > 1 ? auto_capacity : capacity;
+    p = static_cast<int>((nvec + cap - 1) / cap);
   } else {
     p = cfg_split(cfg);
     if (p == 0) p = need < 2 ? 2 : need;

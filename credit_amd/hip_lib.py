@@ -53,6 +53,9 @@ OPS = {
     "ffn": 9,
     "layernorm_backward_bf16": 10,
     "rowwise_quant": 11,
+    "lars_momentum": 12,
+    "weighted_var_backward": 13,
+    "pearson_backward": 14,
 }
 
 
@@ -117,6 +120,9 @@ SIGNATURES: dict[str, list] = {
     "credit_softmax_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_softmax_logits_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_rowwise_quant_f32": [_P, _P, _P, _I64, _I64, _CFG],
+    "credit_lars_momentum_f32": [_P, _P, _P, _P, _P, _I64, _I64, _CFG],
+    "credit_weighted_var_bwd_f32": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
+    "credit_pearson_bwd_f32": [_P, _P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_ffn_rmsnorm_gelu_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
     "credit_layernorm_bwd_f32": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_layernorm_bwd_bf16": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
@@ -383,6 +389,60 @@ def rowwise_quant(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor,
     )
 
 
+def _same_shape(name: str, t: torch.Tensor, shape: tuple[int, int]) -> None:
+    if tuple(t.shape) != shape:
+        raise ValueError(f"{name}: expected shape {shape}, got {tuple(t.shape)}")
+
+
+def lars_momentum(weight: torch.Tensor, grad: torch.Tensor, momentum: torch.Tensor,
+                  weight_out: torch.Tensor, update_out: torch.Tensor, cfg: CreditCfg) -> None:
+    """fp32 [rows, cols] in and out."""
+    rows, cols = _rows_cols(weight)
+    for name, t in (("grad", grad), ("momentum", momentum), ("weight_out", weight_out),
+                    ("update_out", update_out)):
+        _same_shape(name, t, (rows, cols))
+    f32 = torch.float32
+    check(
+        load_library().credit_lars_momentum_f32(
+            _ptr(weight, "weight", f32), _ptr(grad, "grad", f32), _ptr(momentum, "momentum", f32),
+            _ptr(weight_out, "weight_out", f32), _ptr(update_out, "update_out", f32), rows, cols,
+            ctypes.byref(cfg)),
+        "credit_lars_momentum_f32",
+    )
+
+
+def weighted_var_backward(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor,
+                          dx: torch.Tensor, eps: float, cfg: CreditCfg) -> None:
+    """fp32 [rows, cols] in and out."""
+    rows, cols = _rows_cols(x)
+    for name, t in (("weight", weight), ("dy", dy), ("dx", dx)):
+        _same_shape(name, t, (rows, cols))
+    f32 = torch.float32
+    check(
+        load_library().credit_weighted_var_bwd_f32(
+            _ptr(x, "x", f32), _ptr(weight, "weight", f32), _ptr(dy, "dy", f32),
+            _ptr(dx, "dx", f32), rows, cols, eps, ctypes.byref(cfg)),
+        "credit_weighted_var_bwd_f32",
+    )
+
+
+def pearson_backward(x: torch.Tensor, y: torch.Tensor, grad: torch.Tensor, dx: torch.Tensor,
+                     dy: torch.Tensor, eps: float, cfg: CreditCfg) -> None:
+    """x, y, dx, dy fp32 [rows, cols]; grad fp32 with one value per row."""
+    rows, cols = _rows_cols(x)
+    for name, t in (("y", y), ("dx", dx), ("dy", dy)):
+        _same_shape(name, t, (rows, cols))
+    if grad.numel() != rows:
+        raise ValueError(f"grad: expected {rows} elements, got {grad.numel()}")
+    f32 = torch.float32
+    check(
+        load_library().credit_pearson_bwd_f32(
+            _ptr(x, "x", f32), _ptr(y, "y", f32), _ptr(grad, "grad", f32), _ptr(dx, "dx", f32),
+            _ptr(dy, "dy", f32), rows, cols, eps, ctypes.byref(cfg)),
+        "credit_pearson_bwd_f32",
+    )
+
+
 def layernorm_backward(x: torch.Tensor, dy: torch.Tensor, gamma: torch.Tensor,
                        dx: torch.Tensor, eps: float, cfg: CreditCfg) -> None:
     """fp32 or bf16 (all four tensors the same dtype)."""
@@ -501,6 +561,26 @@ def launch_rowwise_quant(inputs, outputs, config: LaunchConfig = LaunchConfig())
     rowwise_quant(x, q, scale, make_cfg(config.variant, config.split))
 
 
+def launch_lars_momentum(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    lars_momentum(*inputs, *outputs, make_cfg(config.variant, config.split))
+
+
+WEIGHTED_VAR_EPS = 1.0e-5  # dsmem_eval/workloads.py:74,78
+PEARSON_EPS = 1.0e-6       # dsmem_eval/workloads.py:104-105
+
+
+def launch_weighted_var_backward(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    x, w, dy = inputs
+    (dx,) = outputs
+    weighted_var_backward(x, w, dy, dx, WEIGHTED_VAR_EPS, make_cfg(config.variant, config.split))
+
+
+def launch_pearson_backward(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    x, y, grad = inputs
+    dx, dy = outputs
+    pearson_backward(x, y, grad, dx, dy, PEARSON_EPS, make_cfg(config.variant, config.split))
+
+
 FFN_EPS = 1.0e-6
 
 
@@ -532,6 +612,9 @@ HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
     "softmax_bwd": launch_softmax_bwd,
     "softmax_logits_backward": launch_softmax_logits_backward,
     "rowwise_quant": launch_rowwise_quant,
+    "lars_momentum": launch_lars_momentum,
+    "weighted_var_backward": launch_weighted_var_backward,
+    "pearson_backward": launch_pearson_backward,
 }
 
 
@@ -579,6 +662,10 @@ def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch
         return torch.empty_like(x), torch.empty(rows, **f32), torch.empty(rows, **f32)
     if name == "rowwise_quant":
         return torch.empty(x.shape, device=x.device, dtype=torch.int8), torch.empty(rows, **f32)
+    if name in ("lars_momentum", "pearson_backward"):
+        return torch.empty_like(x), torch.empty_like(x)
+    if name == "weighted_var_backward":
+        return (torch.empty_like(x),)
     if name in ("softmax_bwd", "softmax_logits_backward", "ffn", "layernorm_backward",
                 "layernorm_backward_bf16"):
         return (torch.empty_like(x),)

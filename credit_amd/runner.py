@@ -56,6 +56,9 @@ SWEEP_WORKLOADS = (
     "layernorm_backward",
     "layernorm_backward_bf16",
     "rowwise_quant",
+    "lars_momentum",
+    "weighted_var_backward",
+    "pearson_backward",
 )
 DEFAULT_N_VALUES = (4096, 8192, 16384, 32768, 65536, 131072, 262144)
 DEFAULT_SPLITS = (2, 4, 8, 16)

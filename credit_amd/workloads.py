@@ -155,6 +155,31 @@ def make_quant_inputs(rows, cols, g):
     return (_uniform((rows, cols), -1.0, 1.0, g),)
 
 
+def make_lars_inputs(rows, cols, g):
+    """weight, grad, momentum ~ U(-1, 1) (dsmem_eval/workloads.py:128-133)."""
+    return tuple(_uniform((rows, cols), -1.0, 1.0, g) for _ in range(3))
+
+
+def make_weighted_var_inputs(rows, cols, g):
+    """x ~ U(-2, 2), weight ~ U(0.5, 1.5), dy ~ U(-1, 1)
+    (dsmem_eval/workloads.py:64-69)."""
+    return (
+        _uniform((rows, cols), -2.0, 2.0, g),
+        _uniform((rows, cols), 0.5, 1.5, g),
+        _uniform((rows, cols), -1.0, 1.0, g),
+    )
+
+
+def make_pearson_inputs(rows, cols, g):
+    """x, y ~ U(-1, 1), grad ~ U(0.75, 1.25) per row
+    (dsmem_eval/workloads.py:88-93)."""
+    return (
+        _uniform((rows, cols), -1.0, 1.0, g),
+        _uniform((rows, cols), -1.0, 1.0, g),
+        _uniform((rows, 1), 0.75, 1.25, g),
+    )
+
+
 # -------------------------------------------------------------- registry --
 
 FP32_TOL = (1.0e-6, 1.0e-5)
@@ -339,6 +364,64 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=4,
         reductions_per_stage=(1,),
         staged_max_cols=65536,
+    ),
+    # dsmem_eval/workloads.py:128-143,194-202.  This build's READ variant
+    # streams w, g, m twice (24 B) and writes w', u (8 B); staging w and u
+    # saves the 12-byte re-read.
+    "lars_momentum": WorkloadSpec(
+        name="lars_momentum",
+        label="LARS momentum",
+        category="optimizer",
+        rows=4096,
+        cols=65536,
+        input_factory=make_lars_inputs,
+        output_names=("weight_out", "update"),
+        algorithmic_bytes=lambda r, c: 4 * r * c * 5,
+        tolerances=(FP32_TOL, FP32_TOL),
+        seed=1234,
+        modeled_bytes_per_element=32.0,
+        reread_bytes_per_element=12.0,
+        staged_bytes_per_element=8,
+        reductions_per_stage=(2,),
+        staged_max_cols=32768,
+    ),
+    # dsmem_eval/workloads.py:64-85,167-175.  One exchange of five sums per
+    # row (the reference: three stages, (2, 1, 2)).
+    "weighted_var_backward": WorkloadSpec(
+        name="weighted_var_backward",
+        label="Weighted variance backward",
+        category="normalization",
+        rows=4096,
+        cols=65536,
+        input_factory=make_weighted_var_inputs,
+        output_names=("dx",),
+        algorithmic_bytes=lambda r, c: 4 * r * c * 4,
+        tolerances=(FP32_TOL,),
+        seed=1234,
+        modeled_bytes_per_element=28.0,
+        reread_bytes_per_element=12.0,
+        staged_bytes_per_element=12,
+        reductions_per_stage=(5,),
+        staged_max_cols=16384,
+    ),
+    # dsmem_eval/workloads.py:88-112,176-184.  One exchange of five sums per
+    # row (the reference: two stages, (2, 3)).
+    "pearson_backward": WorkloadSpec(
+        name="pearson_backward",
+        label="Pearson backward",
+        category="pairwise statistics",
+        rows=4096,
+        cols=65536,
+        input_factory=make_pearson_inputs,
+        output_names=("dx", "dy"),
+        algorithmic_bytes=lambda r, c: 4 * r * c * 4 + 4 * r,
+        tolerances=(FP32_TOL, FP32_TOL),
+        seed=1234,
+        modeled_bytes_per_element=24.0,
+        reread_bytes_per_element=8.0,
+        staged_bytes_per_element=8,
+        reductions_per_stage=(5,),
+        staged_max_cols=32768,
     ),
 }
 

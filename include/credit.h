@@ -83,6 +83,9 @@ typedef struct credit_cfg {
 #define CREDIT_OP_FFN 9
 #define CREDIT_OP_LAYERNORM_BWD_BF16 10
 #define CREDIT_OP_ROWWISE_QUANT 11
+#define CREDIT_OP_LARS_MOMENTUM 12
+#define CREDIT_OP_WEIGHTED_VAR_BWD 13
+#define CREDIT_OP_PEARSON_BWD 14
 
 /* ------------------------------------------------------------ library --- */
 
@@ -230,6 +233,45 @@ int credit_softmax_logits_bwd_f32(const float* logits, const float* dy, float* d
  * aligned). */
 int credit_rowwise_quant_f32(const float* x, int8_t* q, float* scale, int64_t rows,
                              int64_t cols, const credit_cfg* cfg);
+
+/* --------------------------------------- lars_momentum (reference) -----
+ * u = 0.9 m + g + 0.01 w (fp32, torch's operation order: bit-exact),
+ * trust = 0.02 ||w|| / (||u|| + 1e-6) per row, w' = w - 1e-3 trust u: the
+ * reference workload lars_momentum (dsmem_eval/workloads.py:136-143; kernels
+ * src/workloads/lars_momentum.cu:283-416, launched per
+ * dsmem_eval/runner.py:280-310).  weight, grad, momentum in; weight_out
+ * (w') and update_out (u) out, all fp32 [rows, cols].  Variants: STAGED
+ * holds w and u for rows <= 32768 columns; SPLIT exchanges the two sums of
+ * squares once per row; READ streams the inputs twice, any width. */
+int credit_lars_momentum_f32(const float* weight, const float* grad, const float* momentum,
+                             float* weight_out, float* update_out, int64_t rows, int64_t cols,
+                             const credit_cfg* cfg);
+
+/* ------------------------------- weighted_var_backward (reference) -----
+ * dx of y = (x - mean_w) / sqrt(var_w + eps) with row weights w (the
+ * weighted mean and variance normalised by sum w + eps): the reference
+ * workload weighted_var_backward (dsmem_eval/workloads.py:72-85; kernels
+ * src/workloads/weighted_var_backward.cu:303-506, launched per
+ * dsmem_eval/runner.py:280-310).  x, weight, dy, dx fp32 [rows, cols]; eps
+ * > 0 (the reference's torch function uses 1e-5).  One exchange of five
+ * sums per row (SPLIT: at most 12 members); STAGED holds x, w and dy for
+ * rows <= 16384 columns; READ streams the inputs twice, any width. */
+int credit_weighted_var_bwd_f32(const float* x, const float* weight, const float* dy,
+                                float* dx, int64_t rows, int64_t cols, float eps,
+                                const credit_cfg* cfg);
+
+/* ------------------------------------ pearson_backward (reference) -----
+ * Gradients of the row-wise Pearson correlation of x and y, scaled by the
+ * row's upstream grad: the reference workload pearson_backward
+ * (dsmem_eval/workloads.py:96-112; kernels
+ * src/workloads/pearson_backward.cu:311-482, launched per
+ * dsmem_eval/runner.py:280-310).  x, y, dx, dy fp32 [rows, cols]; grad fp32
+ * [rows]; eps > 0 (the torch function uses 1e-6).  One exchange of five
+ * sums per row (SPLIT: at most 12 members); STAGED holds x and y for rows
+ * <= 32768 columns; READ streams the inputs twice, any width. */
+int credit_pearson_bwd_f32(const float* x, const float* y, const float* grad, float* dx,
+                           float* dy, int64_t rows, int64_t cols, float eps,
+                           const credit_cfg* cfg);
 
 /* ------------------------------------------ C5: norm-fused FFN ----------
  * out = bf16(x + bf16(GELU_tanh(bf16(x * rstd) @ W1^T)) @ W2^T) with

@@ -278,3 +278,43 @@ def layernorm_backward_init(rows: int, cols: int):
     col = np.arange(cols)
     gamma = np.float32(0.75) + (col % 31).astype(np.float32) * np.float32(0.015625)
     return x.reshape(rows, cols), dy.reshape(rows, cols), gamma.astype(np.float32)
+
+
+def hash_lcg_c(idx) -> np.ndarray:
+    """(idx*22695477 + 1) >> 16 (lars_momentum.cu:268-269)."""
+    i = np.asarray(idx, dtype=np.uint64)
+    return ((i * np.uint64(22695477) + np.uint64(1)) >> np.uint64(16)).astype(np.uint32)
+
+
+def _grid(bits, mask: int, scale: float, offset: float) -> np.ndarray:
+    return (bits & mask).astype(np.float32) * np.float32(scale) + np.float32(offset)
+
+
+def lars_momentum_init(rows: int, cols: int):
+    """weight, grad, momentum of src/workloads/lars_momentum.cu:257-275."""
+    idx = np.arange(rows * cols, dtype=np.uint64)
+    w = _grid(hash_lcg_a(idx), 2047, 1.0 / 1024.0, -1.0)
+    g = _grid(hash_lcg_b(idx), 2047, 1.0 / 1024.0, -1.0)
+    m = _grid(hash_lcg_c(idx), 2047, 1.0 / 1024.0, -1.0)
+    return w.reshape(rows, cols), g.reshape(rows, cols), m.reshape(rows, cols)
+
+
+def weighted_var_backward_init(rows: int, cols: int):
+    """x, weight, dy of src/workloads/weighted_var_backward.cu:253-285."""
+    idx = np.arange(rows * cols, dtype=np.uint64)
+    base = _grid(hash_lcg_a(idx), 4095, 1.0 / 1024.0, -2.0)
+    tiny = (hash_lcg_b(idx) & 255).astype(np.float32) * np.float32(1.0e-7)
+    x = (base + tiny).astype(np.float32)
+    w = np.float32(0.5) + (hash_lcg_b(idx) & 4095).astype(np.float32) * np.float32(1.0 / 4096.0)
+    dy = _grid(hash_lcg_c(idx), 4095, 1.0 / 2048.0, -1.0)
+    return x.reshape(rows, cols), w.astype(np.float32).reshape(rows, cols), dy.reshape(rows, cols)
+
+
+def pearson_backward_init(rows: int, cols: int):
+    """x, y, grad of src/workloads/pearson_backward.cu:289-309."""
+    idx = np.arange(rows * cols, dtype=np.uint64)
+    x = _grid(hash_lcg_a(idx), 2047, 1.0 / 1024.0, -1.0)
+    y = _grid(hash_lcg_b(idx), 2047, 1.0 / 1024.0, -1.0)
+    grad = np.float32(0.75) + (np.arange(rows) % 17).astype(np.float32) * np.float32(0.03125)
+    return x.reshape(rows, cols), y.reshape(rows, cols), grad.astype(np.float32).reshape(rows, 1)
+

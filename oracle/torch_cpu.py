@@ -72,6 +72,40 @@ def rowwise_quant(x):
     return q, (max_abs / 127.0).squeeze(-1)
 
 
+def lars_momentum(weight, grad, momentum):
+    """dsmem_eval/workloads.py:136-143 as written."""
+    update = 0.9 * momentum + grad + 0.01 * weight
+    weight_norm = torch.sqrt((weight * weight).sum(dim=-1, keepdim=True))
+    update_norm = torch.sqrt((update * update).sum(dim=-1, keepdim=True))
+    trust = 0.02 * weight_norm / (update_norm + 1.0e-6)
+    return weight - 1.0e-3 * trust * update, update
+
+
+def weighted_var_backward(x, weight, dy):
+    """dsmem_eval/workloads.py:72-85 as written."""
+    inv_sum_w = 1.0 / (weight.sum(dim=-1, keepdim=True) + 1.0e-5)
+    mean = (weight * x).sum(dim=-1, keepdim=True) * inv_sum_w
+    diff = x - mean
+    variance = (weight * diff * diff).sum(dim=-1, keepdim=True) * inv_sum_w
+    inv_std = torch.rsqrt(variance + 1.0e-5)
+    sum_dy = dy.sum(dim=-1, keepdim=True)
+    sum_dyc = (dy * diff).sum(dim=-1, keepdim=True)
+    return inv_std * (dy - weight * inv_sum_w * sum_dy
+                      - weight * diff * inv_std * inv_std * inv_sum_w * sum_dyc)
+
+
+def pearson_backward(x, y, grad):
+    """dsmem_eval/workloads.py:96-112 as written."""
+    xc = x - x.mean(dim=-1, keepdim=True)
+    yc = y - y.mean(dim=-1, keepdim=True)
+    inv_x = torch.rsqrt((xc * xc).sum(dim=-1, keepdim=True) + 1.0e-6)
+    inv_y = torch.rsqrt((yc * yc).sum(dim=-1, keepdim=True) + 1.0e-6)
+    cov = (xc * yc).sum(dim=-1, keepdim=True)
+    inv_xy = inv_x * inv_y
+    return (grad * (yc * inv_xy - xc * cov * inv_x * inv_x * inv_x * inv_y),
+            grad * (xc * inv_xy - yc * cov * inv_x * inv_y * inv_y * inv_y))
+
+
 def ffn(x, w1, w2, eps=1.0e-6):
     a = F.rms_norm(x.float(), (x.shape[-1],), None, eps).to(x.dtype)
     h = F.gelu(a @ w1, approximate="tanh")
@@ -91,5 +125,8 @@ FUNCTIONS = {
         x.float(), dy.float(), g.float()).to(x.dtype),
     "softmax_logits_backward": softmax_logits_backward,
     "rowwise_quant": rowwise_quant,
+    "lars_momentum": lars_momentum,
+    "weighted_var_backward": weighted_var_backward,
+    "pearson_backward": pearson_backward,
     "ffn": ffn,
 }
