@@ -43,6 +43,7 @@ import torch
 from . import hip_lib
 from .cost_model import MODEL_VERSION, DeviceProfile, estimate, staged_bytes_per_workgroup
 from .profile import format_profile_text, make_device_profile, profile_as_dict, run_microbenchmarks
+from .report import write_report
 from .workloads import WORKLOADS, WorkloadSpec
 
 # Workloads with a split variant (the cost model's domain).
@@ -374,6 +375,7 @@ def run_suite(raw_config: dict[str, Any], output_dir: Path,
     write_csv(output_dir / "cluster_sweep.csv", sweep)
     metadata.update(status="complete", elapsed_seconds=time.time() - started,
                     profile=profile_as_dict(profile), aggregate=aggregate(summary))
+    metadata["report"] = write_report(output_dir, summary, metadata)
     (output_dir / "metadata.json").write_text(json.dumps(metadata, indent=2) + "\n")
     return metadata
 

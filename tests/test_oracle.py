@@ -262,3 +262,24 @@ def test_hash_lcg_known_values():
     x, dy, gamma = ref.layernorm_backward_init(2, 4)
     assert x[0, 0] == np.float32(0 * (1 / 1024) - 1)
     assert gamma[1] == np.float32(0.75 + 1 * 0.015625)
+
+
+def test_reference_init_restatements():
+    """The init kernels of lars_momentum.cu:257-275,
+    weighted_var_backward.cu:253-285 and pearson_backward.cu:289-309 at
+    hand-computed indices."""
+    # idx 0: (0*22695477 + 1) >> 16 = 0;  idx 1: 22695478 >> 16 = 346
+    assert ref.hash_lcg_c(0) == 0 and ref.hash_lcg_c(1) == 346
+    w, g, m = ref.lars_momentum_init(1, 2)
+    assert w[0, 1] == np.float32((16838 & 2047) / 1024 - 1)  # 454/1024 - 1
+    assert g[0, 0] == np.float32((15470 & 2047) / 1024 - 1)
+    assert m[0, 1] == np.float32((346 & 2047) / 1024 - 1)
+    x, wt, dy = ref.weighted_var_backward_init(1, 2)
+    # base + tiny, each an fp32 operation: a & 4095 = 454 at idx 1
+    expect = np.float32(np.float32(454) * np.float32(1 / 1024) - np.float32(2)) + np.float32(
+        np.float32(15496 & 255) * np.float32(1e-7))
+    assert x[0, 1] == expect
+    assert wt[0, 0] == np.float32(0.5 + (15470 & 4095) / 4096)
+    assert dy[0, 1] == np.float32((346 & 4095) / 2048 - 1)
+    x, y, grad = ref.pearson_backward_init(18, 1)
+    assert grad.shape == (18, 1) and grad[17, 0] == np.float32(0.75) and grad[16, 0] == np.float32(0.75 + 16 * 0.03125)
