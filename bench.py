@@ -41,7 +41,7 @@ CALL_KERNELS = {
     "softmax_logits_backward": ["softmax_logits_bwd_slice_kernel<1024, 8>"],
     "ffn": ["ffn_rstd_kernel", "ffn_gemm256_kernel<0>", "ffn_gemm256_kernel<1>"],
     "layernorm_backward": ["layernorm_bwd_slice_kernel<float, 1024, 8>"],
-    "layernorm_backward_bf16": ["layernorm_bwd_slice_kernel<unsigned short, 1024, 4>"],
+    "layernorm_backward_bf16": ["layernorm_bwd_slice_kernel<unsigned short, 512, 8>"],
     "rowwise_quant": ["rowwise_quant_slice_kernel<1024, 16>"],
     "lars_momentum": ["lars_slice_kernel<512, 8>"],
     "weighted_var_backward": ["wvar_bwd_slice_kernel<1024, 4>"],
