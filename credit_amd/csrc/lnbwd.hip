@@ -51,6 +51,14 @@ struct Vec<uint16_t> {
   __device__ static void store_scalar(uint16_t* p, float v) { *p = f32_to_bf16(v); }
 };
 
+// An empty asm that "redefines" each vector: values computed from the
+// vectors before it cannot be reused after it.
+template <int N, class R>
+__device__ __forceinline__ void opaque_regs(R (&v)[N]) {
+#pragma unroll
+  for (int k = 0; k < N; ++k) __asm__ volatile("" : "+v"(v[k]));
+}
+
 struct RowStats {
   float mean, rstd;
 };
@@ -73,7 +81,10 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
   using raw = typename V::raw;
   constexpr int NW = THREADS / kWave;
   constexpr int E = V::kN;
-  __shared__ double red[4][NW];
+  // One slot array per stage: no workgroup reuses a stage's slots before
+  // the barrier of the other stage (or of the exchanges) has passed.
+  __shared__ double red1[2][NW];
+  __shared__ double red2[2][NW];
   SplitGroup g;
   // members == 1: one workgroup per row.  members > 1: a co-resident grid
   // of G groups; the member covers its slice of rows group, group + G, ...
@@ -87,51 +98,61 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
   const int nvec = cols / E;
   const int v0 = member * chunk;
   const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  // Row traffic through buffer resources over the member's slice: lanes
+  // beyond it read zeros and drop their stores, with no branch around a
+  // load or store.
+  const uint32_t slice_bytes = static_cast<uint32_t>(vlen) * 16u;
+  const uint32_t lane_off = threadIdx.x * 16u;
+  constexpr uint32_t kStride = THREADS * 16u;
+  const buffer_rsrc_t grs = make_rsrc(gamma + static_cast<size_t>(E) * v0, slice_bytes);
   for (int row = row0; row < rows; row += step) {
-  const int tid = opaque_lane_index();
-  const size_t off = static_cast<size_t>(row) * cols;
-  const raw* xr = reinterpret_cast<const raw*>(x + off) + v0;
-  const raw* dr = reinterpret_cast<const raw*>(dy + off) + v0;
-  const raw* gr = reinterpret_cast<const raw*>(gamma) + v0;
-  raw xv[VPT], dv[VPT];
-  // (p + k*THREADS)[tid]: a uniform base per k and one lane offset, so no
-  // per-k lane address stays live across the row loop.
+    const size_t off = static_cast<size_t>(row) * cols + static_cast<size_t>(E) * v0;
+    const buffer_rsrc_t xrs = make_rsrc(x + off, slice_bytes);
+    const buffer_rsrc_t drs = make_rsrc(dy + off, slice_bytes);
+    raw xv[VPT], dv[VPT];
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const bool in = tid < vlen - k * THREADS;
-    xv[k] = in ? load_nt(&(xr + k * THREADS)[tid]) : raw{};
-    dv[k] = in ? load_nt(&(dr + k * THREADS)[tid]) : raw{};
-  }
-  const float x0 = V::scalar(x + off);
-  float a1 = 0.0f, a2 = 0.0f;
+    for (int k = 0; k < VPT; ++k) {
+      xv[k] = __builtin_bit_cast(raw, buffer_load_nt(xrs, lane_off + k * kStride));
+      dv[k] = __builtin_bit_cast(raw, buffer_load_nt(drs, lane_off + k * kStride));
+    }
+    const float x0 = V::scalar(x + static_cast<size_t>(row) * cols);
+    float a1 = 0.0f, a2 = 0.0f;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    if (tid < vlen - k * THREADS) {
+    for (int k = 0; k < VPT; ++k) {
+      // Beyond the slice x reads 0: its shifted value -x0 must add nothing.
+      float p1 = 0.0f, p2 = 0.0f;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const float d = V::get(xv[k], e) - x0;
-        a1 += d;
-        a2 += d * d;
+        p1 += d;
+        p2 += d * d;
       }
+      const bool in = lane_off + k * kStride < slice_bytes;
+      a1 += in ? p1 : 0.0f;
+      a2 += in ? p2 : 0.0f;
     }
-  }
-  double s1 = block_reduce_sum_f64<NW>(static_cast<double>(a1), red[0]);
-  double s2 = block_reduce_sum_f64<NW>(static_cast<double>(a2), red[1]);
-  if (members > 1) {
-    if (tid == 0) {
-      split_publish(g, 0, s1);
-      split_publish(g, 1, s2);
+    double s[2] = {a1, a2};
+    block_reduce_sum_f64_multi<NW, 2>(s, red1);
+    if (members > 1) {
+      if (threadIdx.x == 0) {
+        split_publish(g, 0, s[0]);
+        split_publish(g, 1, s[1]);
+      }
+      split_exchange(g);
+      s[0] = split_sum(g, 0);
+      s[1] = split_sum(g, 1);
     }
-    split_exchange(g);
-    s1 = split_sum(g, 0);
-    s2 = split_sum(g, 1);
-  }
-  const RowStats st = stats_from(s1, s2, x0, cols, eps);
-  float b1 = 0.0f, b2 = 0.0f;
+    const RowStats st = stats_from(s[0], s[1], x0, cols, eps);
+    // The loaded vectors stay packed in registers between the passes: each
+    // pass unpacks them again (cheap) rather than keeping unpacked copies
+    // alive (twice the registers for bf16).
+    opaque_regs<VPT>(xv);
+    opaque_regs<VPT>(dv);
+    // Beyond the slice dy reads 0, so g = dy * gamma adds nothing.
+    float b1 = 0.0f, b2 = 0.0f;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    if (tid < vlen - k * THREADS) {
-      const raw gv = (gr + k * THREADS)[tid];
+    for (int k = 0; k < VPT; ++k) {
+      const raw gv = __builtin_bit_cast(raw, buffer_load(grs, lane_off + k * kStride));
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const float gg = V::get(dv[k], e) * V::get(gv, e);
@@ -139,34 +160,33 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
         b2 += gg * ((V::get(xv[k], e) - st.mean) * st.rstd);
       }
     }
-  }
-  double t1 = block_reduce_sum_f64<NW>(static_cast<double>(b1), red[2]);
-  double t2 = block_reduce_sum_f64<NW>(static_cast<double>(b2), red[3]);
-  if (members > 1) {
-    if (tid == 0) {
-      split_publish(g, 0, t1);
-      split_publish(g, 1, t2);
+    double t[2] = {b1, b2};
+    block_reduce_sum_f64_multi<NW, 2>(t, red2);
+    if (members > 1) {
+      if (threadIdx.x == 0) {
+        split_publish(g, 0, t[0]);
+        split_publish(g, 1, t[1]);
+      }
+      split_exchange(g);
+      t[0] = split_sum(g, 0);
+      t[1] = split_sum(g, 1);
     }
-    split_exchange(g);
-    t1 = split_sum(g, 0);
-    t2 = split_sum(g, 1);
-  }
-  const float mg = static_cast<float>(t1 / cols);
-  const float mgx = static_cast<float>(t2 / cols);
-  raw* outr = reinterpret_cast<raw*>(dx + off) + v0;
+    const float mg = static_cast<float>(t[0] / cols);
+    const float mgx = static_cast<float>(t[1] / cols);
+    opaque_regs<VPT>(xv);
+    opaque_regs<VPT>(dv);
+    const buffer_rsrc_t ors = make_rsrc(dx + off, slice_bytes);
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    if (tid < vlen - k * THREADS) {
-      const raw gv = (gr + k * THREADS)[tid];
+    for (int k = 0; k < VPT; ++k) {
+      const raw gv = __builtin_bit_cast(raw, buffer_load(grs, lane_off + k * kStride));
       float o[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const float xh = (V::get(xv[k], e) - st.mean) * st.rstd;
         o[e] = (V::get(dv[k], e) * V::get(gv, e) - mg - xh * mgx) * st.rstd;
       }
-      store_nt(&(outr + k * THREADS)[tid], V::pack(o));
+      buffer_store_nt(ors, lane_off + k * kStride, __builtin_bit_cast(u32x4, V::pack(o)));
     }
-  }
   }
 }
 
