@@ -37,7 +37,7 @@ CALL_KERNELS = {
     "rmsnorm_fwd": ["rmsnorm_fwd_slice_kernel<1024, 8>"],
     "rmsnorm_bwd": ["rmsnorm_bwd_group_kernel<512, 2>", "rmsnorm_dw_reduce_kernel"],
     "softmax_fwd": ["softmax_fwd_group_kernel<512, 8>"],
-    "softmax_bwd": ["softmax_bwd_slice_kernel<1024, 8>"],
+    "softmax_bwd": ["softmax_bwd_slice_kernel<512, 8>"],
     "softmax_logits_backward": ["softmax_logits_bwd_slice_kernel<1024, 8>"],
     "ffn": ["ffn_rstd_kernel", "ffn_gemm256_kernel<0>", "ffn_gemm256_kernel<1>"],
     "layernorm_backward": ["layernorm_bwd_slice_kernel<float, 1024, 8>"],

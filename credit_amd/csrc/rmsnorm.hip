@@ -83,7 +83,7 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
     uint16_t* __restrict__ y, float* __restrict__ rstd_out, int cols, int chunk,
     int members, int rows, float eps, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
-  __shared__ double red[NW];
+  __shared__ double red[1][NW];
   SplitGroup g;
   // members == 1: one workgroup per row.  members > 1: a co-resident grid
   // of G groups; the member covers its slice of rows group, group + G, ...
@@ -97,32 +97,36 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
   const int nvec = cols >> 3;
   const int v0 = member * chunk;
   const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  // Row traffic through buffer resources over the member's slice: lanes
+  // beyond it read zeros (adding nothing to the sum of squares) and drop
+  // their stores, with no branch around a load or store.
+  const uint32_t slice_bytes = static_cast<uint32_t>(vlen) * 16u;
+  const uint32_t lane_off = threadIdx.x * 16u;
+  constexpr uint32_t kStride = THREADS * 16u;
+  const buffer_rsrc_t wrs = make_rsrc(w + 8 * static_cast<size_t>(v0), slice_bytes);
   for (int row = row0; row < rows; row += step) {
-  const int tid = opaque_lane_index();
-  const u32x4* xr = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(row) * cols) + v0;
-  u32x4 v[VPT];
-  // (p + k*THREADS)[tid]: a uniform base per k and one lane offset, so no
-  // per-k lane address stays live across the row loop.
+    const size_t off = static_cast<size_t>(row) * cols + 8 * static_cast<size_t>(v0);
+    const buffer_rsrc_t xrs = make_rsrc(x + off, slice_bytes);
+    u32x4 v[VPT];
 #pragma unroll
-  for (int k = 0; k < VPT; ++k)
-    v[k] = tid < vlen - k * THREADS ? load_nt(&(xr + k * THREADS)[tid]) : u32x4{0, 0, 0, 0};
-  float ss = 0.0f;
+    for (int k = 0; k < VPT; ++k) v[k] = buffer_load_nt(xrs, lane_off + k * kStride);
+    float ss = 0.0f;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) ss += sumsq8(v[k]);
-  double total = block_reduce_sum_f64<NW>(static_cast<double>(ss), red);
-  if (members > 1) {
-    if (tid == 0) split_publish(g, 0, total);
-    split_exchange(g);
-    total = split_sum(g, 0);
-  }
-  const float rs = static_cast<float>(1.0 / __builtin_sqrt(total / cols + eps));
-  const u32x4* wr = reinterpret_cast<const u32x4*>(w) + v0;
-  u32x4* yr = reinterpret_cast<u32x4*>(y + static_cast<size_t>(row) * cols) + v0;
+    for (int k = 0; k < VPT; ++k) ss += sumsq8(v[k]);
+    double total[1] = {ss};
+    block_reduce_sum_f64_multi<NW, 1>(total, red);
+    if (members > 1) {
+      if (threadIdx.x == 0) split_publish(g, 0, total[0]);
+      split_exchange(g);
+      total[0] = split_sum(g, 0);
+    }
+    const float rs = static_cast<float>(1.0 / __builtin_sqrt(total[0] / cols + eps));
+    const buffer_rsrc_t yrs = make_rsrc(y + off, slice_bytes);
 #pragma unroll
-  for (int k = 0; k < VPT; ++k)
-    if (tid < vlen - k * THREADS)
-      store_nt(&(yr + k * THREADS)[tid], scale8(v[k], (wr + k * THREADS)[tid], rs));
-  if (member == 0 && tid == 0) rstd_out[row] = rs;
+    for (int k = 0; k < VPT; ++k)
+      buffer_store_nt(yrs, lane_off + k * kStride,
+                      scale8(v[k], buffer_load(wrs, lane_off + k * kStride), rs));
+    if (member == 0 && threadIdx.x == 0) rstd_out[row] = rs;
   }
 }
 

@@ -413,35 +413,35 @@ __global__ __launch_bounds__(THREADS) void softmax_bwd_slice_kernel(
     const float* __restrict__ p, const float* __restrict__ dy, float* __restrict__ dx, int cols,
     int chunk, int members, int rows, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
-  __shared__ double sred[NW];
+  __shared__ double sred[1][NW];
   SplitGroup g;
   const Slice sl = slice_of(&g, members, 1, chunk, cols >> 2, sa);
+  const uint32_t lane_off = threadIdx.x * 16u;
+  constexpr uint32_t kStride = THREADS * 16u;
   for (int row = sl.row; row < rows; row += sl.step) {
-  const int tid = opaque_lane_index();
-  const size_t off = static_cast<size_t>(row) * cols;
-  const f32x4* pr = reinterpret_cast<const f32x4*>(p + off) + sl.v0;
-  const f32x4* dr = reinterpret_cast<const f32x4*>(dy + off) + sl.v0;
-  f32x4 pv[VPT], dv[VPT];
+    const size_t off = static_cast<size_t>(row) * cols;
+    const buffer_rsrc_t pr = slice_rsrc(p + off, sl);
+    const buffer_rsrc_t dr = slice_rsrc(dy + off, sl);
+    f32x4 pv[VPT], dv[VPT];
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const bool in = tid < sl.vlen - k * THREADS;
-    pv[k] = in ? load_nt(&(pr + k * THREADS)[tid]) : f32x4{0, 0, 0, 0};
-    dv[k] = in ? load_nt(&(dr + k * THREADS)[tid]) : f32x4{0, 0, 0, 0};
-  }
-  float ld = 0.0f;
+    for (int k = 0; k < VPT; ++k) {
+      pv[k] = slice_load(pr, lane_off + k * kStride);
+      dv[k] = slice_load(dr, lane_off + k * kStride);
+    }
+    float ld = 0.0f;  // beyond the slice p = dy = 0
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) ld += dot4(pv[k], dv[k]);
-  double dot = block_reduce_sum_f64<NW>(static_cast<double>(ld), sred);
-  if (members > 1) {
-    if (tid == 0) split_publish(g, 0, dot);
-    split_exchange(g);
-    dot = split_sum(g, 0);
-  }
-  const float d = static_cast<float>(dot);
-  f32x4* xr = reinterpret_cast<f32x4*>(dx + off) + sl.v0;
+    for (int k = 0; k < VPT; ++k) ld += dot4(pv[k], dv[k]);
+    double dot[1] = {ld};
+    block_reduce_sum_f64_multi<NW, 1>(dot, sred);
+    if (members > 1) {
+      if (threadIdx.x == 0) split_publish(g, 0, dot[0]);
+      split_exchange(g);
+      dot[0] = split_sum(g, 0);
+    }
+    const float d = static_cast<float>(dot[0]);
+    const buffer_rsrc_t xr = slice_rsrc(dx + off, sl);
 #pragma unroll
-  for (int k = 0; k < VPT; ++k)
-    if (tid < sl.vlen - k * THREADS) store_nt(&(xr + k * THREADS)[tid], grad4(pv[k], dv[k], d));
+    for (int k = 0; k < VPT; ++k) slice_store(xr, lane_off + k * kStride, grad4(pv[k], dv[k], d));
   }
 }
 
@@ -495,60 +495,81 @@ __global__ __launch_bounds__(THREADS) void softmax_logits_bwd_slice_kernel(
     const float* __restrict__ logits, const float* __restrict__ dy, float* __restrict__ dx,
     int cols, int chunk, int members, int rows, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
-  __shared__ float mred[NW];
-  __shared__ double sred[2][NW];
+  __shared__ float wmax[NW];
+  __shared__ float wsum[NW];
+  __shared__ double dred[1][NW];
   SplitGroup g;
   const Slice sl = slice_of(&g, members, 2, chunk, cols >> 2, sa);
+  const uint32_t lane_off = threadIdx.x * 16u;
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  constexpr uint32_t kStride = THREADS * 16u;
+  const uint32_t slice_bytes = static_cast<uint32_t>(sl.vlen) * 16u;
   for (int row = sl.row; row < rows; row += sl.step) {
-  const int tid = opaque_lane_index();
-  const size_t off = static_cast<size_t>(row) * cols;
-  const f32x4* lr = reinterpret_cast<const f32x4*>(logits + off) + sl.v0;
-  const f32x4* dr = reinterpret_cast<const f32x4*>(dy + off) + sl.v0;
-  f32x4 v[VPT], dv[VPT];
+    const size_t off = static_cast<size_t>(row) * cols;
+    const buffer_rsrc_t lr = slice_rsrc(logits + off, sl);
+    const buffer_rsrc_t dr = slice_rsrc(dy + off, sl);
+    f32x4 v[VPT], dv[VPT];
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const bool in = tid < sl.vlen - k * THREADS;
-    v[k] = in ? load_nt(&(lr + k * THREADS)[tid]) : f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
-    dv[k] = in ? load_nt(&(dr + k * THREADS)[tid]) : f32x4{0, 0, 0, 0};
-  }
-  float lm = kNegInf;
-#pragma unroll
-  for (int k = 0; k < VPT; ++k) lm = fmax_nan(lm, max4(v[k]));
-  const float wm = block_reduce<NW>(lm, MaxOp{}, mred);
-  float ls = 0.0f;
-  if (wm != kNegInf) {
-#pragma unroll
-    for (int k = 0; k < VPT; ++k) ls += sumexp4(v[k], wm);
-  }
-  const double ws = block_reduce_sum_f64<NW>(static_cast<double>(ls), sred[0]);
-  float m = wm;
-  double s = ws;
-  if (members > 1) {
-    if (tid == 0) {
-      split_publish(g, 0, static_cast<double>(wm));
-      split_publish(g, 1, ws);
+    for (int k = 0; k < VPT; ++k) {
+      v[k] = slice_load(lr, lane_off + k * kStride);
+      dv[k] = slice_load(dr, lane_off + k * kStride);
     }
-    split_exchange(g);
-    split_merge_maxsum(g, &m, &s);
-  }
-  const float inv_s = static_cast<float>(1.0 / s);
-  float ld = 0.0f;
+    // Wave partial (m_w, s_w); the row's values become e^(x - m_w) in place
+    // (zeros beyond the slice), so p costs one exponential per element.
+    float lm = kNegInf;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    v[k] = prob4(v[k], m, inv_s);  // out-of-slice lanes: e^-inf = 0
-    ld += dot4(v[k], dv[k]);
-  }
-  double dot = block_reduce_sum_f64<NW>(static_cast<double>(ld), sred[1]);
-  if (members > 1) {
-    if (tid == 0) split_publish(g, 0, dot);
-    split_exchange(g, 1);  // stage 2 carries the dot only
-    dot = split_sum(g, 0);
-  }
-  const float d = static_cast<float>(dot);
-  f32x4* xr = reinterpret_cast<f32x4*>(dx + off) + sl.v0;
+    for (int k = 0; k < VPT; ++k)
+      lm = lane_off + k * kStride < slice_bytes ? fmax_nan(lm, max4(v[k])) : lm;
+    const float wm = wave_reduce(lm, MaxOp{});
+    float ls = 0.0f;
+    if (wm != kNegInf) {
 #pragma unroll
-  for (int k = 0; k < VPT; ++k)
-    if (tid < sl.vlen - k * THREADS) store_nt(&(xr + k * THREADS)[tid], grad4(v[k], dv[k], d));
+      for (int k = 0; k < VPT; ++k) {
+        const f32x4 e = prob4(v[k], wm, 1.0f);
+        v[k] = lane_off + k * kStride < slice_bytes ? e : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        ls += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < VPT; ++k) v[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const double ws = wave_reduce_sum_f64(static_cast<double>(ls));
+    if (lane == 0) {
+      wmax[wid] = wm;
+      wsum[wid] = static_cast<float>(ws);
+    }
+    __syncthreads();
+    float M, S;
+    merge_maxsum_lanes(lane < NW, lane < NW ? wmax[lane] : kNegInf,
+                       lane < NW ? wsum[lane] : 0.0f, &M, &S);
+    double Sd = S;
+    if (members > 1) {
+      if (threadIdx.x == 0) {
+        split_publish(g, 0, static_cast<double>(M));
+        split_publish(g, 1, Sd);
+      }
+      split_exchange(g);
+      split_merge_maxsum(g, &M, &Sd);
+    }
+    // p = e^(x - m_w) * e^(m_w - M) / S; 0/0 (NaN) on a row of -inf.
+    const float f = (wm == kNegInf ? 0.0f : exp_accurate(wm - M)) / static_cast<float>(Sd);
+    float ld = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      v[k] = v[k] * f;
+      ld += dot4(v[k], dv[k]);
+    }
+    double dot[1] = {ld};
+    block_reduce_sum_f64_multi<NW, 1>(dot, dred);
+    if (members > 1) {
+      if (threadIdx.x == 0) split_publish(g, 0, dot[0]);
+      split_exchange(g, 1);  // stage 2 carries the dot only
+      dot[0] = split_sum(g, 0);
+    }
+    const float d = static_cast<float>(dot[0]);
+    const buffer_rsrc_t xr = slice_rsrc(dx + off, sl);
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) slice_store(xr, lane_off + k * kStride, grad4(v[k], dv[k], d));
   }
 }
 
@@ -643,6 +664,10 @@ const Pick<BwdFn> kLogits[] = {
 
 constexpr int64_t kFwdCapacity = 16384;
 constexpr int64_t kBwdCapacity = 8192;
+// AUTO slices of the softmax backward on rows wider than one workgroup:
+// 512-lane members, two per CU (at 512 x 262144: 16 members 5.18 TB/s,
+// 8 members of 8192 vectors 4.89 TB/s).
+constexpr int64_t kBwdAutoSlice = 4096;
 
 // Forward group kernel (SPLIT on rows wider than one workgroup): four row
 // buffers of VPT f32x4 per lane; 448-512 data lanes + 1 wave give two
@@ -716,8 +741,10 @@ size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int sp
   credit_cfg c{nullptr, variant, split, nullptr, 0};
   Plan p;
   const int64_t cap = op == CREDIT_OP_SOFTMAX_FWD ? kFwdCapacity : kBwdCapacity;
-  const int st = op == CREDIT_OP_SOFTMAX_FWD ? resolve_fwd(&c, cols, cols % 4 == 0, &p)
-                                             : resolve(&c, cols, cols % 4 == 0, cap, "softmax", &p);
+  const int st = op == CREDIT_OP_SOFTMAX_FWD
+                     ? resolve_fwd(&c, cols, cols % 4 == 0, &p)
+                     : resolve(&c, cols, cols % 4 == 0, cap, "softmax", &p,
+                               op == CREDIT_OP_SOFTMAX_BWD ? kBwdAutoSlice : 0);
   if (st != CREDIT_OK) return 0;
   const int k = op == CREDIT_OP_SOFTMAX_BWD ? 1 : 2;
   if (op == CREDIT_OP_SOFTMAX_FWD && fwd_group_ok(p)) {
@@ -794,7 +821,7 @@ extern "C" int credit_softmax_bwd_f32(const float* p, const float* dy, float* dx
   if (rows == 0) return CREDIT_OK;
   const bool vec = vec_ok(cols, {p, dy, dx});
   Plan plan;
-  CREDIT_TRY(resolve(cfg, cols, vec, kBwdCapacity, "softmax_bwd", &plan));
+  CREDIT_TRY(resolve(cfg, cols, vec, kBwdCapacity, "softmax_bwd", &plan, kBwdAutoSlice));
   hipStream_t stream = cfg_stream(cfg);
   const int c = static_cast<int>(cols);
   const unsigned r = static_cast<unsigned>(rows);
