@@ -150,8 +150,8 @@ def cpu_baseline(name, cpu_inputs, spec, seconds):
             break
     runs.sort()
     med = runs[len(runs) // 2]
-    if name == "ffn":
-        work = spec_ffn_flops(sample_rows, cpu_inputs[0].shape[1])
+    if name in ("ffn", "ffn_backward"):
+        work = spec_ffn_flops(sample_rows, cpu_inputs[0].shape[1], name)
         value, unit = work / med / 1e12, "TFLOP/s"
     else:
         work = spec.algorithmic_bytes(sample_rows, cpu_inputs[0].shape[1])
@@ -165,10 +165,10 @@ def cpu_baseline(name, cpu_inputs, spec, seconds):
     }
 
 
-def spec_ffn_flops(rows, d):
-    from credit_amd.workloads import ffn_flops
+def spec_ffn_flops(rows, d, name="ffn"):
+    from credit_amd.workloads import ffn_backward_flops, ffn_flops
 
-    return ffn_flops(rows, d)
+    return ffn_backward_flops(rows, d) if name == "ffn_backward" else ffn_flops(rows, d)
 
 
 # ------------------------------------------------------------------ main --
@@ -182,8 +182,8 @@ def measure(name, args, hip_lib, torch, dev, with_cpu):
     ms_step, kernel_ms = time_gpu(launch, torch, args.steps, args.warmup)
     out = {"rows": spec.rows, "cols": spec.cols, "ms_per_step": round(ms_step, 6),
            "kernel_ms": round(kernel_ms, 6)}
-    if name == "ffn":
-        flops = spec_ffn_flops(spec.rows, spec.cols)
+    if name in ("ffn", "ffn_backward"):
+        flops = spec_ffn_flops(spec.rows, spec.cols, name)
         out.update(metric="MFMA TFLOP/s", value=round(flops / (ms_step * 1e-3) / 1e12, 2),
                    unit="TFLOP/s",
                    roofline={"bound": "mfma", "achieved": round(flops / (kernel_ms * 1e-3) / 1e12, 2),

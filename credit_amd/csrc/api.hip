@@ -327,6 +327,11 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
   return body == 0 ? 0 : kScratchOffset + body;
 }
 
+size_t credit_ffn_bwd_workspace_bytes(int64_t rows, int64_t d, int64_t f) {
+  if (rows <= 0 || d <= 0 || f <= 0) return 0;
+  return kScratchOffset + ffn_bwd_workspace(rows, d, f);
+}
+
 int credit_check_watchdog(const credit_cfg* cfg) {
   CREDIT_TRY(check_cfg(cfg));
   char* base = nullptr;

@@ -159,6 +159,7 @@ int check_launch(const char* kernel);
 size_t row_sum_max_workspace(int64_t rows, int64_t cols, int variant, int split,
                              int cu_count);
 size_t ffn_workspace(int64_t rows, int64_t ffn_dim);
+size_t ffn_bwd_workspace(int64_t rows, int64_t d, int64_t ffn_dim);
 size_t layernorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
                                int elem_bytes, int cu_count);
 size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int split,

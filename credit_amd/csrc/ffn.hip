@@ -38,8 +38,17 @@ constexpr int kBK = 64;
 constexpr int kThreads = 256;
 constexpr int kLdsStride = kBK + 8;  // bf16 per LDS row: 16-byte pad against bank conflicts
 
+// GEMM epilogues.  Forward: kEpiGelu (h = GELU(acc * rstd[m])),
+// kEpiResidual (out = acc + x).  Backward (credit_ffn_rmsnorm_gelu_bwd_bf16):
+// kEpiUH (u = acc * rstd[m] to C, h = GELU(u) transposed to C2),
+// kEpiGeluBwd (du = acc * GELU'(u[m, n]) to C and, transposed, to C2),
+// kEpiStore (bf16(acc)), kEpiStoreF32 (acc as fp32 to Cf).
 constexpr int kEpiGelu = 0;
 constexpr int kEpiResidual = 1;
+constexpr int kEpiUH = 2;
+constexpr int kEpiGeluBwd = 3;
+constexpr int kEpiStore = 4;
+constexpr int kEpiStoreF32 = 5;
 
 // GELU with the tanh approximation; tanh(u) = 1 - 2 / (e^(2u) + 1), which
 // saturates correctly for |u| large (e^(2u) -> inf or 0).
@@ -48,6 +57,42 @@ __device__ __forceinline__ float gelu_tanh(float v) {
   const float u = kC * (v + 0.044715f * v * v * v);
   const float t = 1.0f - 2.0f / (exp_accurate(2.0f * u) + 1.0f);
   return 0.5f * v * (1.0f + t);
+}
+
+// d/dv GELU_tanh(v) = 0.5 (1 + t) + 0.5 v (1 - t^2) dz/dv, t = tanh(z),
+// z = sqrt(2/pi) (v + 0.044715 v^3).
+__device__ __forceinline__ float gelu_tanh_grad(float v) {
+  constexpr float kC = 0.7978845608028654f;
+  const float z = kC * (v + 0.044715f * v * v * v);
+  const float t = 1.0f - 2.0f / (exp_accurate(2.0f * z) + 1.0f);
+  return 0.5f * (1.0f + t) + 0.5f * v * (1.0f - t * t) * kC * (1.0f + 3.0f * 0.044715f * v * v);
+}
+
+// One output element of every epilogue.  s is the row scale still to apply
+// (rstd[m] for the 256-tile kernel, 1 where the A tile was scaled on load).
+template <int EPI>
+__device__ __forceinline__ void epilogue(float acc, float s, int m, int n, int M, int N,
+                                         const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
+                                         uint16_t* __restrict__ C2, float* __restrict__ Cf) {
+  const size_t idx = static_cast<size_t>(m) * N + n;
+  const size_t tdx = static_cast<size_t>(n) * M + m;
+  if (EPI == kEpiGelu) {
+    C[idx] = f32_to_bf16(gelu_tanh(acc * s));
+  } else if (EPI == kEpiResidual) {
+    C[idx] = f32_to_bf16(acc + bf16_to_f32(R[idx]));
+  } else if (EPI == kEpiUH) {
+    const float u = acc * s;
+    C[idx] = f32_to_bf16(u);
+    C2[tdx] = f32_to_bf16(gelu_tanh(u));
+  } else if (EPI == kEpiGeluBwd) {
+    const uint16_t v = f32_to_bf16(acc * gelu_tanh_grad(bf16_to_f32(R[idx])));
+    C[idx] = v;
+    C2[tdx] = v;
+  } else if (EPI == kEpiStore) {
+    C[idx] = f32_to_bf16(acc);
+  } else {
+    Cf[idx] = acc;
+  }
 }
 
 __device__ __forceinline__ u32x4 scale_bf16x8(u32x4 v, float s) {
@@ -85,7 +130,8 @@ template <int EPI>
 __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
     const uint16_t* __restrict__ A, const float* __restrict__ a_scale,
     const uint16_t* __restrict__ B, const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
-    int M, int N, int K) {
+    uint16_t* __restrict__ C2, float* __restrict__ Cf, int M, int N, int K) {
+  constexpr bool kScaleA = EPI == kEpiGelu || EPI == kEpiUH;
   __shared__ __attribute__((aligned(16))) uint16_t As[kBM * kLdsStride];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[kBN * kLdsStride];
   const int tid = threadIdx.x;
@@ -111,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
     const int r = ld_row + 32 * i;
     a_src[i] = reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m0 + r) * K) + ld_chunk;
     b_src[i] = reinterpret_cast<const u32x4*>(B + static_cast<size_t>(n0 + r) * K) + ld_chunk;
-    scale[i] = EPI == kEpiGelu ? a_scale[m0 + r] : 1.0f;
+    scale[i] = kScaleA ? a_scale[m0 + r] : 1.0f;
   }
   u32x4 ra[4], rb[4];
 #pragma unroll
@@ -134,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = ld_row + 32 * i;
-      const u32x4 av = EPI == kEpiGelu ? scale_bf16x8(ra[i], scale[i]) : ra[i];
+      const u32x4 av = kScaleA ? scale_bf16x8(ra[i], scale[i]) : ra[i];
       *reinterpret_cast<u32x4*>(&As[r * kLdsStride + ld_chunk * 8]) = av;
       *reinterpret_cast<u32x4*>(&Bs[r * kLdsStride + ld_chunk * 8]) = rb[i];
     }
@@ -179,13 +225,7 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-        const size_t idx = static_cast<size_t>(m) * N + n;
-        float v = acc[i][j][r];
-        if (EPI == kEpiGelu)
-          v = gelu_tanh(v);
-        else
-          v += bf16_to_f32(R[idx]);
-        C[idx] = f32_to_bf16(v);
+        epilogue<EPI>(acc[i][j][r], 1.0f, m, n, M, N, R, C, C2, Cf);
       }
 }
 
@@ -252,7 +292,7 @@ template <int EPI>
 __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     const uint16_t* __restrict__ A, const float* __restrict__ scale,
     const uint16_t* __restrict__ B, const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
-    int M, int N, int K) {
+    uint16_t* __restrict__ C2, float* __restrict__ Cf, int M, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -359,6 +399,40 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
 
   // Epilogue.  Accumulator register r of lane l holds row
   // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of its 32 x 32 tile.
+  if (EPI == kEpiUH || EPI == kEpiGeluBwd) {
+    // Also stored transposed: registers 4q..4q+3 are four consecutive rows
+    // of one column, so each lane writes them as one 8-byte run of C2.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int mb = m0 + wm * 128 + i * 32 + 8 * q + 4 * (lane >> 5);
+          const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+          uint32_t t[2];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int m = mb + e;
+            const size_t idx = static_cast<size_t>(m) * N + n;
+            float c, ct;
+            if (EPI == kEpiUH) {
+              c = acc[i][j][4 * q + e] * scale[m];
+              ct = gelu_tanh(c);
+            } else {
+              c = ct = acc[i][j][4 * q + e] * gelu_tanh_grad(bf16_to_f32(R[idx]));
+            }
+            C[idx] = f32_to_bf16(c);
+            const uint32_t b = f32_to_bf16(ct);
+            if (e & 1)
+              t[e >> 1] |= b << 16;
+            else
+              t[e >> 1] = b;
+          }
+          *reinterpret_cast<uint2*>(C2 + static_cast<size_t>(n) * M + mb) = uint2{t[0], t[1]};
+        }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -368,29 +442,61 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-        const size_t idx = static_cast<size_t>(m) * N + n;
-        float v = acc[i][j][r];
-        if (EPI == kEpiGelu)
-          v = gelu_tanh(v * sc);
-        else
-          v += bf16_to_f32(R[idx]);
-        C[idx] = f32_to_bf16(v);
+        epilogue<EPI>(acc[i][j][r], sc, m, n, M, N, R, C, C2, Cf);
       }
     }
   }
 }
 
-// dst[c, r] = src[r, c] for a rows x cols bf16 matrix, through a 64 x 64
-// LDS tile.
+// dst[c, r] = bf16(src[r, c] * scale[r]) (scale == nullptr: a plain copy
+// of the bits) for a rows x cols bf16 matrix, through a 64 x 64 LDS tile.
+// Full tiles (rows and cols multiples of 64, 16-byte aligned rows) move 16
+// bytes per lane on both sides; any other shape takes the element path.
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src,
                                                              uint16_t* __restrict__ dst,
-                                                             int rows, int cols) {
-  __shared__ uint16_t tile[64][65];
+                                                             int rows, int cols,
+                                                             const float* __restrict__ scale,
+                                                             int vec) {
+  __shared__ uint16_t tile[64][66];  // row stride 132 bytes: column reads spread over banks
   const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  if (vec) {
+    // Load: lane t reads 8 consecutive columns of rows t/8 and t/8 + 32.
+    const int lr = threadIdx.x >> 3, lc = (threadIdx.x & 7) * 8;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = lr + 32 * h;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(src + static_cast<size_t>(r0 + r) * cols + c0 + lc);
+      const float sc = scale ? scale[r0 + r] : 1.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t w = v[e];
+        if (scale) w = pack_bf16x2(bf16_lo(w) * sc, bf16_hi(w) * sc);
+        tile[r][lc + 2 * e] = static_cast<uint16_t>(w & 0xffffu);
+        tile[r][lc + 2 * e + 1] = static_cast<uint16_t>(w >> 16);
+      }
+    }
+    __syncthreads();
+    // Store: lane t writes 8 consecutive rows of source columns t/8, t/8+32.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = lr + 32 * h;
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = static_cast<uint32_t>(tile[lc + 2 * e][c]) |
+               (static_cast<uint32_t>(tile[lc + 2 * e + 1][c]) << 16);
+      *reinterpret_cast<u32x4*>(dst + static_cast<size_t>(c0 + c) * rows + r0 + lc) = o;
+    }
+    return;
+  }
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   for (int i = ty; i < 64; i += 4) {
     const int r = r0 + i, c = c0 + tx;
-    if (r < rows && c < cols) tile[i][tx] = src[static_cast<size_t>(r) * cols + c];
+    if (r < rows && c < cols) {
+      uint16_t v = src[static_cast<size_t>(r) * cols + c];
+      if (scale) v = f32_to_bf16(bf16_to_f32(v) * scale[r]);
+      tile[i][tx] = v;
+    }
   }
   __syncthreads();
   for (int i = ty; i < 64; i += 4) {
@@ -399,21 +505,142 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
   }
 }
 
+// dx = dout + rstd * (da - ahat * mean(da * ahat)), ahat = x * rstd: the
+// unit-weight RMSNorm backward of the FFN input plus the residual branch.
+// One workgroup per row; x, da and dout are read twice (L2-resident rows).
+__global__ __launch_bounds__(256) void ffn_dx_kernel(const uint16_t* __restrict__ x,
+                                                     const float* __restrict__ rstd,
+                                                     const float* __restrict__ da,
+                                                     const uint16_t* __restrict__ dout,
+                                                     uint16_t* __restrict__ dx, int cols) {
+  __shared__ double red[1][4];
+  const size_t off = static_cast<size_t>(blockIdx.x) * cols;
+  const float rs = rstd[blockIdx.x];
+  const int nvec = cols >> 3;
+  const u32x4* xv = reinterpret_cast<const u32x4*>(x + off);
+  const f32x4* dav = reinterpret_cast<const f32x4*>(da + off);
+  float acc = 0.0f;
+  for (int i = threadIdx.x; i < nvec; i += 256) {
+    const u32x4 v = xv[i];
+    const f32x4 d0 = dav[2 * i], d1 = dav[2 * i + 1];
+    acc += (bf16_lo(v.x) * d0.x + bf16_hi(v.x) * d0.y) + (bf16_lo(v.y) * d0.z + bf16_hi(v.y) * d0.w) +
+           (bf16_lo(v.z) * d1.x + bf16_hi(v.z) * d1.y) + (bf16_lo(v.w) * d1.z + bf16_hi(v.w) * d1.w);
+  }
+  double dot[1] = {acc};
+  block_reduce_sum_f64_multi<4, 1>(dot, red);
+  // mean(da * ahat) = rstd * sum(da * x) / cols
+  const float c = static_cast<float>(dot[0] * rs / cols);
+  const u32x4* gv = reinterpret_cast<const u32x4*>(dout + off);
+  u32x4* ov = reinterpret_cast<u32x4*>(dx + off);
+  for (int i = threadIdx.x; i < nvec; i += 256) {
+    const u32x4 v = xv[i], g = gv[i];
+    const f32x4 d0 = dav[2 * i], d1 = dav[2 * i + 1];
+    const float dd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = bf16_lo(g[e]) + rs * (dd[2 * e] - bf16_lo(v[e]) * rs * c);
+      const float hi = bf16_hi(g[e]) + rs * (dd[2 * e + 1] - bf16_hi(v[e]) * rs * c);
+      o[e] = pack_bf16x2(lo, hi);
+    }
+    ov[i] = o;
+  }
+}
+
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 // The 256-tile kernels take 160 KiB of dynamic LDS; allow it once per
 // process (the attribute belongs to the kernel, not to a device).
+template <int EPI>
+hipError_t allow_big_lds() {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(ffn_gemm256_kernel<EPI>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, kBigLds);
+}
 int enable_big_lds() {
   static int status = [] {
-    for (const void* fn : {reinterpret_cast<const void*>(ffn_gemm256_kernel<kEpiGelu>),
-                           reinterpret_cast<const void*>(ffn_gemm256_kernel<kEpiResidual>)}) {
-      const hipError_t e =
-          hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kBigLds);
+    for (const hipError_t e : {allow_big_lds<kEpiGelu>(), allow_big_lds<kEpiResidual>(),
+                               allow_big_lds<kEpiUH>(), allow_big_lds<kEpiGeluBwd>(),
+                               allow_big_lds<kEpiStore>(), allow_big_lds<kEpiStoreF32>()})
       if (e != hipSuccess) return hip_failure(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
-    }
     return static_cast<int>(CREDIT_OK);
   }();
   return status;
+}
+
+// C[M, N] = epi(A[M, K] B[N, K]^T): the 256-tile kernel when every
+// dimension is a multiple of 256 (so K / 32 >= kStages), the tile count a
+// multiple of the 8 XCDs and element offsets fit 32 bits; otherwise the
+// 128-tile kernel (M, N multiples of 128, K of 64).
+template <int EPI>
+int launch_gemm(const uint16_t* A, const float* scale, const uint16_t* B, const uint16_t* R,
+                uint16_t* C, uint16_t* C2, float* Cf, int M, int N, int K, hipStream_t stream,
+                const char* name) {
+  const bool big = M % kBig == 0 && N % kBig == 0 && K % kBig == 0 &&
+                   ((M / kBig) * (N / kBig)) % 8 == 0 &&
+                   static_cast<int64_t>(M) * K < (int64_t{1} << 31) &&
+                   static_cast<int64_t>(N) * K < (int64_t{1} << 31);
+  if (big) {
+    CREDIT_TRY(enable_big_lds());
+    ffn_gemm256_kernel<EPI><<<dim3(static_cast<unsigned>((M / kBig) * (N / kBig))),
+                              dim3(kBigThreads), kBigLds, stream>>>(A, scale, B, R, C, C2, Cf,
+                                                                     M, N, K);
+  } else {
+    ffn_gemm_kernel<EPI><<<dim3(static_cast<unsigned>((M / kBM) * (N / kBN))), dim3(kThreads), 0,
+                           stream>>>(A, scale, B, R, C, C2, Cf, M, N, K);
+  }
+  return check_launch(name);
+}
+
+int launch_transpose(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t cols,
+                     const float* scale, hipStream_t stream) {
+  const int vec = rows % 64 == 0 && cols % 64 == 0 && aligned16(src) && aligned16(dst);
+  const dim3 grid(static_cast<unsigned>((cols + 63) / 64), static_cast<unsigned>((rows + 63) / 64));
+  transpose_bf16_kernel<<<grid, 256, 0, stream>>>(src, dst, static_cast<int>(rows),
+                                                  static_cast<int>(cols), scale, vec);
+  return check_launch("transpose_bf16_kernel");
+}
+
+// Backward workspace, in order (each region 256-byte aligned): rstd [M]
+// fp32; u, du [M, f] and h^T, du^T [f, M] bf16; W1^T [d, f] and W2^T [f, d]
+// bf16; dout^T, a^T [d, M] bf16; da [M, d] fp32.
+struct BwdLayout {
+  size_t rstd, u, du, ht, dut, w1t, w2t, doutt, at, da, total;
+};
+BwdLayout bwd_layout(int64_t M, int64_t d, int64_t f) {
+  BwdLayout l;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += align_up(bytes, 256);
+    return at;
+  };
+  l.rstd = take(M * sizeof(float));
+  l.u = take(M * f * 2);
+  l.du = take(M * f * 2);
+  l.ht = take(M * f * 2);
+  l.dut = take(M * f * 2);
+  l.w1t = take(d * f * 2);
+  l.w2t = take(d * f * 2);
+  l.doutt = take(M * d * 2);
+  l.at = take(M * d * 2);
+  l.da = take(M * d * sizeof(float));
+  l.total = o;
+  return l;
+}
+
+int check_ffn_shape(int64_t rows, int64_t d, int64_t f) {
+  if (rows < 0 || d < 1 || f < 1)
+    return set_error(CREDIT_ERR_BAD_SHAPE, "ffn: need rows >= 0, d >= 1, f >= 1");
+  if (rows % kBM != 0 || d % kBN != 0 || f % kBN != 0 || d % kBK != 0 || f % kBK != 0)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "ffn: rows, d and f must be multiples of 128 (got %lld, %lld, %lld)",
+                     static_cast<long long>(rows), static_cast<long long>(d),
+                     static_cast<long long>(f));
+  if (rows > (int64_t{1} << 24) || d > (int64_t{1} << 20) || f > (int64_t{1} << 20) ||
+      rows * f >= (int64_t{1} << 31) || d * f >= (int64_t{1} << 31) ||
+      rows * d >= (int64_t{1} << 31))
+    return set_error(CREDIT_ERR_BAD_SHAPE, "ffn: shape too large");
+  return CREDIT_OK;
 }
 
 }  // namespace
@@ -421,6 +648,10 @@ int enable_big_lds() {
 size_t ffn_workspace(int64_t rows, int64_t ffn_dim) {
   return align_up(static_cast<size_t>(rows) * sizeof(float), 256) +
          align_up(static_cast<size_t>(rows) * ffn_dim * sizeof(uint16_t), 256);
+}
+
+size_t ffn_bwd_workspace(int64_t rows, int64_t d, int64_t ffn_dim) {
+  return bwd_layout(rows, d, ffn_dim).total;
 }
 
 }  // namespace credit
@@ -436,10 +667,7 @@ extern "C" int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t
   if (rows == 0) return CREDIT_OK;
   if (rows > (int64_t{1} << 30))
     return set_error(CREDIT_ERR_BAD_SHAPE, "transpose supports at most 2^30 rows");
-  const dim3 grid(static_cast<unsigned>((cols + 63) / 64), static_cast<unsigned>((rows + 63) / 64));
-  transpose_bf16_kernel<<<grid, 256, 0, cfg_stream(cfg)>>>(src, dst, static_cast<int>(rows),
-                                                           static_cast<int>(cols));
-  return check_launch("transpose_bf16_kernel");
+  return launch_transpose(src, dst, rows, cols, nullptr, cfg_stream(cfg));
 }
 
 extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w1,
@@ -451,16 +679,8 @@ extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w
   CREDIT_TRY(check_ptr(w2, "w2"));
   CREDIT_TRY(check_row_ptr(out, "out", rows));
   CREDIT_TRY(check_cfg(cfg));
-  if (rows < 0 || d < 1 || f < 1)
-    return set_error(CREDIT_ERR_BAD_SHAPE, "ffn: need rows >= 0, d >= 1, f >= 1");
+  CREDIT_TRY(check_ffn_shape(rows, d, f));
   if (!(eps >= 0.0f)) return set_error(CREDIT_ERR_BAD_CONFIG, "eps must be >= 0");
-  if (rows % kBM != 0 || d % kBN != 0 || f % kBN != 0 || d % kBK != 0 || f % kBK != 0)
-    return set_error(CREDIT_ERR_UNSUPPORTED,
-                     "ffn: rows, d and f must be multiples of 128 (got %lld, %lld, %lld)",
-                     static_cast<long long>(rows), static_cast<long long>(d),
-                     static_cast<long long>(f));
-  if (rows > (int64_t{1} << 24) || d > (int64_t{1} << 20) || f > (int64_t{1} << 20))
-    return set_error(CREDIT_ERR_BAD_SHAPE, "ffn: shape too large");
   if (!aligned16(x) || !aligned16(w1) || !aligned16(w2) || !aligned16(out))
     return set_error(CREDIT_ERR_ALIGNMENT, "ffn: x, w1, w2 and out must be 16-byte aligned");
   if (rows == 0) return CREDIT_OK;
@@ -473,29 +693,83 @@ extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w
   const int M = static_cast<int>(rows), D = static_cast<int>(d), F = static_cast<int>(f);
   ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, D, eps);
   CREDIT_TRY(check_launch("ffn_rstd_kernel"));
-  // The 256-tile kernels: every dimension a multiple of 256 (so K / 32 >=
-  // kStages), tile counts a multiple of the 8 XCDs, 32-bit element offsets.
-  const bool big = M % kBig == 0 && D % kBig == 0 && F % kBig == 0 &&
-                   ((M / kBig) * (F / kBig)) % 8 == 0 && ((M / kBig) * (D / kBig)) % 8 == 0 &&
-                   static_cast<int64_t>(M) * F < (int64_t{1} << 31) &&
-                   static_cast<int64_t>(F) * D < (int64_t{1} << 31);
-  if (big) {
-    CREDIT_TRY(enable_big_lds());
-    const unsigned g1 = static_cast<unsigned>((M / kBig) * (F / kBig));
-    ffn_gemm256_kernel<kEpiGelu><<<dim3(g1), dim3(kBigThreads), kBigLds, stream>>>(
-        x, rstd, w1, nullptr, h, M, F, D);
-    CREDIT_TRY(check_launch("ffn_gemm256_kernel<gelu>"));
-    const unsigned g2 = static_cast<unsigned>((M / kBig) * (D / kBig));
-    ffn_gemm256_kernel<kEpiResidual><<<dim3(g2), dim3(kBigThreads), kBigLds, stream>>>(
-        h, nullptr, w2, x, out, M, D, F);
-    return check_launch("ffn_gemm256_kernel<residual>");
+  CREDIT_TRY(launch_gemm<kEpiGelu>(x, rstd, w1, nullptr, h, nullptr, nullptr, M, F, D, stream,
+                                   "ffn gemm1 (gelu)"));
+  return launch_gemm<kEpiResidual>(h, nullptr, w2, x, out, nullptr, nullptr, M, D, F, stream,
+                                   "ffn gemm2 (residual)");
+}
+
+extern "C" int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_t* w1,
+                                                const uint16_t* w2, const uint16_t* dout,
+                                                uint16_t* dx, uint16_t* dw1, uint16_t* dw2,
+                                                int64_t rows, int64_t d, int64_t f, float eps,
+                                                const credit_cfg* cfg) {
+  CREDIT_TRY(check_row_ptr(x, "x", rows));
+  CREDIT_TRY(check_ptr(w1, "w1"));
+  CREDIT_TRY(check_ptr(w2, "w2"));
+  CREDIT_TRY(check_row_ptr(dout, "dout", rows));
+  CREDIT_TRY(check_row_ptr(dx, "dx", rows));
+  CREDIT_TRY(check_ptr(dw1, "dw1"));
+  CREDIT_TRY(check_ptr(dw2, "dw2"));
+  CREDIT_TRY(check_cfg(cfg));
+  CREDIT_TRY(check_ffn_shape(rows, d, f));
+  if (!(eps >= 0.0f)) return set_error(CREDIT_ERR_BAD_CONFIG, "eps must be >= 0");
+  for (const void* p : {static_cast<const void*>(x), static_cast<const void*>(w1),
+                        static_cast<const void*>(w2), static_cast<const void*>(dout),
+                        static_cast<const void*>(dx), static_cast<const void*>(dw1),
+                        static_cast<const void*>(dw2)})
+    if (p && !aligned16(p))
+      return set_error(CREDIT_ERR_ALIGNMENT, "ffn backward: every buffer must be 16-byte aligned");
+  hipStream_t stream = cfg_stream(cfg);
+  if (rows == 0) {
+    // No rows: the weight gradients are sums over nothing (zero bits; a
+    // fill kernel rather than a memset, so the call can be graph-captured).
+    const int64_t words = d * f / 2;  // two bf16 per fp32 word (d, f even)
+    const unsigned blocks = static_cast<unsigned>((words + 255) / 256);
+    fill_f32_kernel<<<dim3(blocks), dim3(256), 0, stream>>>(reinterpret_cast<float*>(dw1), 0.0f,
+                                                             words);
+    CREDIT_TRY(check_launch("fill_f32_kernel"));
+    fill_f32_kernel<<<dim3(blocks), dim3(256), 0, stream>>>(reinterpret_cast<float*>(dw2), 0.0f,
+                                                             words);
+    return check_launch("fill_f32_kernel");
   }
-  const unsigned g1 = static_cast<unsigned>((M / kBM) * (F / kBN));
-  ffn_gemm_kernel<kEpiGelu><<<dim3(g1), dim3(kThreads), 0, stream>>>(x, rstd, w1, nullptr, h, M,
-                                                                    F, D);
-  CREDIT_TRY(check_launch("ffn_gemm_kernel<gelu>"));
-  const unsigned g2 = static_cast<unsigned>((M / kBM) * (D / kBN));
-  ffn_gemm_kernel<kEpiResidual><<<dim3(g2), dim3(kThreads), 0, stream>>>(h, nullptr, w2, x, out,
-                                                                        M, D, F);
-  return check_launch("ffn_gemm_kernel<residual>");
+  const BwdLayout L = bwd_layout(rows, d, f);
+  char* ws = nullptr;
+  CREDIT_TRY(acquire_workspace(cfg, L.total, &ws));
+  char* b = ws_scratch(ws);
+  float* rstd = reinterpret_cast<float*>(b + L.rstd);
+  uint16_t* u = reinterpret_cast<uint16_t*>(b + L.u);
+  uint16_t* du = reinterpret_cast<uint16_t*>(b + L.du);
+  uint16_t* ht = reinterpret_cast<uint16_t*>(b + L.ht);
+  uint16_t* dut = reinterpret_cast<uint16_t*>(b + L.dut);
+  uint16_t* w1t = reinterpret_cast<uint16_t*>(b + L.w1t);
+  uint16_t* w2t = reinterpret_cast<uint16_t*>(b + L.w2t);
+  uint16_t* doutt = reinterpret_cast<uint16_t*>(b + L.doutt);
+  uint16_t* at = reinterpret_cast<uint16_t*>(b + L.at);
+  float* da = reinterpret_cast<float*>(b + L.da);
+  const int M = static_cast<int>(rows), D = static_cast<int>(d), F = static_cast<int>(f);
+  ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, D, eps);
+  CREDIT_TRY(check_launch("ffn_rstd_kernel"));
+  // Operands in the K-contiguous layout the GEMM reads.
+  CREDIT_TRY(launch_transpose(w1, w1t, F, D, nullptr, stream));    // W1^T [d, f]
+  CREDIT_TRY(launch_transpose(w2, w2t, D, F, nullptr, stream));    // W2^T [f, d]
+  CREDIT_TRY(launch_transpose(dout, doutt, M, D, nullptr, stream));
+  CREDIT_TRY(launch_transpose(x, at, M, D, rstd, stream));         // a^T = bf16(x rstd)^T
+  // u = (x W1^T) rstd, h^T = GELU(u)^T.
+  CREDIT_TRY(launch_gemm<kEpiUH>(x, rstd, w1, nullptr, u, ht, nullptr, M, F, D, stream,
+                                 "ffn bwd gemm u"));
+  // du = (dout W2) * GELU'(u), and du^T.
+  CREDIT_TRY(launch_gemm<kEpiGeluBwd>(dout, nullptr, w2t, u, du, dut, nullptr, M, F, D, stream,
+                                      "ffn bwd gemm du"));
+  // dW2 [d, f] = dout^T h.
+  CREDIT_TRY(launch_gemm<kEpiStore>(doutt, nullptr, ht, nullptr, dw2, nullptr, nullptr, D, F, M,
+                                    stream, "ffn bwd gemm dw2"));
+  // dW1 [f, d] = du^T a.
+  CREDIT_TRY(launch_gemm<kEpiStore>(dut, nullptr, at, nullptr, dw1, nullptr, nullptr, F, D, M,
+                                    stream, "ffn bwd gemm dw1"));
+  // da [M, d] = du W1 (fp32), then dx = dout + RMSNorm backward of da.
+  CREDIT_TRY(launch_gemm<kEpiStoreF32>(du, nullptr, w1t, nullptr, nullptr, nullptr, da, M, D, F,
+                                       stream, "ffn bwd gemm da"));
+  ffn_dx_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, da, dout, dx, D);
+  return check_launch("ffn_dx_kernel");
 }

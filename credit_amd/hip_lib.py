@@ -124,6 +124,8 @@ SIGNATURES: dict[str, list] = {
     "credit_weighted_var_bwd_f32": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_pearson_bwd_f32": [_P, _P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_ffn_rmsnorm_gelu_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
+    "credit_ffn_rmsnorm_gelu_bwd_bf16": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
+    "credit_ffn_bwd_workspace_bytes": [_I64, _I64, _I64],
     "credit_layernorm_bwd_f32": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_layernorm_bwd_bf16": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_transpose_bf16": [_P, _P, _I64, _I64, _CFG],
@@ -138,6 +140,7 @@ _RESTYPES = {
     "credit_last_error": ctypes.c_char_p,
     "credit_status_string": ctypes.c_char_p,
     "credit_workspace_bytes": ctypes.c_size_t,
+    "credit_ffn_bwd_workspace_bytes": ctypes.c_size_t,
 }
 
 _lib: ctypes.CDLL | None = None
@@ -488,6 +491,30 @@ def transpose(src: torch.Tensor, dst: torch.Tensor, cfg: CreditCfg | None = None
     )
 
 
+def ffn_backward(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, dout: torch.Tensor,
+                 dx: torch.Tensor, dw1: torch.Tensor, dw2: torch.Tensor, eps: float,
+                 cfg: CreditCfg) -> None:
+    """Gradients of ffn(): dx [rows, d], dw1 [f, d], dw2 [d, f] (the
+    weights' own layouts), all bf16; w1 [f, d], w2 [d, f] as the forward."""
+    rows, d = _rows_cols(x)
+    f = int(w1.shape[0])
+    if tuple(w1.shape) != (f, d) or tuple(w2.shape) != (d, f):
+        raise ValueError(f"ffn_backward: w1 must be [f, d] and w2 [d, f]; got {tuple(w1.shape)}, "
+                         f"{tuple(w2.shape)} for d={d}")
+    for name, t, shape in (("dout", dout, (rows, d)), ("dx", dx, (rows, d)),
+                           ("dw1", dw1, (f, d)), ("dw2", dw2, (d, f))):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"ffn_backward: {name} must be {shape}, got {tuple(t.shape)}")
+    bf = torch.bfloat16
+    check(
+        load_library().credit_ffn_rmsnorm_gelu_bwd_bf16(
+            _ptr(x, "x", bf), _ptr(w1, "w1", bf), _ptr(w2, "w2", bf), _ptr(dout, "dout", bf),
+            _ptr(dx, "dx", bf), _ptr(dw1, "dw1", bf), _ptr(dw2, "dw2", bf), rows, d, f,
+            float(eps), ctypes.byref(cfg)),
+        "credit_ffn_rmsnorm_gelu_bwd_bf16",
+    )
+
+
 def linear_layout(w: torch.Tensor) -> torch.Tensor:
     """A [in, out] weight (the BASELINE's W1 [d, f]) in the nn.Linear layout
     [out, in] the FFN takes, transposed on the GPU by this library."""
@@ -594,6 +621,13 @@ def launch_ffn(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
 LAYERNORM_EPS = 1.0e-5  # dsmem_eval/workloads.py:55
 
 
+def launch_ffn_backward(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    """inputs: (x, w1 [f, d], w2 [d, f], dout); outputs: (dx, dw1, dw2)."""
+    x, w1, w2, dout = inputs
+    dx, dw1, dw2 = outputs
+    ffn_backward(x, w1, w2, dout, dx, dw1, dw2, FFN_EPS, make_cfg(config.variant, config.split))
+
+
 def launch_layernorm_backward(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
     x, dy, gamma = inputs
     (dx,) = outputs
@@ -602,6 +636,7 @@ def launch_layernorm_backward(inputs, outputs, config: LaunchConfig = LaunchConf
 
 HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
     "ffn": launch_ffn,
+    "ffn_backward": launch_ffn_backward,
     "layernorm_backward": launch_layernorm_backward,
     "layernorm_backward_bf16": launch_layernorm_backward,
     "row_sum_max": launch_row_sum_max,
@@ -642,6 +677,9 @@ def prepare_inputs(name: str, cpu_inputs: tuple[torch.Tensor, ...],
     if name == "ffn":
         x, w1, w2 = ins  # W1 [d, f], W2 [f, d]
         return x, linear_layout(w1), linear_layout(w2)
+    if name == "ffn_backward":
+        x, w1, w2, dout = ins
+        return x, linear_layout(w1), linear_layout(w2), dout
     return ins
 
 
@@ -662,6 +700,9 @@ def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch
         return torch.empty_like(x), torch.empty(rows, **f32), torch.empty(rows, **f32)
     if name == "rowwise_quant":
         return torch.empty(x.shape, device=x.device, dtype=torch.int8), torch.empty(rows, **f32)
+    if name == "ffn_backward":
+        w1 = inputs[1]
+        return torch.empty_like(x), torch.empty_like(w1), torch.empty_like(inputs[2])
     if name in ("lars_momentum", "pearson_backward"):
         return torch.empty_like(x), torch.empty_like(x)
     if name == "weighted_var_backward":

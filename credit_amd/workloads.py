@@ -129,6 +129,12 @@ def make_ffn_inputs(rows, cols, g, ffn_dim: int = 28672):
     )
 
 
+def make_ffn_backward_inputs(rows, cols, g, ffn_dim: int = 28672):
+    """The forward's x, W1, W2, then the upstream gradient dout ~ N(0, 1)."""
+    x, w1, w2 = make_ffn_inputs(rows, cols, g, ffn_dim)
+    return x, w1, w2, _normal((rows, cols), 0.0, 1.0, g, torch.bfloat16)
+
+
 # Reference workloads: input ranges of dsmem_eval/workloads.py:45-50,115-119.
 
 
@@ -293,6 +299,18 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         algorithmic_bytes=lambda r, c: 2 * (r * c * 2 + 2 * c * 28672),
         tolerances=(BF16_TOL,),
     ),
+    # The "backward of the fused FFN" next row: dx, dW1, dW2 for dout.
+    "ffn_backward": WorkloadSpec(
+        name="ffn_backward",
+        label="Norm-fused FFN backward (bf16 MFMA)",
+        category="gemm",
+        rows=4096,
+        cols=8192,
+        input_factory=make_ffn_backward_inputs,
+        output_names=("dx", "dw1", "dw2"),
+        algorithmic_bytes=lambda r, c: 2 * (3 * r * c + 4 * c * 28672),
+        tolerances=(BF16_TOL, BF16_TOL, BF16_TOL),
+    ),
     # Reference workloads (dsmem_eval/workloads.py:157-212).
     "layernorm_backward": WorkloadSpec(
         name="layernorm_backward",
@@ -431,3 +449,10 @@ FFN_DIM = 28672
 
 def ffn_flops(rows: int, d: int, f: int = FFN_DIM) -> int:
     return 2 * rows * d * f * 2
+
+
+def ffn_backward_flops(rows: int, d: int, f: int = FFN_DIM) -> int:
+    """The four gradient GEMMs (dh, da, dW1, dW2), 2*M*d*f each; the
+    recompute of the forward's first GEMM is extra work, not counted."""
+    return 2 * rows * d * f * 4
+

@@ -286,6 +286,27 @@ int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w1, const ui
                                  uint16_t* out, int64_t rows, int64_t d, int64_t f, float eps,
                                  const credit_cfg* cfg);
 
+/* ----------------------------------- FFN backward (next row of C5) -------
+ * The gradients of out = x + GELU_tanh(RMSNorm(x) @ W1^T) @ W2^T (unit
+ * RMSNorm weight, eps as the forward) for the upstream gradient dout:
+ *   dx  [rows, d] = dout + RMSNorm backward of (du @ W1), bf16;
+ *   dw1 [f, d]    = du^T a,  dw2 [d, f] = dout^T h   (the weights' own
+ *                                                     nn.Linear layouts), bf16;
+ * with a = bf16(x rstd), u = bf16(a W1^T) (recomputed), h = bf16(GELU(u)),
+ * du = bf16((dout W2) * GELU'(u)); fp32 accumulation on MFMA.  Five GEMMs
+ * (one recompute, four gradients) plus transposes of w1, w2, dout and a into
+ * the K-contiguous operand layout.  No FFN exists in the reference; this is
+ * the "backward of the fused FFN" next row.  Same shape and alignment rules
+ * as the forward.  Needs credit_ffn_bwd_workspace_bytes(rows, d, f) bytes of
+ * workspace (cfg->workspace, or the library's cached buffer). */
+int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_t* w1, const uint16_t* w2,
+                                     const uint16_t* dout, uint16_t* dx, uint16_t* dw1,
+                                     uint16_t* dw2, int64_t rows, int64_t d, int64_t f, float eps,
+                                     const credit_cfg* cfg);
+/* Workspace bytes the FFN backward needs at (rows, d, f); 0 for an empty
+ * shape.  Plumbing of this ABI, no counterpart in the reference. */
+size_t credit_ffn_bwd_workspace_bytes(int64_t rows, int64_t d, int64_t f);
+
 /* dst[c, r] = src[r, c] for a rows x cols bf16 matrix: converts a [d, f]
  * weight to the [f, d] layout credit_ffn_rmsnorm_gelu_bf16 takes.  No
  * counterpart in the reference. */

@@ -254,6 +254,43 @@ def ffn_rmsnorm_gelu(x, w1, w2, eps: float = 1.0e-6, round_h: bool = True):
     return x + h @ f64(w2)
 
 
+def gelu_tanh_grad(v):
+    """d/dv of gelu_tanh: 0.5 (1 + tanh z) + 0.5 v (1 - tanh^2 z) dz/dv,
+    z = sqrt(2/pi) (v + 0.044715 v^3)."""
+    v = f64(v)
+    c = np.sqrt(2.0 / np.pi)
+    t = np.tanh(c * (v + 0.044715 * v**3))
+    return 0.5 * (1.0 + t) + 0.5 * v * (1.0 - t * t) * c * (1.0 + 3.0 * 0.044715 * v * v)
+
+
+def ffn_rmsnorm_gelu_backward(x, w1, w2, dout, eps: float = 1.0e-6, rounding: bool = True):
+    """(dx, dW1, dW2) of out = x + GELU_tanh(RMSNorm(x) @ W1) @ W2 (unit
+    RMSNorm weight) for the upstream gradient dout, with W1 [d, f] and
+    W2 [f, d] in the BASELINE layout; float64 arithmetic.
+
+    rounding=True mirrors the bf16 tensors the GPU path materialises for
+    bf16 MFMA: a = bf16(x rstd) (GEMM operand), u = bf16(a W1) (the saved
+    pre-activation gelu' is taken at), h = bf16(gelu(u)) and du =
+    bf16(dh gelu'(u)).  The RMSNorm backward uses the unrounded x rstd.
+    rounding=False is the exact gradient (tests compare it with autograd).
+    """
+    x, w1, w2, dout = f64(x), f64(w1), f64(w2), f64(dout)
+    r = round_bf16 if rounding else (lambda v: v)
+    rstd = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    ahat = x * rstd
+    a = r(ahat)
+    u_exact = a @ w1
+    u = r(u_exact)
+    h = r(gelu_tanh(u_exact))
+    dh = dout @ w2.T
+    du = r(dh * gelu_tanh_grad(u))
+    dw2 = h.T @ dout
+    dw1 = a.T @ du
+    da = du @ w1.T
+    dx = dout + rstd * (da - ahat * (da * ahat).mean(axis=-1, keepdims=True))
+    return dx, dw1, dw2
+
+
 # --------------------------------------------- reference input generators --
 
 

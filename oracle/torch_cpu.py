@@ -112,6 +112,17 @@ def ffn(x, w1, w2, eps=1.0e-6):
     return (x.float() + (h @ w2).float()).to(x.dtype)
 
 
+def ffn_backward(x, w1, w2, dout, eps=1.0e-6):
+    """Autograd of ffn() in the inputs' dtype: (dx, dW1, dW2)."""
+    x = x.detach().requires_grad_()
+    w1 = w1.detach().requires_grad_()
+    w2 = w2.detach().requires_grad_()
+    a = F.rms_norm(x.float(), (x.shape[-1],), None, eps).to(x.dtype)
+    out = x + F.gelu(a @ w1, approximate="tanh") @ w2
+    out.backward(dout)
+    return x.grad, w1.grad, w2.grad
+
+
 # name -> (function, which BASELINE inputs it takes)
 FUNCTIONS = {
     "row_sum_max": row_sum_max,
@@ -129,4 +140,5 @@ FUNCTIONS = {
     "weighted_var_backward": weighted_var_backward,
     "pearson_backward": pearson_backward,
     "ffn": ffn,
+    "ffn_backward": ffn_backward,
 }

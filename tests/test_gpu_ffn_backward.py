@@ -1,0 +1,121 @@
+"""GPU parity of credit_ffn_rmsnorm_gelu_bwd_bf16: dx, dW1, dW2 of
+out = x + GELU_tanh(RMSNorm(x) @ W1) @ W2 for an upstream gradient dout,
+against the float64 oracle (oracle.reference.ffn_rmsnorm_gelu_backward with
+the GPU path's bf16 roundings of a, u, h and du).
+
+Tolerance: bf16 outputs within rtol 1e-2 of each element plus 1e-2 of the
+tensor's largest magnitude (dW entries are sums over the rows and span a wide
+range; a flat atol of 1e-2 would not scale with them).  A wrong operand
+layout or transpose scrambles every output by O(1) of that scale.  Shapes
+cover the 128-tile GEMMs, the 256-tile GEMMs and mixtures of both; at the
+full C5 shape sampled rows of dx and sampled columns of dW1 / dW2 are checked
+(each depends only on its own rows / columns of the intermediates)."""
+import numpy as np
+import pytest
+import torch
+
+from credit_amd import hip_lib
+from credit_amd.workloads import make_ffn_backward_inputs
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1.0e-6
+
+
+def close(got, exp, name):
+    got = np.asarray(got, np.float64)
+    scale = np.abs(exp).max()
+    excess = np.abs(got - exp) - (1e-2 * np.abs(exp) + 1e-2 * scale)
+    assert np.all(excess <= 0), (f"{name}: max excess {excess.max():.3e} (scale {scale:.3e}) "
+                                 f"at {np.unravel_index(excess.argmax(), excess.shape)}")
+
+
+def make(rows, d, f, seed):
+    g = torch.Generator().manual_seed(seed)
+    return make_ffn_backward_inputs(rows, d, g, ffn_dim=f)
+
+
+def run_bwd(x, w1, w2, dout, gpu):
+    xs, ds = x.to(gpu), dout.to(gpu)
+    w1l = hip_lib.linear_layout(w1.to(gpu))  # [f, d]
+    w2l = hip_lib.linear_layout(w2.to(gpu))  # [d, f]
+    dx = torch.full_like(xs, float("nan"))
+    dw1 = torch.full_like(w1l, float("nan"))
+    dw2 = torch.full_like(w2l, float("nan"))
+    hip_lib.ffn_backward(xs, w1l, w2l, ds, dx, dw1, dw2, EPS, hip_lib.make_cfg())
+    torch.cuda.synchronize()
+    # Back to the BASELINE layouts of the oracle: dW1 [d, f], dW2 [f, d].
+    return (dx.float().cpu().numpy(), dw1.float().cpu().numpy().T,
+            dw2.float().cpu().numpy().T)
+
+
+def oracle(x, w1, w2, dout):
+    return ref.ffn_rmsnorm_gelu_backward(x.float().numpy(), w1.float().numpy(),
+                                         w2.float().numpy(), dout.float().numpy(), EPS)
+
+
+# (128, 128, 128) .. (384, 512, 256): 128-tile GEMMs throughout;
+# (512, 512, 1024): the f-wide GEMMs on 256 tiles, da on 128 tiles;
+# (1024, 512, 2048): every GEMM on 256 tiles.
+@pytest.mark.parametrize("rows,d,f", [(128, 128, 128), (128, 256, 384), (256, 128, 512),
+                                      (384, 512, 256), (512, 512, 1024), (1024, 512, 2048)])
+def test_ffn_backward_small_shapes(gpu, rows, d, f):
+    print(f"ffn_backward rows={rows} d={d} f={f}", flush=True)
+    x, w1, w2, dout = make(rows, d, f, seed=rows + d + f)
+    got = run_bwd(x, w1, w2, dout, gpu)
+    for g, e, name in zip(got, oracle(x, w1, w2, dout), ("dx", "dW1", "dW2")):
+        close(g, e, name)
+
+
+def test_ffn_backward_zero_rows(gpu):
+    """No rows: dx is empty and both weight gradients are exactly zero."""
+    _, w1, w2, _ = make(128, 128, 256, seed=9)
+    w1l = hip_lib.linear_layout(w1.to(gpu))
+    w2l = hip_lib.linear_layout(w2.to(gpu))
+    x = torch.empty(0, 128, dtype=torch.bfloat16, device=gpu)
+    dx = torch.empty_like(x)
+    dw1 = torch.full_like(w1l, 1.0)
+    dw2 = torch.full_like(w2l, 1.0)
+    hip_lib.ffn_backward(x, w1l, w2l, x, dx, dw1, dw2, EPS, hip_lib.make_cfg())
+    torch.cuda.synchronize()
+    assert not bool(dw1.any()) and not bool(dw2.any())
+
+
+def test_ffn_backward_rejects_bad_shapes(gpu):
+    x, w1, w2, dout = make(128, 128, 256, seed=10)
+    xs, ds = x.to(gpu), dout.to(gpu)
+    w1l = hip_lib.linear_layout(w1.to(gpu))
+    w2l = hip_lib.linear_layout(w2.to(gpu))
+    dx, dw1, dw2 = torch.empty_like(xs), torch.empty_like(w1l), torch.empty_like(w2l)
+    with pytest.raises(hip_lib.CreditError):  # rows not a multiple of 128
+        hip_lib.ffn_backward(xs[:100], w1l, w2l, ds[:100], dx[:100], dw1, dw2, EPS,
+                             hip_lib.make_cfg())
+    with pytest.raises(ValueError):  # dw1 in the wrong layout
+        hip_lib.ffn_backward(xs, w1l, w2l, ds, dx, dw2, dw1, EPS, hip_lib.make_cfg())
+
+
+def test_ffn_backward_full_shape_samples(gpu):
+    """C5 (4096 x 8192 x 28672): 8 rows of dx and 4 columns each of dW1 and
+    dW2 against the oracle restricted to what they depend on."""
+    x, w1, w2, dout = make(4096, 8192, 28672, seed=0)
+    dx, dw1, dw2 = run_bwd(x, w1, w2, dout, gpu)
+    assert np.isfinite(dx).all() and np.isfinite(dw1).all() and np.isfinite(dw2).all()
+    X = x.float().numpy().astype(np.float64)
+    W1 = w1.float().numpy().astype(np.float64)
+    W2 = w2.float().numpy().astype(np.float64)
+    G = dout.float().numpy().astype(np.float64)
+    rstd = 1.0 / np.sqrt((X * X).mean(-1, keepdims=True) + EPS)
+    a = ref.round_bf16(X * rstd)
+    # dx rows: each needs only its own row of u, du.
+    rows = np.array([0, 1, 777, 2048, 3000, 4000, 4094, 4095])
+    ex, _, _ = ref.ffn_rmsnorm_gelu_backward(X[rows], W1, W2, G[rows], EPS)
+    close(dx[rows], ex, "dx rows")
+    # dW2[f0, :] = h[:, f0]^T dout and dW1[:, f0] = a^T du[:, f0]: one column
+    # of u (all rows) each.
+    for f0 in (0, 5, 10000, 28671):
+        u = a @ W1[:, f0]
+        h = ref.round_bf16(ref.gelu_tanh(u))
+        du = ref.round_bf16((G @ W2[f0, :]) * ref.gelu_tanh_grad(ref.round_bf16(u)))
+        close(dw2[f0], h @ G, f"dW2 row {f0}")
+        close(dw1[:, f0], a.T @ du, f"dW1 column {f0}")

@@ -238,6 +238,34 @@ def test_ffn_matches_torch_composition():
     np.testing.assert_allclose(out, expect.numpy(), rtol=1e-12, atol=1e-12)
 
 
+def test_gelu_tanh_grad_matches_autograd():
+    v = RNG.uniform(-6, 6, 1000)
+    tv = t64(v).requires_grad_()
+    F.gelu(tv, approximate="tanh").sum().backward()
+    np.testing.assert_allclose(ref.gelu_tanh_grad(v), tv.grad.numpy(), rtol=1e-12, atol=1e-14)
+
+
+def test_ffn_backward_matches_autograd():
+    """Exact gradients (rounding=False) against float64 autograd of the
+    forward composition, for x, W1 and W2."""
+    x = RNG.standard_normal((6, 32))
+    w1 = RNG.normal(0, 1 / math.sqrt(32), (32, 48))
+    w2 = RNG.normal(0, 1 / math.sqrt(48), (48, 32))
+    dout = RNG.standard_normal((6, 32))
+    tx, tw1, tw2 = (t64(t).requires_grad_() for t in (x, w1, w2))
+    a = F.rms_norm(tx, (32,), None, 1e-6)
+    out = tx + F.gelu(a @ tw1, approximate="tanh") @ tw2
+    out.backward(t64(dout))
+    dx, dw1, dw2 = ref.ffn_rmsnorm_gelu_backward(x, w1, w2, dout, 1e-6, rounding=False)
+    np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dw1, tw1.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dw2, tw2.grad.numpy(), rtol=1e-10, atol=1e-12)
+    # The bf16 roundings of the GPU path move the result by bf16 amounts only.
+    rdx, rdw1, rdw2 = ref.ffn_rmsnorm_gelu_backward(x, w1, w2, dout, 1e-6, rounding=True)
+    for got, exact in ((rdx, dx), (rdw1, dw1), (rdw2, dw2)):
+        assert np.abs(got - exact).max() <= 0.05 * np.abs(exact).max()
+
+
 # ------------------------------------------------------------- helpers ----
 
 
