@@ -41,7 +41,9 @@ def oracle(x, w1, w2, rows=None):
     return ref.ffn_rmsnorm_gelu(xs, w1.float().numpy(), w2.float().numpy(), EPS)
 
 
-@pytest.mark.parametrize("shape", [(64, 96), (128, 200), (3, 5), (257, 130)])
+# (64, 128) and (256, 1024) take the 16-byte tile path, the rest the element path.
+@pytest.mark.parametrize("shape", [(64, 96), (128, 200), (3, 5), (257, 130), (64, 128),
+                                   (256, 1024)])
 def test_transpose_is_exact(gpu, shape):
     src = torch.randn(shape, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
     dst = torch.empty(shape[1], shape[0], dtype=torch.bfloat16, device=gpu)
