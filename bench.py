@@ -26,6 +26,9 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+# Workloads whose tensors are bf16 (fp32 accumulation); the rest compute in fp32.
+BF16_WORKLOADS = ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd", "ffn", "ffn_backward",
+                  "layernorm_backward_bf16")
 
 # Kernels one AUTO call launches at the BASELINE shape, and the committed
 # rocprofv3 PMC summary (FETCH_SIZE / WRITE_SIZE, scaled by a copy kernel of
@@ -271,8 +274,7 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if args.workload in ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd", "ffn",
-                                             "layernorm_backward_bf16") else "f32",
+        "dtype": "bf16" if args.workload in BF16_WORKLOADS else "f32",
         "data": "synthetic (seeded CPU generator, BASELINE distributions)",
         "config": {"workload": args.workload, "rows": head["rows"], "cols": head["cols"],
                    "device": info["name"], "arch": info["arch"], "cus": info["cu_count"],
