@@ -22,6 +22,8 @@
 // tiles.  Global tiles are prefetched into registers one K-step ahead, so
 // the next tile's HBM/L2 latency overlaps this step's MFMAs.
 #include <initializer_list>
+#include <type_traits>
+#include <utility>
 
 #include "api_internal.hpp"
 #include "common.hpp"
@@ -230,49 +232,56 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
 }
 
 // ----------------------------------------------------- 256 x 256 tiles ---
-// The main GEMM: C[m, n] = epi(sum_k A[m, k] * B[n, k]) with 256 x 256 x 32
-// tiles per 512-lane workgroup: eight waves, two per SIMD.  Wave (wm, wn) of
-// the 2 x 4 wave grid owns a 128 x 64 block as 4 x 2
-// v_mfma_f32_32x32x16_bf16 tiles (128 fp32 accumulators per lane), so two
-// waves fit one SIMD's register file and each SIMD always has a second wave
-// to issue MFMAs from while the first waits on LDS or a barrier.  Measured
-// on the C5 shapes against the same tile with four 128 x 128 waves: +7%;
-// with the global loads removed the eight-wave loop runs at 58-60% of the
-// bf16 peak, so the rest of the gap is the operand feed.
-//  - Operand tiles go straight from global memory to LDS
-//    (global_load_lds_dwordx4: lane l of a wave writes bytes [16 l, 16 l + 16)
-//    of the wave's 1 KiB LDS block) through a ring of kStages K-steps.
-//  - Each K-step is two half-steps of 8 MFMAs (k = 16 each).  The operand
-//    fragments of the next half-step are read from LDS while the current
-//    half-step's MFMAs issue (reads and MFMAs interleaved, pinned with
-//    sched_group_barrier).
-//  - One barrier per K-step, lagged: it publishes step ks+2 and proves every
-//    wave is done reading stage ks, which the following issue refills; the
-//    next step's first fragments (stage ks+1, published one step earlier)
-//    are read before it.
-//  - The stage index runs at run time (a scalar add per step), so K needs
-//    only to be a multiple of 32 and at least kStages steps.
-//  - LDS rows are 64 bytes (32 bf16 of K); the 16-byte chunk c of row r sits
-//    at position c ^ ((r >> 2) & 3), so the fragment reads of 16 consecutive
-//    rows (four rows share a 256-byte bank row) hit 16 distinct 4-bank groups
-//    (SQ_LDS_BANK_CONFLICT reads 0).
+// The main GEMM: C[m, n] = epi(sum_k A[m, k] * B[n, k]) with 256 x 256 x 64
+// tiles per 256-lane workgroup: four waves, one per SIMD.  Wave (wm, wn) of
+// the 2 x 2 wave grid owns a 128 x 128 block as 4 x 4
+// v_mfma_f32_32x32x16_bf16 tiles (256 fp32 accumulators per lane, held in
+// AGPRs).  Measured on the C5 shapes against the eight-wave 256 x 256 x 32
+// form with global_load_lds it replaces: +13-17% (1.07 -> 1.23-1.27
+// PFLOP/s on GEMM1, bit-identical results); the gain is the K depth of 64
+// (every 8 lanes of a load read one whole 128-byte line) and the buffer form
+// of the LDS-direct load.
+//  - Operand tiles go from global memory straight to LDS with
+//    buffer_load_dwordx4 ... lds: a wave instruction writes 1 KiB of LDS
+//    (lane l at M0 + 16 l), i.e. 8 rows of 128 bytes.  Two stages of
+//    64 KiB (A and B, 256 rows x 64 K each).
+//  - The loads are issued from inline assembly.  The compiler's waitcnt
+//    pass cannot tell an LDS-direct load's destination from the fragment
+//    reads of the other stage and would wait for every load before every
+//    read; here the only waits on the loads are the explicit ones below,
+//    which count them (no other vector-memory instruction is in flight in
+//    the K loop).
+//  - K-step k (64 wide) lives in stage k & 1.  Iteration it runs four
+//    sub-steps of 16 MFMAs (k = 16 each) on stage it & 1, reading the next
+//    sub-step's 8 fragments while the current MFMAs issue (interleaving
+//    pinned with sched_group_barrier / sched_barrier).  The barrier sits
+//    before the last sub-step: own loads of step it+1 landed (vmcnt(0)),
+//    then s_barrier publishes stage (it+1) & 1 to every wave and proves
+//    every wave has read its last fragments of stage it & 1.  The last
+//    sub-step then reads the first fragments of the next stage, and 8 of
+//    the 16 loads of step it+2 (into stage it & 1) go out; the other 8 go
+//    out in the first two sub-steps of the next iteration.  Tail steps
+//    re-load the last K-step into a stage nobody reads again, so the loop
+//    is one basic block with fixed wait counts.
+//  - The barrier is a bare s_barrier after s_waitcnt lgkmcnt(0): a
+//    workgroup-scope release fence would also drain the loads in flight.
+//  - LDS rows are 128 bytes (64 bf16 of K); 16-byte chunk c of row r sits
+//    at position c ^ ((r >> 1) & 7): the 16 lanes of one fragment read
+//    (rows r..r+15, one chunk) and of one load's LDS write (rows r, r+1,
+//    eight chunks each) hit 16 distinct 4-bank groups.  A load lane picks
+//    its global chunk so that it lands at its fixed LDS position.
 //   kEpiGelu:     C = bf16(GELU(acc * scale[m]))   (RMSNorm folded in: the
 //                 row scale commutes with the GEMM)
 //   kEpiResidual: C = bf16(acc + R[m, n])
 constexpr int kBig = 256;
-constexpr int kBigK = 32;
-// Five K-steps in flight through LDS: the waits at the end of step ks need
-// step ks+2 and let ks+3 and ks+4 stay in flight, three steps of load lead
-// (four stages: two steps, measured 10% slower at C5).
-constexpr int kStages = 5;
-constexpr int kBigTile = kBig * kBigK * 2;   // one operand tile, bytes (16 KiB)
+constexpr int kBigK = 64;
+constexpr int kBigTile = kBig * kBigK * 2;   // one operand tile of a stage, bytes (32 KiB)
 constexpr int kBigStage = 2 * kBigTile;      // A and B tiles of one stage
-constexpr int kBigLds = kStages * kBigStage; // 160 KiB, the whole LDS
-static_assert(kStages == 5, "the wait counts in ffn_gemm256_kernel assume five stages");
+constexpr int kBigLds = 2 * kBigStage;       // two stages, 128 KiB
 // Tile blocks within an XCD: 8 M-tiles x 4 N-tiles run concurrently and
 // share their A rows and B columns through that XCD's L2.
 constexpr int kGroupM = 8;
-constexpr int kBigThreads = 512;
+constexpr int kBigThreads = 256;
 
 // s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in
 // bits 15:14; expcnt and lgkmcnt left at their maxima).
@@ -281,12 +290,49 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(((N >> 4) << 14) | (0xF << 8) | (0x7 << 4) | (N & 15));
 }
 
+// Workgroup barrier for LDS only: this wave's LDS operations complete
+// (lgkmcnt(0)), then s_barrier; signal fences keep the compiler from moving
+// memory operations across it.  Vector-memory loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt at their maxima
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// One LDS-direct load: 16 bytes per lane from rsrc at voff + soff into LDS
+// at M0 = m0base + QOFF + 16 * lane.  s_nop covers the M0 write -> LDS-DMA
+// hazard.  M0 is a reserved register to the compiler, which warns that it
+// does not restore a clobbered M0; nothing else in these kernels reads M0
+// (no LDS-direct builtins, GWS, s_sendmsg or indexed register moves), so a
+// value left by one load is only ever overwritten by the next.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <uint32_t QOFF>
+__device__ __forceinline__ void load_to_lds(buffer_rsrc_t rsrc, uint32_t voff, uint32_t m0base,
+                                            uint32_t soff) {
+  asm volatile(
+      "s_add_u32 m0, %2, %3\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %0, %1, %4 offen lds"
+      :
+      : "v"(voff), "s"(rsrc), "s"(m0base), "i"(QOFF), "s"(soff)
+      : "memory", "m0", "scc");
+}
+#pragma clang diagnostic pop
+
 // sched_group_barrier masks.
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Loads per thread per K-step: 16 (8 of A, 8 of B).  Load q of wave w fills
+// rows 8 b .. 8 b + 7 of operand q >> 3, b = (q & 7) * 4 + w.
+constexpr int kLoadsEarly = 8;  // loads of step it+2 issued after iteration it's barrier
+constexpr int kLoadsSub0 = 4;   // ... in sub-step 0 of iteration it+1
+constexpr int kLoadsSub1 = 4;   // ... in sub-step 1 of iteration it+1
+static_assert(kLoadsEarly + kLoadsSub0 + kLoadsSub1 == 16, "16 loads per K-step");
 
 template <int EPI>
 __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
@@ -297,13 +343,12 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves, 128 x 64 each
+  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves, 128 x 128 each
 
   // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin,
   // so XCD x runs ids x, x + 8, ...; give each XCD a contiguous run of the
   // tile sequence, and walk that run in blocks of kGroupM M-tiles (8 M-tiles
-  // x 4 N-tiles run at once per XCD and share A rows and B columns in its L2;
-  // 4 or 16 M-tiles measured 3-8% slower).
+  // x 4 N-tiles run at once per XCD and share A rows and B columns in its L2).
   const int tiles_m = M / kBig, tiles_n = N / kBig;
   const int total = tiles_m * tiles_n;
   const int per_xcd = total / 8;  // host guarantees total % 8 == 0
@@ -314,88 +359,120 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
   const int tm = group * kGroupM + within % gm;
   const int tn = within / gm;
   const int m0 = tm * kBig, n0 = tn * kBig;
-  // Load assignment: instruction i (0..1) of wave w fills LDS rows
-  // (8 i + w) * 16 + lane / 4, swizzled position lane % 4.  Element offsets
-  // fit 32 bits (host checks M*K and N*K < 2^31).
-  uint32_t a_off[2], b_off[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = (8 * i + wave) * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ ((r >> 2) & 3);
-    a_off[i] = static_cast<uint32_t>((m0 + r) * K + c * 8);
-    b_off[i] = static_cast<uint32_t>((n0 + r) * K + c * 8);
-  }
-  auto issue = [&](int ks, int stage) {
-    char* a_base = smem + stage * kBigStage;
-    char* b_base = a_base + kBigTile;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int blk = (8 * i + wave) * 1024;
-      __builtin_amdgcn_global_load_lds(A + a_off[i] + ks * kBigK, (lds_ptr_t)(a_base + blk), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(B + b_off[i] + ks * kBigK, (lds_ptr_t)(b_base + blk), 16, 0, 0);
-    }
+  const int iters = K / kBigK;  // host guarantees an even count >= 2
+
+  // Load addressing.  Lane l of load q reads row 8 b + l / 8 (b as above)
+  // and writes LDS chunk l % 8 of it, so it loads logical chunk
+  // (l % 8) ^ ((row >> 1) & 7) = (l % 8) ^ ((w & 1) * 4 + l / 16).  The
+  // lane-dependent part of the byte offset is one VGPR; row block (q & 7)
+  // * 32 rows and the K step go into the scalar offset.
+  const buffer_rsrc_t rsrc_a = make_rsrc(A + static_cast<size_t>(m0) * K, 256u * K * 2u);
+  const buffer_rsrc_t rsrc_b = make_rsrc(B + static_cast<size_t>(n0) * K, 256u * K * 2u);
+  const int chunk = (lane & 7) ^ (((wave & 1) << 2) + (lane >> 4));
+  const uint32_t voff = static_cast<uint32_t>(((wave * 8 + (lane >> 3)) * K + chunk * 8) * 2);
+  // LDS byte address of smem (an address-space cast; C++ casts do not express it).
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
+  const uint32_t m0_wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+      static_cast<int>(lds0 + wave * 1024)));
+  auto load = [&](int k, auto qc) {
+    constexpr int q = decltype(qc)::value;
+    constexpr uint32_t qoff = static_cast<uint32_t>((q >> 3) * kBigTile + (q & 7) * 4096);
+    const int kc = k < iters ? k : iters - 1;  // tail: a harmless re-load
+    const uint32_t base = static_cast<uint32_t>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(m0_wave + (k & 1) * kBigStage)));
+    const uint32_t soff = static_cast<uint32_t>(
+        __builtin_amdgcn_readfirstlane(kc * kBigK * 2 + (q & 7) * 64 * K));
+    if constexpr (q < 8)
+      load_to_lds<qoff>(rsrc_a, voff, base, soff);
+    else
+      load_to_lds<qoff>(rsrc_b, voff, base, soff);
   };
-  // Fragment addresses: row part (lane-dependent) plus the swizzled chunk of
-  // half-step kk; rows i*32 / j*32 further are +2048 bytes.
-  const int sw = ((lane & 31) >> 2) & 3;
-  const int a_row = (wm * 128 + (lane & 31)) * 64;
-  const int b_row = kBigTile + (wn * 64 + (lane & 31)) * 64;
-  const int koff[2] = {((lane >> 5) ^ sw) << 4, ((2 + (lane >> 5)) ^ sw) << 4};
-  struct F8 { bf16x8_t a[4], b[2]; };
-  auto read_frags = [&](int stage, int kk, F8& f) {
+
+  // Fragment reads: A rows wm*128 + i*32 + (l & 31), B rows wn*128 + j*32 +
+  // (l & 31); K sub-step kk covers logical chunks 2 kk and 2 kk + 1 (lanes
+  // 0-31 and 32-63).
+  const int fsw = ((lane & 31) >> 1) & 7;
+  const int a_frag = (wm * 128 + (lane & 31)) * 128;
+  const int b_frag = kBigTile + (wn * 128 + (lane & 31)) * 128;
+  struct Frags { bf16x8_t a[4], b[4]; };
+  auto frag = [&](int stage, int kk, int idx) {
+    const int c = ((2 * kk + (lane >> 5)) ^ fsw) << 4;
     const char* base = smem + stage * kBigStage;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      f.a[i] = *reinterpret_cast<const bf16x8_t*>(base + a_row + koff[kk] + i * 2048);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      f.b[j] = *reinterpret_cast<const bf16x8_t*>(base + b_row + koff[kk] + j * 2048);
+    return idx < 4 ? *reinterpret_cast<const bf16x8_t*>(base + a_frag + idx * 4096 + c)
+                   : *reinterpret_cast<const bf16x8_t*>(base + b_frag + (idx - 4) * 4096 + c);
   };
-  f32x16 acc[4][2];
+  f32x16 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  // 8 MFMAs on `cur` while the 6 fragment reads of `nxt` go out.
-  auto half_step = [&](const F8& cur, F8& nxt, int nstage, int nkk) {
-    read_frags(nstage, nkk, nxt);
+
+  // MFMA M of a sub-step: fragment read M of the next sub-step first (M < 8);
+  // with NL loads numbered Q0.. of step lk, load j follows MFMA
+  // (j + 1) * (16 / NL) - 1.
+  auto mfma = [&]<int Q0, int NL, int Mi>(const Frags& cur, Frags& nxt, int ns, int nkk, int lk) {
+    if constexpr (Mi < 8) {
+      const bf16x8_t v = frag(ns, nkk, Mi);
+      if constexpr (Mi < 4)
+        nxt.a[Mi] = v;
+      else
+        nxt.b[Mi - 4] = v;
+    }
+    acc[Mi >> 2][Mi & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        cur.a[Mi >> 2], cur.b[Mi & 3], acc[Mi >> 2][Mi & 3], 0, 0, 0);
+    if constexpr (NL > 0) {
+      constexpr int stride = 16 / NL;
+      if constexpr ((Mi + 1) % stride == 0 && (Mi + 1) / stride <= NL)
+        load(lk, std::integral_constant<int, Q0 + (Mi + 1) / stride - 1>{});
+    }
+  };
+  auto sub_step = [&]<int Q0, int NL>(const Frags& cur, Frags& nxt, int ns, int nkk, int lk) {
+    [&]<int... Ms>(std::integer_sequence<int, Ms...>) {
+      (mfma.template operator()<Q0, NL, Ms>(cur, nxt, ns, nkk, lk), ...);
+    }(std::make_integer_sequence<int, 16>{});
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur.a[i], cur.b[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int q = 0; q < 6; ++q) {
+    for (int q = 0; q < 8; ++q) {
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
   };
-  const int ksteps = K / kBigK;  // host guarantees ksteps >= kStages
+
+  // Prologue: step 0 whole and the first kLoadsEarly loads of step 1.
+  [&]<int... Qs>(std::integer_sequence<int, Qs...>) {
+    (load(0, std::integral_constant<int, Qs>{}), ...);
+  }(std::make_integer_sequence<int, 16>{});
+  [&]<int... Qs>(std::integer_sequence<int, Qs...>) {
+    (load(1, std::integral_constant<int, Qs>{}), ...);
+  }(std::make_integer_sequence<int, kLoadsEarly>{});
+  wait_vmcnt<kLoadsEarly>();  // own loads of step 0 landed
+  lds_barrier();
+  Frags f0, f1;
 #pragma unroll
-  for (int st = 0; st < kStages; ++st) issue(st, st);
-  wait_vmcnt<4 * (kStages - 2)>();  // steps 0 and 1 landed (this thread's loads)
-  __syncthreads();
-  F8 f0, f1;
-  read_frags(0, 0, f0);
-  int s = 0;
-  for (int ks = 0; ks < ksteps; ++ks) {
-    const int sn = s + 1 == kStages ? 0 : s + 1;
-    half_step(f0, f1, s, 1);   // MFMAs k 0..15; read k 16..31
-    half_step(f1, f0, sn, 0);  // MFMAs k 16..31; read next step
-    // Own loads of step ks+2 landed: steps ks+3 and ks+4 may stay in flight.
-    if (ks + 4 < ksteps)
-      wait_vmcnt<8>();
-    else if (ks + 3 < ksteps)
-      wait_vmcnt<4>();
+  for (int m = 0; m < 8; ++m) {
+    const bf16x8_t v = frag(0, 0, m);
+    if (m < 4)
+      f0.a[m] = v;
     else
-      wait_vmcnt<0>();
-    __syncthreads();
-    if (ks + kStages < ksteps) issue(ks + kStages, s);
-    s = sn;
+      f0.b[m - 4] = v;
   }
+  auto iteration = [&](int it, int cur) {
+    const int nxt = cur ^ 1;
+    sub_step.template operator()<kLoadsEarly, kLoadsSub0>(f0, f1, cur, 1, it + 1);
+    sub_step.template operator()<kLoadsEarly + kLoadsSub0, kLoadsSub1>(f1, f0, cur, 2, it + 1);
+    sub_step.template operator()<0, 0>(f0, f1, cur, 3, it + 1);
+    wait_vmcnt<0>();  // own loads of step it+1 landed
+    lds_barrier();
+    sub_step.template operator()<0, kLoadsEarly>(f1, f0, nxt, 0, it + 2);
+  };
+  for (int it = 0; it < iters; it += 2) {
+    iteration(it, 0);
+    iteration(it + 1, 1);
+  }
+  wait_vmcnt<0>();  // the tail re-loads
 
   // Epilogue.  Accumulator register r of lane l holds row
   // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of its 32 x 32 tile.
@@ -405,11 +482,11 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int mb = m0 + wm * 128 + i * 32 + 8 * q + 4 * (lane >> 5);
-          const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+          const int n = n0 + wn * 128 + j * 32 + (lane & 31);
           uint32_t t[2];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -440,8 +517,8 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
       const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
       const float sc = EPI == kEpiGelu ? scale[m] : 1.0f;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 128 + j * 32 + (lane & 31);
         epilogue<EPI>(acc[i][j][r], sc, m, n, M, N, R, C, C2, Cf);
       }
     }
@@ -567,18 +644,17 @@ int enable_big_lds() {
   return status;
 }
 
-// C[M, N] = epi(A[M, K] B[N, K]^T): the 256-tile kernel when every
-// dimension is a multiple of 256 (so K / 32 >= kStages), the tile count a
-// multiple of the 8 XCDs and element offsets fit 32 bits; otherwise the
-// 128-tile kernel (M, N multiples of 128, K of 64).
+// C[M, N] = epi(A[M, K] B[N, K]^T): the 256-tile kernel when M and N are
+// multiples of 256, K a multiple of 128 (an even number of 64-wide K-steps),
+// the tile count a multiple of the 8 XCDs and a 256-row operand tile
+// (256 * K * 2 bytes) fits a buffer resource; otherwise the 128-tile kernel
+// (M, N multiples of 128, K of 64).
 template <int EPI>
 int launch_gemm(const uint16_t* A, const float* scale, const uint16_t* B, const uint16_t* R,
                 uint16_t* C, uint16_t* C2, float* Cf, int M, int N, int K, hipStream_t stream,
                 const char* name) {
-  const bool big = M % kBig == 0 && N % kBig == 0 && K % kBig == 0 &&
-                   ((M / kBig) * (N / kBig)) % 8 == 0 &&
-                   static_cast<int64_t>(M) * K < (int64_t{1} << 31) &&
-                   static_cast<int64_t>(N) * K < (int64_t{1} << 31);
+  const bool big = M % kBig == 0 && N % kBig == 0 && K % (2 * kBigK) == 0 &&
+                   ((M / kBig) * (N / kBig)) % 8 == 0 && K <= (1 << 22);
   if (big) {
     CREDIT_TRY(enable_big_lds());
     ffn_gemm256_kernel<EPI><<<dim3(static_cast<unsigned>((M / kBig) * (N / kBig))),
