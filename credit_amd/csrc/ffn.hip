@@ -71,23 +71,25 @@ __device__ __forceinline__ float gelu_tanh_grad(float v) {
 }
 
 // One output element of every epilogue.  s is the row scale still to apply
-// (rstd[m] for the 256-tile kernel, 1 where the A tile was scaled on load).
+// (rstd[m] for the 256-tile kernel, 1 where the A tile was scaled on load);
+// rv is R[m, n] widened to fp32 for kEpiResidual and kEpiGeluBwd (unused
+// otherwise).
 template <int EPI>
-__device__ __forceinline__ void epilogue(float acc, float s, int m, int n, int M, int N,
-                                         const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
-                                         uint16_t* __restrict__ C2, float* __restrict__ Cf) {
+__device__ __forceinline__ void epilogue(float acc, float s, float rv, int m, int n, int M, int N,
+                                         uint16_t* __restrict__ C, uint16_t* __restrict__ C2,
+                                         float* __restrict__ Cf) {
   const size_t idx = static_cast<size_t>(m) * N + n;
   const size_t tdx = static_cast<size_t>(n) * M + m;
   if (EPI == kEpiGelu) {
     C[idx] = f32_to_bf16(gelu_tanh(acc * s));
   } else if (EPI == kEpiResidual) {
-    C[idx] = f32_to_bf16(acc + bf16_to_f32(R[idx]));
+    C[idx] = f32_to_bf16(acc + rv);
   } else if (EPI == kEpiUH) {
     const float u = acc * s;
     C[idx] = f32_to_bf16(u);
     C2[tdx] = f32_to_bf16(gelu_tanh(u));
   } else if (EPI == kEpiGeluBwd) {
-    const uint16_t v = f32_to_bf16(acc * gelu_tanh_grad(bf16_to_f32(R[idx])));
+    const uint16_t v = f32_to_bf16(acc * gelu_tanh_grad(rv));
     C[idx] = v;
     C2[tdx] = v;
   } else if (EPI == kEpiStore) {
@@ -96,6 +98,10 @@ __device__ __forceinline__ void epilogue(float acc, float s, int m, int n, int M
     Cf[idx] = acc;
   }
 }
+
+// Epilogues that read a second [M, N] operand.
+template <int EPI>
+constexpr bool kEpiReadsR = EPI == kEpiResidual || EPI == kEpiGeluBwd;
 
 __device__ __forceinline__ u32x4 scale_bf16x8(u32x4 v, float s) {
   return u32x4{pack_bf16x2(bf16_lo(v.x) * s, bf16_hi(v.x) * s),
@@ -227,7 +233,8 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-        epilogue<EPI>(acc[i][j][r], 1.0f, m, n, M, N, R, C, C2, Cf);
+        const float rv = kEpiReadsR<EPI> ? bf16_to_f32(R[static_cast<size_t>(m) * N + n]) : 0.0f;
+        epilogue<EPI>(acc[i][j][r], 1.0f, rv, m, n, M, N, C, C2, Cf);
       }
 }
 
@@ -474,6 +481,30 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
   }
   wait_vmcnt<0>();  // the tail re-loads
 
+  // R tile (256 x 256 bf16 = 128 KiB, the whole LDS) for the epilogues that
+  // read it: LDS-direct loads, 2 rows of 512 bytes per wave instruction
+  // (wave w fills rows 64 w .. 64 w + 63), so the epilogue's per-element
+  // reads come from LDS instead of 256 scattered 2-byte global loads per
+  // lane.
+  const uint16_t* r_tile = reinterpret_cast<const uint16_t*>(smem);
+  if constexpr (kEpiReadsR<EPI>) {
+    lds_barrier();  // every wave has read its last fragments
+    const buffer_rsrc_t rsrc_r = make_rsrc(R + static_cast<size_t>(m0) * N + n0,
+                                           static_cast<uint32_t>((255u * N + 256u) * 2u));
+    const uint32_t voff_r = static_cast<uint32_t>(((lane >> 5) * N + (lane & 31) * 8) * 2);
+    const uint32_t m0_r = static_cast<uint32_t>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(lds0 + wave * 32768)));
+    [&]<int... Is>(std::integer_sequence<int, Is...>) {
+      (load_to_lds<static_cast<uint32_t>(Is * 1024)>(
+           rsrc_r, voff_r, m0_r,
+           static_cast<uint32_t>(__builtin_amdgcn_readfirstlane((64 * wave + 2 * Is) * N * 2))),
+       ...);
+    }(std::make_integer_sequence<int, 32>{});
+    wait_vmcnt<0>();
+    lds_barrier();
+  }
+  auto r_at = [&](int m, int n) { return bf16_to_f32(r_tile[(m - m0) * kBig + (n - n0)]); };
+
   // Epilogue.  Accumulator register r of lane l holds row
   // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of its 32 x 32 tile.
   if (EPI == kEpiUH || EPI == kEpiGeluBwd) {
@@ -497,7 +528,7 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
               c = acc[i][j][4 * q + e] * scale[m];
               ct = gelu_tanh(c);
             } else {
-              c = ct = acc[i][j][4 * q + e] * gelu_tanh_grad(bf16_to_f32(R[idx]));
+              c = ct = acc[i][j][4 * q + e] * gelu_tanh_grad(r_at(m, n));
             }
             C[idx] = f32_to_bf16(c);
             const uint32_t b = f32_to_bf16(ct);
@@ -519,7 +550,7 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n = n0 + wn * 128 + j * 32 + (lane & 31);
-        epilogue<EPI>(acc[i][j][r], sc, m, n, M, N, R, C, C2, Cf);
+        epilogue<EPI>(acc[i][j][r], sc, kEpiReadsR<EPI> ? r_at(m, n) : 0.0f, m, n, M, N, C, C2, Cf);
       }
     }
   }
