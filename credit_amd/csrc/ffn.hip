@@ -678,14 +678,15 @@ int enable_big_lds() {
 // C[M, N] = epi(A[M, K] B[N, K]^T): the 256-tile kernel when M and N are
 // multiples of 256, K a multiple of 128 (an even number of 64-wide K-steps),
 // the tile count a multiple of the 8 XCDs and a 256-row operand tile
-// (256 * K * 2 bytes) fits a buffer resource; otherwise the 128-tile kernel
-// (M, N multiples of 128, K of 64).
+// (256 * K * 2 bytes) and the epilogue's R tile ((255 * N + 256) * 2 bytes)
+// fit a buffer resource; otherwise the 128-tile kernel (M, N multiples of
+// 128, K of 64).
 template <int EPI>
 int launch_gemm(const uint16_t* A, const float* scale, const uint16_t* B, const uint16_t* R,
                 uint16_t* C, uint16_t* C2, float* Cf, int M, int N, int K, hipStream_t stream,
                 const char* name) {
   const bool big = M % kBig == 0 && N % kBig == 0 && K % (2 * kBigK) == 0 &&
-                   ((M / kBig) * (N / kBig)) % 8 == 0 && K <= (1 << 22);
+                   ((M / kBig) * (N / kBig)) % 8 == 0 && K <= (1 << 22) && N <= (1 << 22);
   if (big) {
     CREDIT_TRY(enable_big_lds());
     ffn_gemm256_kernel<EPI><<<dim3(static_cast<unsigned>((M / kBig) * (N / kBig))),
