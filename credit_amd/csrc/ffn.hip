@@ -13,14 +13,15 @@
 //
 // Kernels:
 //  1. ffn_rstd_kernel: rstd per row of x (one read of x, 64 MiB at C5).
-//  2. ffn_gemm_kernel<kEpiGelu>: GEMM1.  The A tile is scaled by rstd and
-//     rounded to bf16 while it is staged into LDS (the RMSNorm is fused into
-//     the operand load); the epilogue applies GELU-tanh and stores h.
-//  3. ffn_gemm_kernel<kEpiResidual>: GEMM2, epilogue adds x.
-// GEMM tile: 128 x 128 x 64 per 256-lane workgroup; wave (wm, wn) of the
-// 2 x 2 wave grid owns a 64 x 64 quadrant as 2 x 2 v_mfma_f32_32x32x16_bf16
-// tiles.  Global tiles are prefetched into registers one K-step ahead, so
-// the next tile's HBM/L2 latency overlaps this step's MFMAs.
+//  2. GEMM1 with epilogue kEpiGelu: h = bf16(GELU_tanh(acc * rstd[m])); the
+//     RMSNorm commutes with the GEMM and is applied as a row scale.
+//  3. GEMM2 with epilogue kEpiResidual: out = bf16(acc + x).
+// Each GEMM runs on ffn_gemm256_kernel (256 x 256 x 64 tiles, four waves,
+// LDS-direct operand loads; the C5 path) when the shape allows, else on
+// ffn_gemm_kernel (128 x 128 x 64 tiles, operands prefetched through
+// registers one K-step ahead, the A tile scaled by rstd and rounded to bf16
+// while it is staged into LDS).  The backward (credit_ffn_rmsnorm_gelu_bwd_bf16)
+// runs five GEMMs on the same two kernels with its own epilogues.
 #include <initializer_list>
 #include <type_traits>
 #include <utility>
