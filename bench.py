@@ -223,7 +223,7 @@ VARIANT_SWEEP = {
     "rmsnorm_fwd": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
     "rmsnorm_bwd": [("read", 0), ("split", 16), ("split", 18), ("split", 32), ("split", 37)],
     "softmax_fwd": [("read", 0), ("split", 4), ("split", 8), ("split", 16), ("split", 32)],
-    "softmax_bwd": [("read", 0), ("split", 8), ("split", 16)],
+    "softmax_bwd": [("read", 0), ("split", 8), ("split", 16), ("split", 32)],
     "softmax_logits_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
     "layernorm_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
     "layernorm_backward_bf16": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
