@@ -653,6 +653,56 @@ HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
 }
 
 
+class _Recorder:
+    """Stands in for the loaded library while a launcher runs under bind():
+    every entry point it calls is recorded with its converted arguments and
+    reports CREDIT_OK."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self._lib = lib
+        self.calls: list[tuple[Callable[..., int], str, tuple]] = []
+
+    def __getattr__(self, name: str):
+        fn = getattr(self._lib, name)
+
+        def record(*args):
+            self.calls.append((fn, name, args))
+            return CREDIT_OK
+
+        return record
+
+
+def bind(name: str, inputs: tuple[torch.Tensor, ...], outputs: tuple[torch.Tensor, ...],
+         config: LaunchConfig = LaunchConfig()) -> Callable[[], None]:
+    """HIP_LAUNCHERS[name](inputs, outputs, config) as a call with its
+    arguments checked and converted once: the returned function makes only
+    the library calls themselves (one ctypes call per entry point), on the
+    torch stream that was current here.  A timing loop over a kernel shorter
+    than the launcher's Python checks measures the kernel this way, not the
+    checks.  The tensors must stay alive and in place while it is used;
+    the runner is single-threaded, and binding swaps the library handle for
+    the duration of one launcher call."""
+    global _lib
+    lib = load_library()
+    recorder = _Recorder(lib)
+    _lib = recorder  # type: ignore[assignment]
+    try:
+        HIP_LAUNCHERS[name](inputs, outputs, config)
+    finally:
+        _lib = lib
+    calls = tuple(recorder.calls)
+    keep = (inputs, outputs)
+
+    def call() -> None:
+        for fn, fname, args in calls:
+            status = fn(*args)
+            if status != CREDIT_OK:
+                raise CreditError(status, fname, last_error())
+
+    call.tensors = keep  # type: ignore[attr-defined]
+    return call
+
+
 def prepare_inputs(name: str, cpu_inputs: tuple[torch.Tensor, ...],
                    device: torch.device | str) -> tuple[torch.Tensor, ...]:
     """The workload registry's inputs (credit_amd.workloads) as launcher

@@ -1,0 +1,249 @@
+"""Writes the golden fixtures in this directory (run from the repository root:
+``python tests/golden/make_golden.py``).
+
+Each ``<case>.npz`` holds the inputs of one launcher call (bf16 tensors as
+their uint16 bit patterns), the expected outputs, and a JSON ``meta`` record:
+workload name, launcher variants to run, input/output dtypes and the check
+for every output (``allclose`` with rtol/atol, ``exact``, or ``rowmax``:
+atol scaled by the row's largest expected magnitude).
+
+The expected outputs come from torch's own CPU routines in float64
+(``F.layer_norm``, ``F.rms_norm``, ``torch.softmax``/``logsumexp``,
+``torch._softmax_backward_data``, autograd), or, where the reference defines
+the operation as a torch operator sequence (``rowwise_quant``,
+``lars_momentum``, ``dsmem_eval/workloads.py:136-154``), from that sequence.
+They are not computed by ``oracle/``: ``tests/test_golden.py`` checks the
+oracle against them, and ``tests/test_gpu_golden.py`` checks the HIP library.
+
+Inputs are drawn by ``credit_amd.workloads`` with the seeds recorded in meta
+(one CPU ``torch.Generator`` per case), plus the edge rows named per case.
+"""
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+ROOT = Path(__file__).resolve().parents[2]
+OUT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from credit_amd.workloads import WORKLOADS  # noqa: E402
+
+FP32 = {"check": "allclose", "rtol": 1e-5, "atol": 1e-6}
+BF16 = {"check": "allclose", "rtol": 1e-2, "atol": 1e-2}
+EXACT = {"check": "exact"}
+
+
+def d64(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().to(torch.float64)
+
+
+def as_array(t: torch.Tensor):
+    """(numpy array, dtype tag) of a CPU tensor; bf16 as uint16 bits."""
+    if t.dtype == torch.bfloat16:
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16), "bf16"
+    if t.dtype == torch.float32:
+        return t.contiguous().numpy(), "f32"
+    if t.dtype == torch.int8:
+        return t.contiguous().numpy(), "i8"
+    raise TypeError(t.dtype)
+
+
+def save(case: str, workload: str, variants, inputs, outputs, checks, note: str, seed: int,
+         out_dtypes) -> None:
+    arrays = {}
+    in_dtypes = []
+    for i, t in enumerate(inputs):
+        arrays[f"in{i}"], tag = as_array(t)
+        in_dtypes.append(tag)
+    for i, t in enumerate(outputs):
+        arrays[f"out{i}"] = np.asarray(t)
+    meta = {
+        "workload": workload,
+        "variants": variants,
+        "inputs": in_dtypes,
+        "outputs": out_dtypes,
+        "checks": checks,
+        "seed": seed,
+        "note": note,
+    }
+    arrays["meta"] = np.array(json.dumps(meta))
+    np.savez_compressed(OUT / f"{case}.npz", **arrays)
+    print(f"{case}: {', '.join(f'{k}{tuple(v.shape)}' for k, v in arrays.items() if k != 'meta')}")
+
+
+def row_sum_max():
+    seed = 101
+    (x,) = WORKLOADS["row_sum_max"].make_inputs(6, 4100, seed=seed)
+    x[1, 7] = float("nan")
+    x[2, 100] = float("inf")
+    x[3, 4099] = float("-inf")
+    x[4, :] = -0.5
+    s = torch.sum(d64(x), -1).numpy()
+    m = torch.amax(x, -1).numpy()
+    save("row_sum_max_6x4100", "row_sum_max", [["auto", 0], ["read", 0], ["split", 2]], (x,),
+         (s, m), [FP32, EXACT], "torch.sum (float64) / torch.amax; NaN, +inf, -inf and a "
+         "constant row", seed, ["f32", "f32"])
+
+
+def layernorm_fwd():
+    for rows, cols, seed, variants in ((9, 4096, 102, [["auto", 0], ["staged", 0], ["read", 0]]),
+                                       (3, 1003, 103, [["auto", 0], ["read", 0]])):
+        x, g, b = WORKLOADS["layernorm_fwd"].make_inputs(rows, cols, seed=seed)
+        x[1, :] = 1.5  # variance 0: y = beta
+        y = F.layer_norm(d64(x), (cols,), d64(g), d64(b), 1e-5).numpy()
+        var, mean = torch.var_mean(d64(x), -1, unbiased=False)
+        rstd = torch.rsqrt(var + 1e-5).numpy()
+        save(f"layernorm_fwd_{rows}x{cols}", "layernorm_fwd", variants, (x, g, b),
+             (y, mean.numpy(), rstd), [BF16, FP32, FP32],
+             "F.layer_norm and torch.var_mean in float64, eps 1e-5; row 1 constant", seed,
+             ["bf16", "f32", "f32"])
+
+
+def rmsnorm():
+    seed = 104
+    rows, cols = 3, 8192
+    x, w, dy = WORKLOADS["rmsnorm_fwd"].make_inputs(rows, cols, seed=seed)
+    x64 = d64(x).requires_grad_()
+    y = F.rms_norm(x64, (cols,), d64(w), 1e-6)
+    rstd = torch.rsqrt(d64(x).pow(2).mean(-1) + 1e-6)
+    save("rmsnorm_fwd_3x8192", "rmsnorm_fwd", [["auto", 0], ["read", 0], ["split", 2]], (x, w),
+         (y.detach().numpy(), rstd.numpy()), [BF16, FP32], "F.rms_norm in float64, eps 1e-6",
+         seed, ["bf16", "f32"])
+    w64 = d64(w).requires_grad_()
+    x64 = d64(x).requires_grad_()
+    F.rms_norm(x64, (cols,), w64, 1e-6).backward(d64(dy))
+    rstd32 = rstd.to(torch.float32)
+    save("rmsnorm_bwd_3x8192", "rmsnorm_bwd", [["auto", 0], ["read", 0], ["split", 2]],
+         (x, w, dy, rstd32), (x64.grad.numpy(), w64.grad.numpy()), [BF16, FP32],
+         "autograd of F.rms_norm in float64 (dx, dweight); rstd input rounded to fp32", seed,
+         ["bf16", "f32"])
+
+
+def softmax():
+    seed = 105
+    rows, cols = 3, 5000
+    x, dy = WORKLOADS["softmax_fwd"].make_inputs(rows, cols, seed=seed)
+    p = torch.softmax(d64(x), -1)
+    lse = torch.logsumexp(d64(x), -1)
+    m = torch.amax(x, -1)
+    save("softmax_fwd_3x5000", "softmax_fwd", [["auto", 0], ["read", 0], ["split", 2]], (x,),
+         (p.numpy(), m.numpy(), lse.numpy()), [FP32, EXACT, FP32],
+         "torch.softmax / torch.logsumexp in float64, torch.amax; N(0, 4) logits with 1% "
+         "set to +20", seed, ["f32", "f32", "f32"])
+    p32 = p.to(torch.float32)
+    dx = torch._softmax_backward_data(d64(dy), d64(p32), -1, torch.float64)
+    save("softmax_bwd_3x5000", "softmax_bwd", [["auto", 0], ["read", 0], ["split", 2]],
+         (p32, dy), (dx.numpy(),), [FP32],
+         "torch._softmax_backward_data in float64 on the fp32 probabilities", seed, ["f32"])
+    seed = 106
+    x, dy = WORKLOADS["softmax_logits_backward"].make_inputs(3, 4096, seed=seed)
+    x64 = d64(x).requires_grad_()
+    torch.softmax(x64, -1).backward(d64(dy))
+    save("softmax_logits_backward_3x4096", "softmax_logits_backward",
+         [["auto", 0], ["read", 0], ["split", 2]], (x, dy), (x64.grad.numpy(),), [FP32],
+         "autograd of torch.softmax in float64", seed, ["f32"])
+
+
+def layernorm_backward():
+    for name, seed, tol, tag in (("layernorm_backward", 107, FP32, "f32"),
+                                 ("layernorm_backward_bf16", 108, BF16, "bf16")):
+        x, dy, gamma = WORKLOADS[name].make_inputs(3, 4096, seed=seed)
+        x64 = d64(x).requires_grad_()
+        F.layer_norm(x64, (4096,), d64(gamma), None, 1e-5).backward(d64(dy))
+        save(f"{name}_3x4096", name, [["auto", 0], ["read", 0], ["split", 2]], (x, dy, gamma),
+             (x64.grad.numpy(),), [tol], "autograd of F.layer_norm in float64, eps 1e-5", seed,
+             [tag])
+
+
+def rowwise_quant():
+    seed = 109
+    (x,) = WORKLOADS["rowwise_quant"].make_inputs(8, 1024, seed=seed)
+    x[2, :] = 0.0  # scale 0, codes 0
+    x[3, :] = torch.linspace(-1.0, 1.0, 1024)
+    # the reference's operator sequence (dsmem_eval/workloads.py:150-154) in fp32
+    max_abs = x.abs().amax(dim=-1, keepdim=True)
+    inv = torch.where(max_abs > 0, 127.0 / max_abs, torch.zeros_like(max_abs))
+    q = torch.round(x * inv).clamp(-127, 127).to(torch.int8)
+    scale = (max_abs / 127.0).squeeze(-1)
+    save("rowwise_quant_8x1024", "rowwise_quant", [["auto", 0], ["read", 0], ["split", 2]],
+         (x,), (q.numpy(), scale.numpy()), [EXACT, EXACT],
+         "the reference's torch operator sequence in fp32; an all-zero row", seed, ["i8", "f32"])
+
+
+def lars_momentum():
+    seed = 110
+    w, g, m = WORKLOADS["lars_momentum"].make_inputs(3, 2048, seed=seed)
+    # dsmem_eval/workloads.py:136-143 in float64 for the new weight; the
+    # update is also defined by its fp32 evaluation, operation by operation.
+    w64, g64, m64 = d64(w), d64(g), d64(m)
+    u64 = 0.9 * m64 + g64 + 0.01 * w64
+    trust = 0.02 * torch.linalg.vector_norm(w64, dim=-1, keepdim=True) / (
+        torch.linalg.vector_norm(u64, dim=-1, keepdim=True) + 1e-6)
+    wn = w64 - 1e-3 * trust * u64
+    u32 = (m * 0.9 + g) + w * 0.01
+    save("lars_momentum_3x2048", "lars_momentum", [["auto", 0], ["read", 0], ["split", 2]],
+         (w, g, m), (wn.numpy(), u32.numpy()), [FP32, EXACT],
+         "torch float64 for the weight; the update as the fp32 expression", seed, ["f32", "f32"])
+
+
+def weighted_var_backward():
+    seed = 111
+    x, w, dy = WORKLOADS["weighted_var_backward"].make_inputs(3, 2048, seed=seed)
+    tx = d64(x).requires_grad_()
+    tw = d64(w)
+    eps = 1e-5
+    inv = 1.0 / (tw.sum(-1, keepdim=True) + eps)
+    mean = (tw * tx).sum(-1, keepdim=True) * inv
+    var = (tw * (tx - mean) ** 2).sum(-1, keepdim=True) * inv
+    ((tx - mean) * torch.rsqrt(var + eps)).backward(d64(dy))
+    save("weighted_var_backward_3x2048", "weighted_var_backward",
+         [["auto", 0], ["read", 0], ["split", 2]], (x, w, dy), (tx.grad.numpy(),), [FP32],
+         "autograd of the weighted standardisation (x - mean_w) / sqrt(var_w + eps) in "
+         "float64; the reference formula drops an O(eps) term (relative 1e-6 here)", seed,
+         ["f32"])
+
+
+def pearson_backward():
+    seed = 112
+    x, y, grad = WORKLOADS["pearson_backward"].make_inputs(3, 2048, seed=seed)
+    tx, ty = d64(x).requires_grad_(), d64(y).requires_grad_()
+    xc = tx - tx.mean(-1, keepdim=True)
+    yc = ty - ty.mean(-1, keepdim=True)
+    r = ((xc * yc).sum(-1, keepdim=True) * torch.rsqrt((xc * xc).sum(-1, keepdim=True) + 1e-6)
+         * torch.rsqrt((yc * yc).sum(-1, keepdim=True) + 1e-6))
+    r.backward(d64(grad))
+    rowmax = {"check": "rowmax", "rtol": 1e-5, "atol": 1e-6}
+    save("pearson_backward_3x2048", "pearson_backward", [["auto", 0], ["read", 0], ["split", 2]],
+         (x, y, grad), (tx.grad.numpy(), ty.grad.numpy()), [rowmax, rowmax],
+         "autograd of the Pearson correlation in float64 (eps 1e-6); gradients scale as 1/N, "
+         "so atol is 1e-6 times the row's largest gradient", seed, ["f32", "f32"])
+
+
+def ffn():
+    seed = 113
+    rows, d, f = 128, 128, 256
+    x, w1, w2 = WORKLOADS["ffn"].input_factory(rows, d, torch.Generator().manual_seed(seed), f)
+    w1l, w2l = w1.t().contiguous(), w2.t().contiguous()  # nn.Linear layouts [f, d], [d, f]
+    u = F.rms_norm(d64(x), (d,), None, 1e-6) @ d64(w1l).t()
+    h = F.gelu(u, approximate="tanh").to(torch.bfloat16)  # the hidden activation is bf16
+    out = d64(x) + d64(h) @ d64(w2l).t()
+    save("ffn_128x128x256", "ffn", [["auto", 0]], (x, w1l, w2l), (out.numpy(),), [BF16],
+         "F.rms_norm -> matmul -> F.gelu(tanh), rounded to bf16 -> matmul -> + x in float64; "
+         "weights in the nn.Linear layout", seed, ["bf16"])
+
+
+def main() -> None:
+    torch.manual_seed(0)
+    for fn in (row_sum_max, layernorm_fwd, rmsnorm, softmax, layernorm_backward, rowwise_quant,
+               lars_momentum, weighted_var_backward, pearson_backward, ffn):
+        fn()
+
+
+if __name__ == "__main__":
+    main()

@@ -66,3 +66,39 @@ def test_layernorm_fwd_full_config(gpu, variant):
     """BASELINE C2: 2048 x 32768 bf16, N(0,1); gamma N(1,.02), beta N(0,.02)."""
     x, g, b = SPEC.make_inputs()
     check(x, g, b, *run(x, g, b, variant, gpu))
+
+
+@pytest.mark.parametrize("shape", [(512, 32768), (773, 32768), (600, 24576), (1030, 16392),
+                                   (2049, 20000)])
+def test_layernorm_fwd_pipeline_rows(gpu, shape):
+    """AUTO's persistent pipeline (2049..4096 vectors per row, at least two
+    rows per CU): row counts that end the three-row rotation at each of its
+    steps, rows shorter than the 4096-vector layout, and the same rows
+    through the one-row-per-workgroup STAGED kernel, which must agree with it
+    up to the fp32 summation order."""
+    print(f"layernorm_fwd pipeline shape={shape}", flush=True)
+    x, g, b = SPEC.make_inputs(*shape, seed=37)
+    x[5, :] = 2.25  # a constant row: var = 0, y = beta
+    y, mean, rstd = run(x, g, b, "auto", gpu)
+    check(x, g, b, y, mean, rstd)
+    assert mean[5] == 2.25
+    np.testing.assert_allclose(y[5], b.float().numpy(), atol=1e-6)
+    sy, smean, srstd = run(x, g, b, "staged", gpu)
+    np.testing.assert_allclose(mean, smean, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(rstd, srstd, rtol=1e-6)
+    np.testing.assert_allclose(y, sy, rtol=1e-2, atol=1e-2)  # bf16 rounding flips only
+
+
+def test_layernorm_fwd_pipeline_back_to_back(gpu):
+    """Calls queued without synchronisation on one stream, each checked."""
+    x, g, b = SPEC.make_inputs(700, 32768, seed=3)
+    ins = tuple(t.to(gpu) for t in (x, g, b))
+    outs = [hip_lib.allocate_outputs("layernorm_fwd", ins) for _ in range(3)]
+    for o in outs:
+        hip_lib.layernorm_fwd(*ins, *o, EPS, hip_lib.make_cfg("auto"))
+    torch.cuda.synchronize()
+    first = [t.cpu() for t in outs[0]]
+    for o in outs[1:]:
+        for a, b_ in zip(first, o):
+            assert torch.equal(a, b_.cpu())
+    check(x, g, b, *(t.float().numpy() for t in first))
