@@ -83,6 +83,7 @@ class RunConfig:
     profile_only: bool = False
     tensor_bytes: int = DEFAULT_TENSOR_BYTES
     buffer_sets: int = 3
+    settle_ms: float = 20.0
 
     @classmethod
     def from_dict(cls, raw: dict[str, Any]) -> "RunConfig":
@@ -97,6 +98,7 @@ class RunConfig:
             profile_only=bool(raw.get("profile_only", False)),
             tensor_bytes=int(raw.get("tensor_bytes", DEFAULT_TENSOR_BYTES)),
             buffer_sets=int(raw.get("buffer_sets", 3)),
+            settle_ms=float(raw.get("settle_ms", 20.0)),
         )
         cfg.validate()
         return cfg
@@ -147,9 +149,16 @@ def summarize(samples: Iterable[float]) -> dict[str, float]:
 
 
 def benchmark_callable(fn: Callable[[int], object], warmup: int, iterations: int,
-                       trials: int) -> list[float]:
+                       trials: int, settle_ms: float = 0.0) -> list[float]:
     """ms per call, one sample per trial (runner.py:166-182); fn(i) gets the
-    call index so callers can rotate buffer sets."""
+    call index so callers can rotate buffer sets.  settle_ms of wall time
+    (synchronised every 8 calls) run before the warmup calls: HBM-bound work
+    after an idle period runs slow for its first 10-20 ms on the MI355X."""
+    t_end = time.perf_counter() + settle_ms / 1e3
+    while time.perf_counter() < t_end:
+        for i in range(8):
+            fn(i)
+        torch.cuda.synchronize()
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -214,9 +223,11 @@ def measure_point(name: str, spec: WorkloadSpec, rows: int, cols: int, cfg: RunC
             torch.cuda.synchronize()
             hip_lib.check_watchdog()
             row["correct"] = all(_close(o, r) for o, r in zip(outs[0], reference))
-            samples = benchmark_callable(
-                lambda i: launcher(sets[i % len(sets)], outs[i % len(outs)], lc),
-                cfg.warmup, cfg.iterations, cfg.trials)
+            # Arguments checked and converted once per buffer set: the timed
+            # calls are the library calls alone, not the launcher's Python.
+            bound = [hip_lib.bind(name, ins, o, lc) for ins, o in zip(sets, outs)]
+            samples = benchmark_callable(lambda i: bound[i % len(bound)](), cfg.warmup,
+                                         cfg.iterations, cfg.trials, cfg.settle_ms)
         except hip_lib.CreditError as err:
             row["error"] = f"{err.status}: {err}"
             samples = []
@@ -393,6 +404,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--iterations", type=int, default=20)
     ap.add_argument("--trials", type=int, default=5)
+    ap.add_argument("--settle-ms", type=float, default=20.0,
+                    help="wall time each variant runs before its warmup calls")
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--profile-only", action="store_true")
     ap.add_argument("--profile-text", type=Path,
@@ -404,7 +417,7 @@ def main(argv=None) -> int:
         w.strip() for w in args.workloads.split(",") if w.strip())
     config = {"workloads": workloads, "n_values": args.n_values, "splits": args.splits,
               "warmup": args.warmup, "iterations": args.iterations, "trials": args.trials,
-              "quick": args.quick, "profile_only": args.profile_only}
+              "settle_ms": args.settle_ms, "quick": args.quick, "profile_only": args.profile_only}
     text = args.profile_text.read_text() if args.profile_text else None
     meta = run_suite(config, args.output_dir.resolve(), text)
     print(f"Status: {meta['status']}")
