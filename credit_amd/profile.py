@@ -158,6 +158,30 @@ def profile_as_dict(profile: DeviceProfile) -> dict[str, Any]:
     return asdict(profile)
 
 
+def run_ffn_reference(rows: int = 4096, d: int = 8192, f: int = 28672) -> None:
+    """The FFN forward (this library's two GEMMs) and the vendor library's GEMM
+    of GEMM1's shape (torch.matmul -> hipBLASLt), twice each, on random bf16
+    operands in the nn.Linear layouts: a workload for per-kernel counter
+    collection (rocprofv3 --pmc), not a benchmark."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x = torch.randn(rows, d, device=dev, generator=g).bfloat16()
+    w1 = (torch.randn(f, d, device=dev, generator=g) / d ** 0.5).bfloat16()
+    w2 = (torch.randn(d, f, device=dev, generator=g) / f ** 0.5).bfloat16()
+    out = torch.empty_like(x)
+    cfg = hip_lib.make_cfg("auto")
+    for _ in range(2):
+        hip_lib.ffn(x, w1, w2, out, hip_lib.FFN_EPS, cfg)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        torch.matmul(x, w1.t())
+    torch.cuda.synchronize()
+    print("ffn reference workload done", flush=True)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="gfx950 calibration microbenchmarks")
     ap.add_argument("--hbm-bytes", type=int, default=1 << 30)
@@ -167,9 +191,15 @@ def main(argv=None) -> int:
     ap.add_argument("--only", choices=sorted(hip_lib.MICROBENCH),
                     help="run just this microbenchmark (e.g. hbm_copy of --hbm-bytes as the "
                          "known-size reference for PMC byte counters) and print its results")
+    ap.add_argument("--ffn-reference", action="store_true",
+                    help="run the C5 FFN forward twice, then hipBLASLt (torch.matmul) on GEMM1's "
+                         "shape twice: the workload of the FFN-against-library counter runs")
     args = ap.parse_args(argv)
     import torch  # noqa: F401  (loads the HIP runtime torch uses before the library)
 
+    if args.ffn_reference:
+        run_ffn_reference()
+        return 0
     if args.only:
         res = hip_lib.microbench(args.only, args.hbm_bytes, args.iters)
         print(f"{args.only} bytes={args.hbm_bytes} iters={args.iters} results={res}", flush=True)
