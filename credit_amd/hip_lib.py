@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import threading
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Callable
@@ -144,6 +145,8 @@ _RESTYPES = {
 }
 
 _lib: ctypes.CDLL | None = None
+# Per-thread stand-in for the library while bind() records a launcher.
+_recording = threading.local()
 
 
 def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
@@ -153,8 +156,12 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     the one the library binds to (both carry the soname libamdhip64.so.7).
     """
     global _lib
-    if _lib is not None and path is None:
-        return _lib
+    if path is None:
+        recorder = getattr(_recording, "recorder", None)
+        if recorder is not None:
+            return recorder
+        if _lib is not None:
+            return _lib
     lib_path = Path(path) if path is not None else LIB_PATH
     if not lib_path.is_file():
         raise FileNotFoundError(
@@ -679,24 +686,22 @@ def bind(name: str, inputs: tuple[torch.Tensor, ...], outputs: tuple[torch.Tenso
     the library calls themselves (one ctypes call per entry point), on the
     torch stream that was current here.  A timing loop over a kernel shorter
     than the launcher's Python checks measures the kernel this way, not the
-    checks.  The tensors must stay alive and in place while it is used;
-    the runner is single-threaded, and binding swaps the library handle for
-    the duration of one launcher call."""
-    global _lib
-    lib = load_library()
-    recorder = _Recorder(lib)
-    _lib = recorder  # type: ignore[assignment]
+    checks.  The tensors must stay alive and in place while it is used.
+    Recording is per thread: launchers called on other threads meanwhile
+    run as usual."""
+    recorder = _Recorder(load_library())
+    _recording.recorder = recorder
     try:
         HIP_LAUNCHERS[name](inputs, outputs, config)
     finally:
-        _lib = lib
+        _recording.recorder = None
     calls = tuple(recorder.calls)
     keep = (inputs, outputs)
 
     def call() -> None:
         for fn, fname, args in calls:
             status = fn(*args)
-            if status != CREDIT_OK:
+            if isinstance(status, int) and status != CREDIT_OK:
                 raise CreditError(status, fname, last_error())
 
     call.tensors = keep  # type: ignore[attr-defined]

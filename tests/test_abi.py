@@ -108,3 +108,36 @@ def test_query_device_without_gpu_fails_cleanly(lib):
     info = hip_lib.DeviceInfo()
     assert lib.credit_query_device(-1, ctypes.byref(info)) == -8
     assert lib.credit_query_device(0, None) == -1
+
+
+def test_bind_records_per_thread_and_replays_statuses(lib):
+    """hip_lib.bind records a launcher's library calls (each reports OK while
+    recording) and replays them, raising on a failing status; another thread
+    sees the real library meanwhile.  No GPU: the replayed call fails
+    argument validation, which runs before any HIP call."""
+    import threading
+
+    from credit_amd import hip_lib
+
+    seen = {}
+
+    def other_thread():
+        seen["lib"] = hip_lib.load_library()
+
+    def launcher(inputs, outputs, config):
+        t = threading.Thread(target=other_thread)
+        t.start()
+        t.join()
+        hip_lib.check(hip_lib.load_library().credit_row_sum_max_f32(None, None, None, 4, 4, None),
+                      "credit_row_sum_max_f32")
+
+    hip_lib.HIP_LAUNCHERS["_test_bind"] = launcher
+    try:
+        call = hip_lib.bind("_test_bind", (), ())
+    finally:
+        del hip_lib.HIP_LAUNCHERS["_test_bind"]
+    assert seen["lib"] is hip_lib.load_library()
+    assert not isinstance(hip_lib.load_library(), hip_lib._Recorder)
+    with pytest.raises(hip_lib.CreditError) as err:
+        call()
+    assert err.value.status < 0
