@@ -251,26 +251,32 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
 // of the LDS-direct load.
 //  - Operand tiles go from global memory straight to LDS with
 //    buffer_load_dwordx4 ... lds: a wave instruction writes 1 KiB of LDS
-//    (lane l at M0 + 16 l), i.e. 8 rows of 128 bytes.  Two stages of
-//    64 KiB (A and B, 256 rows x 64 K each).
+//    (lane l at M0 + 16 l), i.e. 8 rows of 128 bytes.  An operand tile
+//    (256 rows x 64 K) is 32 KiB; A has two stages and B three, 160 KiB.
 //  - The loads are issued from inline assembly.  The compiler's waitcnt
 //    pass cannot tell an LDS-direct load's destination from the fragment
 //    reads of the other stage and would wait for every load before every
 //    read; here the only waits on the loads are the explicit ones below,
 //    which count them (no other vector-memory instruction is in flight in
 //    the K loop).
-//  - K-step k (64 wide) lives in stage k & 1.  Iteration it runs four
-//    sub-steps of 16 MFMAs (k = 16 each) on stage it & 1, reading the next
+//  - K-step k (64 wide) reads A stage k & 1 and B stage k % 3.  Iteration
+//    it runs four sub-steps of 16 MFMAs (k = 16 each), reading the next
 //    sub-step's 8 fragments while the current MFMAs issue (interleaving
 //    pinned with sched_group_barrier / sched_barrier).  The barrier sits
-//    before the last sub-step: own loads of step it+1 landed (vmcnt(0)),
-//    then s_barrier publishes stage (it+1) & 1 to every wave and proves
-//    every wave has read its last fragments of stage it & 1.  The last
-//    sub-step then reads the first fragments of the next stage, and 8 of
-//    the 16 loads of step it+2 (into stage it & 1) go out; the other 8 go
-//    out in the first two sub-steps of the next iteration.  Tail steps
-//    re-load the last K-step into a stage nobody reads again, so the loop
-//    is one basic block with fixed wait counts.
+//    before the last sub-step: own loads of step it+1 landed, then
+//    s_barrier publishes step it+1's stages to every wave and proves every
+//    wave has read its last fragments of step it.  The last sub-step then
+//    reads the first fragments of step it+1.
+//  - Loads of step it+2: B (8 per lane) in sub-steps 0-2 of iteration it,
+//    3 + 3 + 2 -- its stage (it+2) % 3 was last read in step it-1, before
+//    the previous barrier; A (8) in sub-step 3, after the barrier, into A
+//    stage it & 1.  Every load thus has at least three sub-steps to land
+//    before the wait for it, vmcnt(8) (step it+2's B loads stay in flight).
+//    Against two 64 KiB stages, where the last loads of a step had one
+//    sub-step: +5.6% on the C5 forward (1291 -> 1363 TFLOP/s, bit-identical
+//    outputs).  B's loads spread 2/3/3: the same; 4/4/0 -1%, 0/4/4 -1%,
+//    all 8 in sub-step 0: -5%.  Tail steps re-load the last K-step into
+//    stages nobody reads again, so the loop body has fixed wait counts.
 //  - The barrier is a bare s_barrier after s_waitcnt lgkmcnt(0): a
 //    workgroup-scope release fence would also drain the loads in flight.
 //  - LDS rows are 128 bytes (64 bf16 of K); 16-byte chunk c of row r sits
@@ -284,8 +290,9 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
 constexpr int kBig = 256;
 constexpr int kBigK = 64;
 constexpr int kBigTile = kBig * kBigK * 2;   // one operand tile of a stage, bytes (32 KiB)
-constexpr int kBigStage = 2 * kBigTile;      // A and B tiles of one stage
-constexpr int kBigLds = 2 * kBigStage;       // two stages, 128 KiB
+constexpr int kBigBRing = 3;                 // B stages (A has two)
+constexpr int kBigBBase = 2 * kBigTile;      // B ring after the two A stages
+constexpr int kBigLds = (2 + kBigBRing) * kBigTile;  // 160 KiB
 // Tile blocks within an XCD: 8 M-tiles x 4 N-tiles run concurrently and
 // share their A rows and B columns through that XCD's L2.
 constexpr int kGroupM = 8;
@@ -337,10 +344,6 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // Loads per thread per K-step: 16 (8 of A, 8 of B).  Load q of wave w fills
 // rows 8 b .. 8 b + 7 of operand q >> 3, b = (q & 7) * 4 + w.
-constexpr int kLoadsEarly = 8;  // loads of step it+2 issued after iteration it's barrier
-constexpr int kLoadsSub0 = 4;   // ... in sub-step 0 of iteration it+1
-constexpr int kLoadsSub1 = 4;   // ... in sub-step 1 of iteration it+1
-static_assert(kLoadsEarly + kLoadsSub0 + kLoadsSub1 == 16, "16 loads per K-step");
 
 template <int EPI>
 __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
@@ -384,10 +387,11 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
       static_cast<int>(lds0 + wave * 1024)));
   auto load = [&](int k, auto qc) {
     constexpr int q = decltype(qc)::value;
-    constexpr uint32_t qoff = static_cast<uint32_t>((q >> 3) * kBigTile + (q & 7) * 4096);
+    constexpr uint32_t qoff = static_cast<uint32_t>((q & 7) * 4096);
     const int kc = k < iters ? k : iters - 1;  // tail: a harmless re-load
+    const int stage_off = q < 8 ? (k & 1) * kBigTile : kBigBBase + (k % kBigBRing) * kBigTile;
     const uint32_t base = static_cast<uint32_t>(
-        __builtin_amdgcn_readfirstlane(static_cast<int>(m0_wave + (k & 1) * kBigStage)));
+        __builtin_amdgcn_readfirstlane(static_cast<int>(m0_wave + stage_off)));
     const uint32_t soff = static_cast<uint32_t>(
         __builtin_amdgcn_readfirstlane(kc * kBigK * 2 + (q & 7) * 64 * K));
     if constexpr (q < 8)
@@ -401,13 +405,15 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
   // 0-31 and 32-63).
   const int fsw = ((lane & 31) >> 1) & 7;
   const int a_frag = (wm * 128 + (lane & 31)) * 128;
-  const int b_frag = kBigTile + (wn * 128 + (lane & 31)) * 128;
+  const int b_frag = (wn * 128 + (lane & 31)) * 128;
   struct Frags { bf16x8_t a[4], b[4]; };
-  auto frag = [&](int stage, int kk, int idx) {
+  // step: the K-step whose stages are read (A stage step & 1, B stage step % 3).
+  auto frag = [&](int step, int kk, int idx) {
     const int c = ((2 * kk + (lane >> 5)) ^ fsw) << 4;
-    const char* base = smem + stage * kBigStage;
-    return idx < 4 ? *reinterpret_cast<const bf16x8_t*>(base + a_frag + idx * 4096 + c)
-                   : *reinterpret_cast<const bf16x8_t*>(base + b_frag + (idx - 4) * 4096 + c);
+    const char* abase = smem + (step & 1) * kBigTile;
+    const char* bbase = smem + kBigBBase + __builtin_amdgcn_readfirstlane(step % kBigBRing) * kBigTile;
+    return idx < 4 ? *reinterpret_cast<const bf16x8_t*>(abase + a_frag + idx * 4096 + c)
+                   : *reinterpret_cast<const bf16x8_t*>(bbase + b_frag + (idx - 4) * 4096 + c);
   };
   f32x16 acc[4][4];
 #pragma unroll
@@ -449,14 +455,17 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Prologue: step 0 whole and the first kLoadsEarly loads of step 1.
+  // Prologue: steps 0 and 1 whole (B before A in each step's issue order).
   [&]<int... Qs>(std::integer_sequence<int, Qs...>) {
     (load(0, std::integral_constant<int, Qs>{}), ...);
   }(std::make_integer_sequence<int, 16>{});
   [&]<int... Qs>(std::integer_sequence<int, Qs...>) {
+    (load(1, std::integral_constant<int, 8 + Qs>{}), ...);
+  }(std::make_integer_sequence<int, 8>{});
+  [&]<int... Qs>(std::integer_sequence<int, Qs...>) {
     (load(1, std::integral_constant<int, Qs>{}), ...);
-  }(std::make_integer_sequence<int, kLoadsEarly>{});
-  wait_vmcnt<kLoadsEarly>();  // own loads of step 0 landed
+  }(std::make_integer_sequence<int, 8>{});
+  wait_vmcnt<16>();  // own loads of step 0 landed
   lds_barrier();
   Frags f0, f1;
 #pragma unroll
@@ -467,19 +476,20 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     else
       f0.b[m - 4] = v;
   }
-  auto iteration = [&](int it, int cur) {
-    const int nxt = cur ^ 1;
-    sub_step.template operator()<kLoadsEarly, kLoadsSub0>(f0, f1, cur, 1, it + 1);
-    sub_step.template operator()<kLoadsEarly + kLoadsSub0, kLoadsSub1>(f1, f0, cur, 2, it + 1);
-    sub_step.template operator()<0, 0>(f0, f1, cur, 3, it + 1);
-    wait_vmcnt<0>();  // own loads of step it+1 landed
+  // Iteration it computes step it.  Sub-steps 0-2 issue B of step it+2 (its
+  // stage (it+2) % 3 was last read in step it-1, before the previous
+  // barrier); after this iteration's barrier, sub-step 3 issues A of step
+  // it+2 into A stage it & 1, whose reads all precede the barrier.  The wait
+  // before the barrier leaves B of step it+2 (8 loads) in flight.
+  auto iteration = [&](int it) {
+    sub_step.template operator()<8, 3>(f0, f1, it, 1, it + 2);
+    sub_step.template operator()<11, 3>(f1, f0, it, 2, it + 2);
+    sub_step.template operator()<14, 2>(f0, f1, it, 3, it + 2);
+    wait_vmcnt<8>();  // own loads of step it+1 landed
     lds_barrier();
-    sub_step.template operator()<0, kLoadsEarly>(f1, f0, nxt, 0, it + 2);
+    sub_step.template operator()<0, 8>(f1, f0, it + 1, 0, it + 2);
   };
-  for (int it = 0; it < iters; it += 2) {
-    iteration(it, 0);
-    iteration(it + 1, 1);
-  }
+  for (int it = 0; it < iters; ++it) iteration(it);
   wait_vmcnt<0>();  // the tail re-loads
 
   // R tile (256 x 256 bf16 = 128 KiB, the whole LDS) for the epilogues that
