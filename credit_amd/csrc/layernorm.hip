@@ -327,7 +327,8 @@ extern "C" int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamm
   CREDIT_TRY(current_device_props(&props));
   // AUTO: the pipeline once every CU has at least two rows to overlap.
   if (variant == CREDIT_VARIANT_AUTO && nvec > kPipeVec / 2 && nvec <= kPipeVec &&
-      rows >= 2 * static_cast<int64_t>(props->cu_count) && rows <= INT32_MAX) {
+      rows >= 2 * static_cast<int64_t>(props->cu_count) &&
+      rows <= INT32_MAX - 4 * static_cast<int64_t>(props->cu_count)) {  // row + 4G fits an int
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(layernorm_fwd_pipe_kernel<kPipeThreads, kPipeVpt>),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kPipeLds));
