@@ -10,18 +10,39 @@
 
 #include "api_internal.hpp"
 #include "common.hpp"
+#include "workspace_cache.hpp"
 
 namespace credit {
 
 namespace {
 thread_local char g_last_error[512] = "";
 
-struct Workspace {
-  char* ptr = nullptr;
-  size_t bytes = 0;
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t v, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// A new buffer for the cache: hipMalloc, then its header, counter and slot
+// areas zeroed by a fill kernel queued on the stream that will use it (a
+// kernel, not a memset node, so it stays correct inside a captured graph;
+// the allocation itself cannot be captured).
+struct DeviceAlloc {
+  int operator()(int device, void* stream, size_t bytes, char** out) const {
+    (void)device;
+    void* p = nullptr;
+    CREDIT_HIP(hipMalloc(&p, bytes));
+    const int64_t words = static_cast<int64_t>(kScratchOffset / 4);
+    fill_u32_kernel<<<dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256), 0,
+                      static_cast<hipStream_t>(stream)>>>(static_cast<uint32_t*>(p), 0u, words);
+    CREDIT_TRY(check_launch("fill_u32_kernel"));
+    *out = static_cast<char*>(p);
+    return CREDIT_OK;
+  }
 };
-std::mutex g_ws_mutex;
-std::vector<Workspace> g_ws;  // indexed by device
+WorkspaceCache<DeviceAlloc>& workspace_cache() {
+  static WorkspaceCache<DeviceAlloc>* cache = new WorkspaceCache<DeviceAlloc>();  // never freed
+  return *cache;
+}
 
 std::mutex g_props_mutex;
 std::vector<DeviceProps> g_props;
@@ -116,28 +137,7 @@ int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base) {
   }
   int dev = 0;
   CREDIT_HIP(hipGetDevice(&dev));
-  std::lock_guard<std::mutex> lock(g_ws_mutex);
-  if (static_cast<int>(g_ws.size()) <= dev) g_ws.resize(dev + 1);
-  Workspace& ws = g_ws[dev];
-  if (ws.bytes < need) {
-    if (ws.ptr != nullptr) {
-      // Earlier calls may still use the old buffer.
-      CREDIT_HIP(hipDeviceSynchronize());
-      CREDIT_HIP(hipFree(ws.ptr));
-      ws.ptr = nullptr;
-      ws.bytes = 0;
-    }
-    size_t grow = align_up(need < (size_t{1} << 20) ? (size_t{1} << 20) : need,
-                           size_t{1} << 20);
-    void* p = nullptr;
-    CREDIT_HIP(hipMalloc(&p, grow));
-    CREDIT_HIP(hipMemset(p, 0, grow));
-    CREDIT_HIP(hipDeviceSynchronize());
-    ws.ptr = static_cast<char*>(p);
-    ws.bytes = grow;
-  }
-  *base = ws.ptr;
-  return CREDIT_OK;
+  return workspace_cache().get(dev, cfg_stream(cfg), need, base);
 }
 
 __global__ void fill_f32_kernel(float* __restrict__ p, float v, int64_t n) {
@@ -154,8 +154,19 @@ uint32_t next_split_epoch(uint32_t stages) {
     const uint32_t end = base + stages;  // may wrap; [base, 2^32) ending at 0 is fine
     const bool wraps = base == 0 || (end < base && end != 0);
     const uint32_t start = wraps ? 1u : base;
-    if (next.compare_exchange_weak(base, start + stages, std::memory_order_relaxed))
+    if (next.compare_exchange_weak(base, start + stages, std::memory_order_relaxed)) {
+      if (wraps) {
+        // Tags restart at 1 after 2^32 - 1 stages: slots still holding tags
+        // from the previous cycle could match again, so the library's own
+        // workspaces return their slot areas to zero first.  (Caller
+        // workspaces are the caller's to re-zero; include/credit.h.)
+        if (hipDeviceSynchronize() == hipSuccess)
+          for (const WsBuffer& b : workspace_cache().live())
+            if (b.ptr != nullptr) (void)hipMemset(b.ptr + kSlotOffset, 0, kSlotAreaBytes);
+        (void)hipDeviceSynchronize();
+      }
       return start;
+    }
   }
 }
 
@@ -165,14 +176,18 @@ int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
     return set_error(CREDIT_ERR_UNSUPPORTED,
                      "split of %d members exchanges %d partials per stage (at most %d)", members,
                      members * k_values, kMaxExchangeValues);
-  const size_t slot_bytes =
-      align_up(split_slot_bytes(groups, members, k_values, ring), 256);
+  const size_t slot_bytes = split_slot_bytes(groups, members, k_values, ring);
+  if (slot_bytes > kSlotAreaBytes)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "split launch of %lld groups x %d members x %d values x ring %d needs %zu "
+                     "bytes of exchange slots (at most %zu)", static_cast<long long>(groups),
+                     members, k_values, ring, slot_bytes, kSlotAreaBytes);
   char* base = nullptr;
-  CREDIT_TRY(acquire_workspace(cfg, slot_bytes + extra_bytes, &base));
+  CREDIT_TRY(acquire_workspace(cfg, extra_bytes, &base));
   out->counters = ws_counters(base);
   out->watchdog = ws_watchdog(base);
-  out->slots = reinterpret_cast<uint64_t*>(ws_scratch(base));
-  out->extra = ws_scratch(base) + slot_bytes;
+  out->slots = ws_slots(base);
+  out->extra = ws_scratch(base);
   return CREDIT_OK;
 }
 
@@ -335,7 +350,14 @@ size_t credit_ffn_bwd_workspace_bytes(int64_t rows, int64_t d, int64_t f) {
 int credit_check_watchdog(const credit_cfg* cfg) {
   CREDIT_TRY(check_cfg(cfg));
   char* base = nullptr;
-  CREDIT_TRY(acquire_workspace(cfg, 0, &base));
+  if (cfg != nullptr && cfg->workspace != nullptr) {
+    CREDIT_TRY(acquire_workspace(cfg, 0, &base));
+  } else {
+    int dev = 0;
+    CREDIT_HIP(hipGetDevice(&dev));
+    base = workspace_cache().peek(dev, cfg_stream(cfg));
+    if (base == nullptr) return CREDIT_OK;  // no call on this stream used a workspace
+  }
   uint32_t flag = 0;
   CREDIT_HIP(hipStreamSynchronize(cfg_stream(cfg)));
   CREDIT_HIP(hipMemcpy(&flag, base, sizeof(flag), hipMemcpyDeviceToHost));

@@ -69,20 +69,31 @@ inline int cfg_split(const credit_cfg* cfg) { return cfg ? cfg->split : 0; }
 //                            kDispensers lines are the ticket dispensers of
 //                            split launches; group arrival counters follow
 //                            from slot kGroupCounterBase, one 64-byte line
-//                            each.  Only
-//                            the arrival protocols write here and each
-//                            returns its counters to zero, so the area
-//                            stays zero between calls whatever shapes the
-//                            calls have.
-//   [kScratchOffset, ...)    op-specific partials; always written before
-//                            they are read, so stale contents are harmless.
-// Uses the caller's buffer when cfg->workspace is set (at least
-// kScratchOffset + `bytes` long, 256-byte aligned, zero-filled before its
-// first use), otherwise a per-device buffer the library keeps for the life
-// of the process.
+//                            each.  Only the arrival protocols write here
+//                            and each returns its counters to zero, so the
+//                            area stays zero between calls whatever shapes
+//                            the calls have.
+//   [kSlotOffset, +4 MiB)    exchange slots of the tagged-slot split
+//                            protocol.  Only split launches write here, and
+//                            every slot carries the tag of the launch stage
+//                            that wrote it, so a later launch (new tags)
+//                            never takes an old value for its own.
+//   [kScratchOffset, ...)    op-specific scratch (dweight partials, FFN h,
+//                            row-sum partials): written before it is read
+//                            within one call, so its contents between calls
+//                            do not matter.
+// The first kScratchOffset bytes must read zero before the workspace's
+// first use; calls keep them that way (counters return to zero, slot tags
+// only grow).  Uses the caller's buffer when cfg->workspace is set, else the
+// library's buffer for (device, stream) (workspace_cache.hpp).
 constexpr size_t kWorkspaceHeader = 256;
 constexpr int kCounterSlots = 262144;
-constexpr size_t kScratchOffset = kWorkspaceHeader + size_t{4} * kCounterSlots;
+constexpr size_t kSlotOffset = kWorkspaceHeader + size_t{4} * kCounterSlots;
+// Tagged slots of one split launch: at most (resident workgroups) x ring x
+// values per member; 512 KiB at 256 CUs for the largest (softmax group
+// kernel, ring 16, two values), 4 MiB leaves room for larger devices.
+constexpr size_t kSlotAreaBytes = size_t{4} << 20;
+constexpr size_t kScratchOffset = kSlotOffset + kSlotAreaBytes;
 constexpr int kDispensers = 8;           // ticket dispensers, one per blockIdx % 8
 constexpr int kDispenserStride = 16;     // one 64-byte line each
 constexpr int kGroupCounterBase = kDispensers * kDispenserStride;  // first group counter
@@ -108,18 +119,20 @@ uint32_t next_split_epoch(uint32_t stages);
 int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base);
 
 // Workspace of a ticketed split launch: the counter area, the partial slots
-// of `groups` groups, then `extra_bytes` (256-byte aligned) for the
-// operation's own use.
+// of `groups` groups (in the slot area), then `extra_bytes` of scratch for
+// the operation's own use.
 struct SplitWorkspace {
   uint32_t* counters = nullptr;
   uint32_t* watchdog = nullptr;
   uint64_t* slots = nullptr;
   char* extra = nullptr;
 };
+// Scratch bytes (after kScratchOffset) of a split launch, never 0 so that
+// credit_workspace_bytes reports that the launch needs a workspace.
 inline size_t split_workspace_bytes(int64_t groups, int members, int k_values, int ring,
                                     size_t extra_bytes) {
-  const size_t slots = (split_slot_bytes(groups, members, k_values, ring) + 255) / 256 * 256;
-  return slots + extra_bytes;
+  (void)groups, (void)members, (void)k_values, (void)ring;
+  return (extra_bytes + 255) / 256 * 256 + 256;
 }
 int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
                             int k_values, int ring, size_t extra_bytes, SplitWorkspace* out);
@@ -148,6 +161,7 @@ inline uint32_t* ws_watchdog(char* base) { return reinterpret_cast<uint32_t*>(ba
 inline uint32_t* ws_counters(char* base) {
   return reinterpret_cast<uint32_t*>(base + kWorkspaceHeader);
 }
+inline uint64_t* ws_slots(char* base) { return reinterpret_cast<uint64_t*>(base + kSlotOffset); }
 inline char* ws_scratch(char* base) { return base + kScratchOffset; }
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }

@@ -43,6 +43,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ uint16_t f32_to_bf16(float v) {
   return static_cast<uint16_t>(pack_bf16x2(v, 0.0f) & 0xffffu);
 }
+// a.lo * b.lo + a.hi * b.hi + c on two packed bf16 pairs (v_dot2_f32_bf16):
+// the bf16 products are exact in fp32.  With b = (1, 1) it sums a pair, with
+// b = a it sums a pair's squares, one instruction per two elements.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
 
 // ---------------------------------------------------------- max with NaN --
 // torch.amax propagates NaN.  v_maximum3_f32 (IEEE 754-2019 maximum) does the

@@ -13,6 +13,8 @@
 // report a timeout instead of hanging.
 #include <string.h>
 
+#include <algorithm>
+#include <chrono>
 #include <vector>
 
 #include "api_internal.hpp"
@@ -22,71 +24,101 @@ namespace credit {
 namespace {
 
 // --------------------------------------------------------- HBM streams ---
-template <int UNROLL>
-__global__ __launch_bounds__(256) void mb_read_kernel(const f32x4* __restrict__ src,
-                                                      int64_t n4, float* __restrict__ sink) {
-  float acc = 0.0f;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-  int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  for (; i + (UNROLL - 1) * stride < n4; i += UNROLL * stride) {
-    f32x4 v[UNROLL];
+// R source and W destination streams of equal length: a read:write byte mix
+// of R:W.  Every workgroup of T lanes moves chunks of T*U 16-byte vectors
+// per stream (each lane U vectors per stream), chunk c = blockIdx.x + k*grid:
+// the whole grid advances through the streams as one narrow front, which is
+// the access order the settled measurements found fastest (one large
+// contiguous region per workgroup ran 10% slower at 1:1).  Loads are
+// nontemporal; stores nontemporal (SP = kBufferNt) or plain (SP = 0).  The
+// destination value depends on every source vector, so no load is dead.
+struct StreamArgs {
+  const void* src[4];
+  void* dst[2];
+  uint32_t bytes;  // per stream, a multiple of T * U * 16
+};
+
+template <int R, int W, int U, int SP>
+__global__ __launch_bounds__(512) void mb_stream_kernel(StreamArgs a, uint32_t* sink) {
+  const uint32_t lanes = blockDim.x;
+  const uint32_t chunk = lanes * U * 16u;
+  const uint32_t nchunks = a.bytes / chunk;
+  buffer_rsrc_t rs[R > 0 ? R : 1];
+  buffer_rsrc_t ws[W > 0 ? W : 1];
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) v[u] = load_nt(src + i + u * stride);
+  for (int i = 0; i < R; ++i) rs[i] = make_rsrc(a.src[i], a.bytes);
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+  for (int i = 0; i < W; ++i) ws[i] = make_rsrc(a.dst[i], a.bytes);
+  u32x4 acc = {0, 0, 0, 0};
+  for (uint32_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const uint32_t base = c * chunk + threadIdx.x * 16u;
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = u32x4{c, c, c, c};
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        v[u] += __builtin_amdgcn_raw_buffer_load_b128(rs[i], base + u * lanes * 16u, 0, kBufferNt);
+#pragma unroll
+    for (int i = 0; i < W; ++i)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        __builtin_amdgcn_raw_buffer_store_b128(v[u] + static_cast<uint32_t>(i), ws[i],
+                                               base + u * lanes * 16u, 0, SP);
+    if (W == 0)
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= v[u];
   }
-  for (; i < n4; i += stride) {
-    const f32x4 v = load_nt(src + i);
-    acc += (v.x + v.y) + (v.z + v.w);
-  }
-  if (acc == 1.2345e-30f) sink[0] = acc;  // keeps the loads alive
+  // Read-only streams: a data-dependent store that never fires keeps the
+  // loads alive.
+  if (W == 0 && acc.x == 0x9e3779b9u && acc.y == 0x7f4a7c15u) sink[0] = acc.z;
 }
 
-__global__ __launch_bounds__(256) void mb_write_kernel(f32x4* __restrict__ dst, int64_t n4) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-  const f32x4 v = {1.0f, 2.0f, 3.0f, 4.0f};
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n4; i += stride)
-    store_nt(dst + i, v);
+using StreamFn = void (*)(StreamArgs, uint32_t*);
+
+template <int R, int W, int U>
+StreamFn stream_fn(bool nt_store) {
+  return nt_store ? mb_stream_kernel<R, W, U, kBufferNt> : mb_stream_kernel<R, W, U, 0>;
 }
 
-template <int UNROLL, bool NT_STORE>
-__global__ __launch_bounds__(256) void mb_copy_kernel(const f32x4* __restrict__ src,
-                                                      f32x4* __restrict__ dst, int64_t n4) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-  int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  for (; i + (UNROLL - 1) * stride < n4; i += UNROLL * stride) {
-    f32x4 v[UNROLL];
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) v[u] = load_nt(src + i + u * stride);
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      if (NT_STORE)
-        store_nt(dst + i + u * stride, v[u]);
-      else
-        dst[i + u * stride] = v[u];
-    }
-  }
-  for (; i < n4; i += stride) {
-    if (NT_STORE)
-      store_nt(dst + i, load_nt(src + i));
-    else
-      dst[i] = load_nt(src + i);
+template <int R, int W>
+StreamFn stream_fn_u(int u, bool nt_store) {
+  switch (u) {
+    case 1: return stream_fn<R, W, 1>(nt_store);
+    case 2: return stream_fn<R, W, 2>(nt_store);
+    case 4: return stream_fn<R, W, 4>(nt_store);
+    default: return stream_fn<R, W, 8>(nt_store);
   }
 }
 
-// One contiguous chunk per workgroup (the access shape of the row kernels:
-// a workgroup owns a row, reads it whole, then writes it whole).
-template <int VPT>
-__global__ __launch_bounds__(256) void mb_copy_rows_kernel(const f32x4* __restrict__ src,
-                                                           f32x4* __restrict__ dst) {
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * VPT;
-  f32x4 v[VPT];
-#pragma unroll
-  for (int k = 0; k < VPT; ++k) v[k] = load_nt(src + base + k * 256 + threadIdx.x);
-#pragma unroll
-  for (int k = 0; k < VPT; ++k) store_nt(dst + base + k * 256 + threadIdx.x, v[k]);
+StreamFn stream_kernel_for(int reads, int writes, int u, bool nt_store) {
+  const int mix = reads * 10 + writes;
+  switch (mix) {
+    case 10: return stream_fn_u<1, 0>(u, nt_store);
+    case 1: return stream_fn_u<0, 1>(u, nt_store);
+    case 11: return stream_fn_u<1, 1>(u, nt_store);
+    case 21: return stream_fn_u<2, 1>(u, nt_store);
+    case 31: return stream_fn_u<3, 1>(u, nt_store);
+    case 41: return stream_fn_u<4, 1>(u, nt_store);
+    case 32: return stream_fn_u<3, 2>(u, nt_store);
+    case 22: return stream_fn_u<2, 2>(u, nt_store);
+    case 12: return stream_fn_u<1, 2>(u, nt_store);
+    default: return nullptr;
+  }
 }
 
+// Launch shapes tried per mix: lanes per workgroup, vectors per lane and
+// stream, workgroups per CU.  Each stays under 48 KiB of loads in flight
+// per CU; the settled sweep over 64..1024 lanes, 1..16 vectors and 1..8
+// workgroups per CU put every mix's best among these.
+struct StreamShape {
+  int lanes, u, per_cu;
+};
+constexpr StreamShape kStreamShapes[] = {
+    {64, 4, 4}, {128, 2, 4}, {256, 4, 1}, {256, 2, 1}, {512, 1, 2}, {512, 2, 1}, {256, 8, 1},
+};
+constexpr int kStreamShapeCount = sizeof(kStreamShapes) / sizeof(kStreamShapes[0]);
 // ------------------------------------------------------------- latency ---
 // Single-lane pointer chase; the chain is laid out with a fixed stride so a
 // working set of `bytes` is walked.  Cycles come from s_memtime.
@@ -195,6 +227,80 @@ __global__ __launch_bounds__(256) void mb_plain_kernel(int* sink) {
   if (threadIdx.x == 0 && blockIdx.x == 0x7fffffff) sink[0] = 1;
 }
 
+// ------------------------------------------------- L1 / L2 bandwidth (H2) -
+// Every workgroup reads a `bytes`-long buffer `passes` times with plain
+// dwordx4 loads, starting at a rotated offset so concurrent workgroups hit
+// different channels.  Sized to fit the CU's vector L1 (16 KiB, one
+// workgroup per CU) the loads hit L1; sized far above L1 and below one XCD's
+// 4 MiB L2 (2 MiB) they miss L1 and hit L2.  Thread 0 records s_memtime
+// cycles around the passes.
+template <int U>
+__global__ __launch_bounds__(1024) void mb_cache_read_kernel(const u32x4* __restrict__ buf,
+                                                             uint32_t nvec, int passes,
+                                                             uint32_t* sink, uint64_t* cycles) {
+  const uint32_t lanes = blockDim.x;
+  const uint32_t rot = (blockIdx.x * 2048u) % nvec;
+  u32x4 acc = {0, 0, 0, 0};
+  __syncthreads();
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  for (int p = 0; p < passes; ++p) {
+    // An index the compiler cannot prove the same every pass: no load is
+    // hoisted out of the pass loop.
+    uint32_t first = threadIdx.x;
+    __asm__ volatile("" : "+v"(first));
+    for (uint32_t i = first; i < nvec; i += lanes * U) {
+      u32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        uint32_t j = i + u * lanes + rot;
+        j = j >= nvec ? j - nvec : j;
+        v[u] = buf[j];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= v[u];
+    }
+  }
+  __syncthreads();
+  const uint64_t t1 = __builtin_amdgcn_s_memtime();
+  if (threadIdx.x == 0) cycles[blockIdx.x] = t1 - t0;
+  if (acc.x == 0x9e3779b9u && acc.w == 0x7f4a7c15u) sink[0] = acc.y;
+}
+
+// ----------------------------------------- exchange slot throughput (H3) --
+// One workgroup per CU; its first wave stores 64 tagged 64-bit slots per
+// round to its own 512-byte row with device-scope atomic stores (the
+// publish of the split kernels, all lanes at once), `rounds` rounds, then
+// waits for every store to be acknowledged.  s_memtime cycles of wave 0.
+__global__ __launch_bounds__(64) void mb_slot_store_kernel(uint64_t* slots, int rounds,
+                                                           uint64_t* cycles) {
+  uint64_t* row = slots + static_cast<size_t>(blockIdx.x) * kWave;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  for (int r = 0; r < rounds; ++r)
+    __hip_atomic_store(row + threadIdx.x,
+                       (static_cast<uint64_t>(r + 1) << 32) | threadIdx.x, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  publish_wait();
+  const uint64_t t1 = __builtin_amdgcn_s_memtime();
+  if (threadIdx.x == 0) cycles[blockIdx.x] = t1 - t0;
+}
+
+// Ticket draws: lane 0 of every workgroup takes `draws` tickets one after
+// another (each waits for the returned value, as split_join does) from its
+// own 64-byte line (shared == 0) or from one line every workgroup uses.
+__global__ __launch_bounds__(64) void mb_ticket_kernel(uint32_t* lines, int draws, int shared,
+                                                       uint64_t* cycles) {
+  if (threadIdx.x != 0) return;
+  uint32_t* line = lines + (shared ? 0 : (static_cast<size_t>(blockIdx.x) + 1) * 16);
+  uint32_t t = 0;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  // Each draw's operand depends on the previous ticket (the sum stays far
+  // below 2^31, so the increment is always 1).
+  for (int d = 0; d < draws; ++d)
+    t += __hip_atomic_fetch_add(line, 1u + (t >> 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t t1 = __builtin_amdgcn_s_memtime();
+  cycles[blockIdx.x] = t1 - t0 + (t >> 31);
+}
+
 struct Events {
   hipEvent_t a = nullptr, b = nullptr;
   ~Events() {
@@ -231,75 +337,116 @@ struct DevBuf {
   }
 };
 
-int bench_stream(int which, int64_t bytes, int iters, double* results, int n) {
-  if (bytes < (int64_t{1} << 20)) bytes = int64_t{1} << 30;
+// Settle the HBM clocks with `settle_ms` of back-to-back launches
+// (synchronised every 8), then `trials` timed blocks of `iters` launches;
+// *median_ms = the median block's time per launch.  After an idle period
+// the first 10-20 ms of HBM traffic on the MI355X run slow.
+template <class F>
+int settled_median_ms(F&& launch, double settle_ms, int trials, int iters, double* median_ms) {
+  int i = 0;
+  const auto t_end = std::chrono::steady_clock::now() +
+                     std::chrono::microseconds(static_cast<int64_t>(settle_ms * 1e3));
+  while (std::chrono::steady_clock::now() < t_end) {
+    for (int k = 0; k < 8; ++k) CREDIT_TRY(launch(i++));
+    CREDIT_HIP(hipDeviceSynchronize());
+  }
+  Events ev;
+  CREDIT_HIP(hipEventCreate(&ev.a));
+  CREDIT_HIP(hipEventCreate(&ev.b));
+  std::vector<double> per_call;
+  for (int t = 0; t < trials; ++t) {
+    CREDIT_HIP(hipEventRecord(ev.a, nullptr));
+    for (int k = 0; k < iters; ++k) CREDIT_TRY(launch(i++));
+    CREDIT_HIP(hipEventRecord(ev.b, nullptr));
+    CREDIT_HIP(hipEventSynchronize(ev.b));
+    float ms = 0.0f;
+    CREDIT_HIP(hipEventElapsedTime(&ms, ev.a, ev.b));
+    per_call.push_back(static_cast<double>(ms) / iters);
+  }
+  std::sort(per_call.begin(), per_call.end());
+  *median_ms = per_call[per_call.size() / 2];
+  return CREDIT_OK;
+}
+
+}  // namespace
+
+// The stream ceiling of a read:write mix: every shape of kStreamShapes with
+// nontemporal and with plain stores over three rotating buffer sets.
+// results: [0] best GB/s (bytes moved / median time per call), [1] its
+// median ms per call, [2] lanes, [3] vectors per lane, [4] workgroups per
+// CU, [5] 1 for nontemporal stores, [6] bytes moved per call, then GB/s of
+// each (shape, store policy) in table order, nontemporal first.
+int stream_ceiling(int reads, int writes, int64_t call_bytes, int trials, int iters,
+                   double settle_ms, double* results, int n) {
+  if (reads < 0 || writes < 0 || reads > 4 || writes > 2 || reads + writes == 0 ||
+      stream_kernel_for(reads, writes, 1, true) == nullptr)
+    return set_error(CREDIT_ERR_BAD_CONFIG,
+                     "stream mix %d:%d not built (reads 0..4, writes 0..2: 1:0 0:1 1:1 2:1 "
+                     "3:1 4:1 3:2 2:2 1:2)", reads, writes);
+  if (trials < 1 || iters < 1) return set_error(CREDIT_ERR_BAD_CONFIG, "trials, iters >= 1");
+  const int streams = reads + writes;
+  constexpr int64_t kGranule = int64_t{512} * 8 * 16;  // the largest chunk, 64 KiB
+  const int64_t per = call_bytes / streams / kGranule * kGranule;
+  if (per < kGranule || per > (int64_t{1} << 32) - kGranule)
+    return set_error(CREDIT_ERR_BAD_CONFIG,
+                     "%lld bytes per call over %d streams: each stream must hold 64 KiB to 4 GiB",
+                     static_cast<long long>(call_bytes), streams);
   const DeviceProps* props = nullptr;
   CREDIT_TRY(current_device_props(&props));
-  // Three source/destination pairs rotate so the 256 MB MALL cannot serve a
-  // repeated working set.
-  DevBuf src[3], dst[3], sink;
-  for (int k = 0; k < 3; ++k) {
-    CREDIT_TRY(src[k].alloc(bytes));
-    if (which != CREDIT_MB_HBM_READ) CREDIT_TRY(dst[k].alloc(bytes));
-  }
+  constexpr int kSets = 3;
+  std::vector<DevBuf> bufs(static_cast<size_t>(kSets) * streams);
+  for (DevBuf& b : bufs) CREDIT_TRY(b.alloc(static_cast<size_t>(per)));
+  DevBuf sink;
   CREDIT_TRY(sink.alloc(256));
-  const int64_t n4 = bytes / 16;
-  const int grids[] = {props->cu_count * 4, props->cu_count * 8, props->cu_count * 16,
-                       props->cu_count * 32};
+  StreamArgs sets[kSets];
+  for (int k = 0; k < kSets; ++k) {
+    sets[k] = StreamArgs{};
+    sets[k].bytes = static_cast<uint32_t>(per);
+    for (int i = 0; i < reads; ++i) sets[k].src[i] = bufs[k * streams + i].p;
+    for (int i = 0; i < writes; ++i) sets[k].dst[i] = bufs[k * streams + reads + i].p;
+  }
+  const double moved = static_cast<double>(per) * streams;
   double best = 0.0;
-  int slot = 0;
-  for (int gi = 0; gi < 4; ++gi) {
-    const int grid = grids[gi];
-    for (int variant = 0; variant < 3; ++variant) {
-      double ms = 0.0;
+  int slot = 7;
+  for (int i = 0; i < 7 && i < n; ++i) results[i] = 0.0;
+  for (int nt = 1; nt >= 0; --nt) {
+    if (writes == 0 && nt == 0) break;  // no stores to vary
+    for (const StreamShape& sh : kStreamShapes) {
+      const StreamFn fn = stream_kernel_for(reads, writes, sh.u, nt != 0);
+      const unsigned grid = static_cast<unsigned>(props->cu_count * sh.per_cu);
       auto launch = [&](int i) -> int {
-        const f32x4* s = static_cast<const f32x4*>(src[i % 3].p);
-        f32x4* d = static_cast<f32x4*>(dst[i % 3].p);
-        if (which == CREDIT_MB_HBM_READ) {
-          if (variant == 0) mb_read_kernel<4><<<grid, 256>>>(s, n4, static_cast<float*>(sink.p));
-          else if (variant == 1) mb_read_kernel<8><<<grid, 256>>>(s, n4, static_cast<float*>(sink.p));
-          else mb_read_kernel<16><<<grid, 256>>>(s, n4, static_cast<float*>(sink.p));
-        } else if (which == CREDIT_MB_HBM_WRITE) {
-          mb_write_kernel<<<grid, 256>>>(d, n4);
-        } else {
-          if (variant == 0) mb_copy_kernel<4, true><<<grid, 256>>>(s, d, n4);
-          else if (variant == 1) mb_copy_kernel<8, true><<<grid, 256>>>(s, d, n4);
-          else mb_copy_kernel<8, false><<<grid, 256>>>(s, d, n4);
-        }
-        return check_launch("microbench stream");
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(sh.lanes), 0, nullptr, sets[i % kSets],
+                           static_cast<uint32_t*>(sink.p));
+        return check_launch("mb_stream_kernel");
       };
-      CREDIT_TRY(time_ms(launch, 3, iters, &ms));
-      const double moved = (which == CREDIT_MB_HBM_COPY ? 2.0 : 1.0) * static_cast<double>(bytes);
+      double ms = 0.0;
+      CREDIT_TRY(settled_median_ms(launch, settle_ms, trials, iters, &ms));
       const double gbps = moved / (ms * 1e-3) / 1e9;
-      if (slot + 1 < n) results[1 + slot] = gbps;
+      if (slot < n) results[slot] = gbps;
       ++slot;
-      if (gbps > best) best = gbps;
-      if (which == CREDIT_MB_HBM_WRITE) break;
+      if (gbps > best) {
+        best = gbps;
+        const double rec[7] = {gbps, ms, static_cast<double>(sh.lanes), static_cast<double>(sh.u),
+                               static_cast<double>(sh.per_cu), static_cast<double>(nt), moved};
+        for (int i = 0; i < 7 && i < n; ++i) results[i] = rec[i];
+      }
     }
   }
-  // Row-shaped copy: workgroups own contiguous 16*VPT KiB chunks.
-  if (which == CREDIT_MB_HBM_COPY) {
-    const int vpts[] = {4, 8, 16};
-    for (int vi = 0; vi < 3; ++vi) {
-      const int vpt = vpts[vi];
-      const int64_t grid = n4 / (256 * vpt);
-      double ms = 0.0;
-      auto launch = [&](int i) -> int {
-        const f32x4* s = static_cast<const f32x4*>(src[i % 3].p);
-        f32x4* d = static_cast<f32x4*>(dst[i % 3].p);
-        if (vpt == 4) mb_copy_rows_kernel<4><<<static_cast<unsigned>(grid), 256>>>(s, d);
-        else if (vpt == 8) mb_copy_rows_kernel<8><<<static_cast<unsigned>(grid), 256>>>(s, d);
-        else mb_copy_rows_kernel<16><<<static_cast<unsigned>(grid), 256>>>(s, d);
-        return check_launch("microbench copy rows");
-      };
-      CREDIT_TRY(time_ms(launch, 3, iters, &ms));
-      const double gbps = 2.0 * static_cast<double>(grid * 256 * vpt * 16) / (ms * 1e-3) / 1e9;
-      if (slot + 1 < n) results[1 + slot] = gbps;
-      ++slot;
-      if (gbps > best) best = gbps;
-    }
-  }
-  results[0] = best;
+  return CREDIT_OK;
+}
+
+namespace {
+
+int bench_stream(int which, int64_t bytes, int iters, double* results, int n) {
+  if (bytes < (int64_t{1} << 20)) bytes = int64_t{1} << 30;
+  const int reads = which == CREDIT_MB_HBM_WRITE ? 0 : 1;
+  const int writes = which == CREDIT_MB_HBM_READ ? 0 : 1;
+  // results[0] = best GB/s, then the per-shape figures of stream_ceiling.
+  std::vector<double> r(7 + 2 * kStreamShapeCount, 0.0);
+  CREDIT_TRY(stream_ceiling(reads, writes, bytes * (reads + writes), 5, iters, 20.0, r.data(),
+                            static_cast<int>(r.size())));
+  results[0] = r[0];
+  for (int i = 0; i + 1 < n && 7 + i < static_cast<int>(r.size()); ++i) results[1 + i] = r[7 + i];
   return CREDIT_OK;
 }
 
@@ -367,6 +514,96 @@ int bench_lds(bool write, int iters, double* results, int n) {
   return CREDIT_OK;
 }
 
+uint64_t max_of(const std::vector<uint64_t>& v) {
+  uint64_t worst = 1;
+  for (uint64_t c : v) worst = c > worst ? c : worst;
+  return worst;
+}
+
+// [0] B/cycle per CU from its vector L1: one 1024-lane workgroup per CU
+// (its 96 KiB LDS allocation keeps a second one off the CU) re-reading
+// 16 KiB, s_memtime cycles of the slowest.  [1] B/cycle per XCD from L2:
+// two 1024-lane workgroups per CU re-reading a 2 MiB buffer, timed with
+// events over the launch and converted at the measured shader clock; [2]
+// that L2 rate as device GB/s.
+int bench_cache(int passes, double* results, int n) {
+  const DeviceProps* props = nullptr;
+  CREDIT_TRY(current_device_props(&props));
+  if (passes <= 0) passes = 64;
+  DevBuf buf, sink, cyc;
+  CREDIT_TRY(buf.alloc(size_t{2} << 20));
+  CREDIT_TRY(sink.alloc(256));
+  CREDIT_TRY(cyc.alloc(sizeof(uint64_t) * props->cu_count * 2));
+  std::vector<uint64_t> h(props->cu_count);
+  const u32x4* b = static_cast<const u32x4*>(buf.p);
+  constexpr size_t kHoldCu = size_t{96} << 10;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(mb_cache_read_kernel<1>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHoldCu));
+  if (attr != hipSuccess) return hip_failure(attr, "hipFuncSetAttribute(mb_cache_read_kernel)");
+  // L1: 16 KiB = 1024 vectors, one vector per lane per pass.
+  mb_cache_read_kernel<1><<<props->cu_count, 1024, kHoldCu>>>(
+      b, 1024u, passes * 16, static_cast<uint32_t*>(sink.p), static_cast<uint64_t*>(cyc.p));
+  CREDIT_TRY(check_launch("mb_cache_read_kernel"));
+  CREDIT_HIP(hipMemcpy(h.data(), cyc.p, sizeof(uint64_t) * props->cu_count,
+                       hipMemcpyDeviceToHost));
+  results[0] = 16384.0 * passes * 16 / static_cast<double>(max_of(h));
+  // L2: 2 MiB = 131072 vectors per workgroup pass.
+  const int grid = props->cu_count * 2;
+  const int l2_passes = passes / 4 > 0 ? passes / 4 : 1;
+  auto launch = [&](int) -> int {
+    mb_cache_read_kernel<4><<<grid, 1024>>>(b, 131072u, l2_passes,
+                                            static_cast<uint32_t*>(sink.p),
+                                            static_cast<uint64_t*>(cyc.p));
+    return check_launch("mb_cache_read_kernel");
+  };
+  double ms = 0.0;
+  CREDIT_TRY(time_ms(launch, 2, 5, &ms));
+  const double bytes = (double{2} * (1 << 20)) * l2_passes * grid;
+  const double gbps = bytes / (ms * 1e-3) / 1e9;
+  double clk[1] = {0.0};
+  CREDIT_TRY(bench_clock(clk, 1));
+  if (n > 1) results[1] = gbps * 1e9 / (clk[0] * 1e6) / props->xcd_count;
+  if (n > 2) results[2] = gbps;
+  return CREDIT_OK;
+}
+
+// [0] bytes per cycle per workgroup of device-scope slot stores with one
+// workgroup per CU, [1] the same stores as GB/s over the device, [2] cycles
+// per ticket draw on a workgroup's own line, [3] cycles per draw when one
+// workgroup per CU draws from one shared line.
+int bench_exchange_throughput(int rounds, double* results, int n) {
+  const DeviceProps* props = nullptr;
+  CREDIT_TRY(current_device_props(&props));
+  if (rounds <= 0) rounds = 4096;
+  const int grid = props->cu_count;
+  DevBuf slots, lines, cyc;
+  CREDIT_TRY(slots.alloc(sizeof(uint64_t) * kWave * grid));
+  CREDIT_TRY(lines.alloc(size_t{64} * (grid + 1)));
+  CREDIT_TRY(cyc.alloc(sizeof(uint64_t) * grid));
+  std::vector<uint64_t> h(grid);
+  mb_slot_store_kernel<<<grid, 64>>>(static_cast<uint64_t*>(slots.p), rounds,
+                                     static_cast<uint64_t*>(cyc.p));
+  CREDIT_TRY(check_launch("mb_slot_store_kernel"));
+  CREDIT_HIP(hipMemcpy(h.data(), cyc.p, sizeof(uint64_t) * grid, hipMemcpyDeviceToHost));
+  const double store_cycles = static_cast<double>(max_of(h));
+  const double per_wg = 8.0 * kWave * rounds;
+  results[0] = per_wg / store_cycles;
+  double clk[1] = {0.0};
+  CREDIT_TRY(bench_clock(clk, 1));
+  if (n > 1) results[1] = per_wg * grid / (store_cycles / (clk[0] * 1e6)) / 1e9;
+  const int draws = rounds / 4 > 0 ? rounds / 4 : 1;
+  for (int shared = 0; shared <= 1; ++shared) {
+    CREDIT_HIP(hipMemset(lines.p, 0, size_t{64} * (grid + 1)));
+    mb_ticket_kernel<<<grid, 64>>>(static_cast<uint32_t*>(lines.p), draws, shared,
+                                   static_cast<uint64_t*>(cyc.p));
+    CREDIT_TRY(check_launch("mb_ticket_kernel"));
+    CREDIT_HIP(hipMemcpy(h.data(), cyc.p, sizeof(uint64_t) * grid, hipMemcpyDeviceToHost));
+    if (n > 2 + shared) results[2 + shared] = static_cast<double>(max_of(h)) / draws;
+  }
+  return CREDIT_OK;
+}
+
 int bench_pingpong(int rounds, double* results, int n) {
   if (rounds <= 0) rounds = 2000;
   DevBuf flag, out, tmo;
@@ -404,12 +641,14 @@ int control_overhead(int64_t rows, int split, int barriers, int warmup, int iter
   if (groups > padded_groups(rows)) groups = padded_groups(rows);
   const int64_t per_group = (rows + groups - 1) / groups;
   DevBuf ws, sink;
-  CREDIT_TRY(ws.alloc(kScratchOffset + split_slot_bytes(groups, split, 1, kSplitRing)));
+  if (split_slot_bytes(groups, split, 1, kSplitRing) > kSlotAreaBytes)
+    return set_error(CREDIT_ERR_UNSUPPORTED, "barrier benchmark slots exceed the slot area");
+  CREDIT_TRY(ws.alloc(kScratchOffset));
   CREDIT_TRY(sink.alloc(256));
   char* base = static_cast<char*>(ws.p);
   uint32_t* counters = ws_counters(base);
   uint32_t* watchdog = ws_watchdog(base);
-  uint64_t* slots = reinterpret_cast<uint64_t*>(ws_scratch(base));
+  uint64_t* slots = ws_slots(base);
   double* sinkp = static_cast<double*>(sink.p);
   const unsigned grid = static_cast<unsigned>(groups * split);
   // The plain reference launches one workgroup per (row, member): the work
@@ -467,9 +706,24 @@ extern "C" int credit_microbench(int32_t which, int64_t bytes, int32_t iters, do
       return bench_lds(true, iters, results, n_results);
     case CREDIT_MB_EXCHANGE_ROUNDTRIP:
       return bench_pingpong(iters, results, n_results);
+    case CREDIT_MB_CACHE_READ:
+      return bench_cache(iters, results, n_results);
+    case CREDIT_MB_EXCHANGE_THROUGHPUT:
+      return bench_exchange_throughput(iters, results, n_results);
     default:
       return set_error(CREDIT_ERR_BAD_CONFIG, "unknown microbenchmark %d", which);
   }
+}
+
+extern "C" int credit_stream_ceiling(int32_t reads, int32_t writes, int64_t call_bytes,
+                                     int32_t trials, int32_t iters, double settle_ms,
+                                     double* results, int32_t n_results) {
+  CREDIT_TRY(check_ptr(results, "results"));
+  if (n_results < 1) return set_error(CREDIT_ERR_BAD_CONFIG, "n_results must be >= 1");
+  if (!(settle_ms >= 0.0) || settle_ms > 10000.0)
+    return set_error(CREDIT_ERR_BAD_CONFIG, "settle_ms must lie in [0, 10000]");
+  for (int i = 0; i < n_results; ++i) results[i] = 0.0;
+  return stream_ceiling(reads, writes, call_bytes, trials, iters, settle_ms, results, n_results);
 }
 
 extern "C" int credit_control_overhead(int64_t rows, int32_t split, int32_t barriers,

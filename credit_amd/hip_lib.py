@@ -132,6 +132,8 @@ SIGNATURES: dict[str, list] = {
     "credit_transpose_bf16": [_P, _P, _I64, _I64, _CFG],
     "credit_microbench": [ctypes.c_int32, _I64, ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
                           ctypes.c_int32],
+    "credit_stream_ceiling": [ctypes.c_int32, ctypes.c_int32, _I64, ctypes.c_int32, ctypes.c_int32,
+                              ctypes.c_double, ctypes.POINTER(ctypes.c_double), ctypes.c_int32],
     "credit_control_overhead": [_I64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                 ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
                                 ctypes.POINTER(ctypes.c_double)],
@@ -253,6 +255,8 @@ MICROBENCH = {
     "lds_read": 6,
     "lds_write": 7,
     "exchange_roundtrip": 8,
+    "cache_read": 9,
+    "exchange_throughput": 10,
 }
 
 
@@ -262,6 +266,21 @@ def microbench(name: str, nbytes: int = 0, iters: int = 0, n_results: int = 16) 
     check(load_library().credit_microbench(MICROBENCH[name], nbytes, iters, out, n_results),
           "credit_microbench")
     return list(out)
+
+
+def stream_ceiling(reads: int, writes: int, call_bytes: int, trials: int = 5, iters: int = 20,
+                   settle_ms: float = 20.0) -> dict:
+    """Settled HBM stream ceiling of a reads:writes byte mix at call_bytes
+    per call (credit_stream_ceiling): the best GB/s over the library's
+    stream-kernel shapes and the shape that reached it."""
+    out = (ctypes.c_double * 32)()
+    check(load_library().credit_stream_ceiling(reads, writes, int(call_bytes), trials, iters,
+                                               float(settle_ms), out, 32),
+          "credit_stream_ceiling")
+    return {"mix": f"{reads}:{writes}", "GBps": round(out[0], 1), "ms": out[1],
+            "shape": {"lanes": int(out[2]), "vectors_per_lane": int(out[3]),
+                      "workgroups_per_cu": int(out[4]), "nontemporal_stores": bool(out[5])},
+            "bytes": int(out[6])}
 
 
 def control_overhead(rows: int, split: int, barriers: int, warmup: int = 3, iters: int = 20,

@@ -46,10 +46,17 @@ TEXT_KEYS: tuple[tuple[str, str, str], ...] = (
     ("hbm_read_gbps", "HBM read bandwidth", "GB/s"),
     ("hbm_write_gbps", "HBM write bandwidth", "GB/s"),
     ("hbm_copy_gbps", "HBM copy bandwidth", "GB/s"),
+    ("l1_read_bytes_per_cycle_cu", "L1 read bandwidth", "B/cycle/CU"),
+    ("l2_read_bytes_per_cycle_xcd", "L2 read bandwidth", "B/cycle/XCD"),
+    ("l2_read_gbps", "L2 read bandwidth (device)", "GB/s"),
     ("lds_read_bytes_per_cycle_cu", "LDS read throughput", "B/cycle/CU"),
     ("lds_write_bytes_per_cycle_cu", "LDS write throughput", "B/cycle/CU"),
     ("exchange_roundtrip_cycles_xcd", "Exchange round trip same XCD", "cycles"),
     ("exchange_roundtrip_cycles_cross", "Exchange round trip cross XCD", "cycles"),
+    ("slot_store_bytes_per_cycle_wg", "Exchange slot store throughput", "B/cycle/WG"),
+    ("slot_store_gbps", "Exchange slot store throughput (device)", "GB/s"),
+    ("ticket_cycles_private", "Ticket draw private line", "cycles"),
+    ("ticket_cycles_shared", "Ticket draw shared line", "cycles"),
 )
 
 
@@ -64,6 +71,8 @@ def run_microbenchmarks(hbm_bytes: int = 1 << 30, iters: int = 20) -> dict[str, 
     lds_r = hip_lib.microbench("lds_read", 0, 4096)[0]
     lds_w = hip_lib.microbench("lds_write", 0, 4096)[0]
     rt = hip_lib.microbench("exchange_roundtrip", 0, 2000, 2)
+    cache = hip_lib.microbench("cache_read", 0, 64, 3)
+    xput = hip_lib.microbench("exchange_throughput", 0, 4096, 4)
     return {
         "name": info["name"],
         "arch": info["arch"],
@@ -86,6 +95,13 @@ def run_microbenchmarks(hbm_bytes: int = 1 << 30, iters: int = 20) -> dict[str, 
         "lds_write_bytes_per_cycle_cu": lds_w,
         "exchange_roundtrip_cycles_xcd": rt[0],
         "exchange_roundtrip_cycles_cross": rt[1],
+        "l1_read_bytes_per_cycle_cu": cache[0],
+        "l2_read_bytes_per_cycle_xcd": cache[1],
+        "l2_read_gbps": cache[2],
+        "slot_store_bytes_per_cycle_wg": xput[0],
+        "slot_store_gbps": xput[1],
+        "ticket_cycles_private": xput[2],
+        "ticket_cycles_shared": xput[3],
     }
 
 

@@ -1,130 +1,120 @@
-"""REPORT.md of a result bundle (the role of dsmem_eval/report.py:29-139).
+"""REPORT.md of a split-sweep bundle.
 
-A bundle is the directory the runner writes (credit_amd.runner.run_suite):
-metadata.json, summary.csv (one row per workload x width: best no-split
-variant, best split, the cost model's prediction), cluster_sweep.csv (one
-row per split factor), raw.csv, control.csv.  The report states how often
-splitting a row across workgroups beat the best single-workgroup variant,
-how often the cost model predicted that sign correctly, the results at the
-widest swept row, and where each workload's split first pays off (measured
-and predicted).  Rows read back from CSV carry strings; every field is
-converted here.
+The reference summarises a run in markdown (dsmem_eval/report.py:29-139).
+This report is organised around the two questions the gfx950 sweep answers:
+
+1. Did the cost model pick the right side -- split the row across P
+   workgroups or keep it in one -- at each (workload, width) point?  A grid
+   of workloads x widths shows the measured winner and whether the model
+   agreed, followed by the points it got wrong with both deltas.
+2. How close to HBM bandwidth does each side run?  Every point lists the
+   no-split and best-split rates as a fraction of the 8 TB/s MI355X peak,
+   the rate the roofline of the bench is quoted against.
+
+Rows are the typed summary rows of ``credit_amd.bundle`` (or the dicts
+``runner.build_summary`` returns, which carry the same keys and types).
 """
 from __future__ import annotations
 
 import math
 from collections import defaultdict
 from pathlib import Path
-from typing import Any, Iterable
+from typing import Any
+
+HBM_PEAK_GBPS = 8000.0
 
 
-def truth(value: Any) -> bool:
-    if isinstance(value, bool):
-        return value
-    return str(value).strip().lower() == "true"
+def _ok(v: Any) -> bool:
+    return v is True
 
 
-def _finite(value: Any) -> bool:
+def _num(v: Any) -> float:
     try:
-        return math.isfinite(float(value))
+        f = float(v)
     except (TypeError, ValueError):
-        return False
-
-
-def geometric_mean(values: Iterable[float]) -> float:
-    positive = [v for v in values if v > 0.0 and math.isfinite(v)]
-    if not positive:
         return math.nan
-    return math.exp(sum(math.log(v) for v in positive) / len(positive))
+    return f
 
 
-def crossovers(summary_rows: list[dict[str, Any]]) -> list[dict[str, Any]]:
-    """Per workload, the narrowest swept width at which the split measured
-    (and was predicted) faster than the best no-split variant; None when it
-    never was."""
-    by_workload: dict[str, list[dict[str, Any]]] = defaultdict(list)
-    for row in summary_rows:
-        by_workload[str(row["workload"])].append(row)
-    out = []
-    for name, rows in sorted(by_workload.items()):
-        ordered = sorted(rows, key=lambda r: int(r["cols"]))
-        measured = next((int(r["cols"]) for r in ordered if truth(r.get("measured_profitable"))), None)
-        predicted = next((int(r["cols"]) for r in ordered if truth(r.get("predicted_profitable"))),
-                         None)
-        out.append({"workload": name, "label": str(ordered[0].get("label", name)),
-                    "predicted": predicted, "measured": measured})
-    return out
+def _cell(row: dict[str, Any]) -> str:
+    """Measured winner at a point and the model's verdict on it."""
+    winner = f"P{row['measured_split']}" if _ok(row.get("measured_profitable")) else "one WG"
+    return f"{winner} {'ok' if _ok(row.get('model_correct')) else 'MISS'}"
 
 
-def build_report(summary_rows: list[dict[str, Any]],
-                 metadata: dict[str, Any]) -> tuple[str, dict[str, Any]]:
-    """(markdown, aggregate) for a bundle's summary rows and metadata."""
-    valid = [r for r in summary_rows if _finite(r.get("split_vs_block"))]
-    wins = sum(float(r["split_vs_block"]) > 1.0 for r in valid)
-    model_rows = [r for r in summary_rows if "model_correct" in r]
-    model_correct = sum(truth(r["model_correct"]) for r in model_rows)
-    widest = max((int(r["cols"]) for r in valid), default=0)
-    widest_rows = sorted((r for r in valid if int(r["cols"]) == widest),
-                         key=lambda r: str(r["workload"]))
-    widest_geomean = geometric_mean(float(r["split_vs_block"]) for r in widest_rows)
-    version = metadata.get("cost_model", {}).get("version", "")
-    device = f"{metadata.get('device', 'unknown device')} ({metadata.get('arch', '')})"
-    lines = [
-        f"# Split-row evaluation on {device}",
-        "",
-        f"- Splitting a row across workgroups beats the best single-workgroup variant on "
-        f"{wins}/{len(valid)} workload-width points.",
-        f"- The cost model ({version}) predicts {model_correct}/{len(model_rows)} "
-        f"profitability signs correctly.",
-    ]
-    if widest:
-        lines.append(f"- At N={widest}, the best split is {widest_geomean:.3f}x the best "
-                     f"single-workgroup variant (geometric mean over workloads).")
-    lines += ["", f"## Results at N={widest}", "",
-              "| Workload | rows | no-split | no-split ms | split ms | split / no-split | P | "
-              "predicted P | model correct |",
-              "|---|---:|---|---:|---:|---:|---:|---:|---|"]
-    for r in widest_rows:
-        lines.append(
-            f"| {r.get('label', r['workload'])} | {int(r['rows'])} | {r['block_variant']} "
-            f"| {float(r['block_ms']):.4f} | {float(r['split_ms']):.4f} "
-            f"| {float(r['split_vs_block']):.3f}x | {int(float(r['measured_split']))} "
-            f"| {int(float(r['predicted_split']))} | {truth(r.get('model_correct'))} |")
-    cross = crossovers(summary_rows)
-    lines += ["", "## Crossover validation", "",
-              "Narrowest swept width at which the split is faster than the best "
-              "single-workgroup variant.", "",
-              "| Workload | Predicted | Measured |", "|---|---:|---:|"]
-    for c in cross:
-        pred = "none" if c["predicted"] is None else str(c["predicted"])
-        meas = "none" if c["measured"] is None else str(c["measured"])
-        lines.append(f"| {c['label']} | {pred} | {meas} |")
-    lines += ["", "## All points", "",
-              "| workload | rows | cols | no-split | no-split ms | split ms | best P | "
-              "no-split GB/s | split GB/s | predicted | measured | correct |",
-              "|---|---:|---:|---|---:|---:|---:|---:|---:|---|---|---|"]
-    for r in sorted(valid, key=lambda r: (str(r["workload"]), int(r["cols"]))):
-        lines.append(
-            f"| {r['workload']} | {int(r['rows'])} | {int(r['cols'])} | {r['block_variant']} "
-            f"| {float(r['block_ms']):.4f} | {float(r['split_ms']):.4f} "
-            f"| {int(float(r['measured_split']))} | {float(r['block_gbps']):.0f} "
-            f"| {float(r['split_gbps']):.0f} | {truth(r.get('predicted_profitable'))} "
-            f"| {truth(r.get('measured_profitable'))} | {truth(r.get('model_correct'))} |")
-    aggregate = {
-        "device": str(metadata.get("device", "")),
-        "points": len(valid),
-        "split_wins": wins,
-        "model_points": len(model_rows),
-        "model_correct": model_correct,
-        "largest_width": widest,
-        "largest_width_geomean_speedup": widest_geomean,
-        "crossovers": cross,
+def summarize(rows: list[dict[str, Any]]) -> dict[str, Any]:
+    """Counts behind the report: overall and per workload."""
+    scored = [r for r in rows if r.get("model_correct") is not None]
+    per: dict[str, dict[str, int]] = defaultdict(lambda: {"points": 0, "split_wins": 0,
+                                                          "model_correct": 0})
+    for r in scored:
+        p = per[str(r["workload"])]
+        p["points"] += 1
+        p["split_wins"] += _ok(r.get("measured_profitable"))
+        p["model_correct"] += _ok(r.get("model_correct"))
+    misses = [{"workload": r["workload"], "cols": int(r["cols"]), "rows": int(r["rows"]),
+               "measured_delta_ms": _num(r.get("block_ms")) - _num(r.get("split_ms")),
+               "predicted_delta_ms": _num(r.get("predicted_delta_ms"))}
+              for r in scored if not _ok(r.get("model_correct"))]
+    correct = sum(p["model_correct"] for p in per.values())
+    return {
+        "points": len(scored),
+        "model_correct": correct,
+        "accuracy": correct / len(scored) if scored else math.nan,
+        "split_wins": sum(p["split_wins"] for p in per.values()),
+        "by_workload": dict(sorted(per.items())),
+        "misses": misses,
     }
-    return "\n".join(lines) + "\n", aggregate
 
 
-def write_report(output_dir: Path, summary_rows: list[dict[str, Any]],
+def render(rows: list[dict[str, Any]], metadata: dict[str, Any]) -> tuple[str, dict[str, Any]]:
+    """(markdown, aggregate) for a bundle's summary rows and metadata."""
+    agg = summarize(rows)
+    agg["device"] = str(metadata.get("device", ""))
+    model = metadata.get("cost_model", {}).get("version", "unknown model")
+    device = f"{metadata.get('device', 'unknown device')} ({metadata.get('arch', '?')})"
+    acc = agg["accuracy"]
+    out = [f"# Split-row sweep on {device}", "",
+           f"Cost model `{model}`: {agg['model_correct']}/{agg['points']} points decided "
+           f"correctly ({100 * acc:.1f}%)." if agg["points"] else "No scored points.",
+           f"Splitting the row measured faster at {agg['split_wins']} of them.", "",
+           "## Decisions by workload and width", "",
+           "Each cell: the measured winner (`P<k>`: split over k workgroups; `one WG`: the "
+           "best single-workgroup variant) and whether the model chose the same side.", ""]
+    widths = sorted({int(r["cols"]) for r in rows})
+    by_point = {(str(r["workload"]), int(r["cols"])): r for r in rows}
+    names = sorted({str(r["workload"]) for r in rows})
+    out.append("| workload | " + " | ".join(str(w) for w in widths) + " | correct |")
+    out.append("|---|" + "---|" * len(widths) + "---:|")
+    for name in names:
+        cells = [(_cell(by_point[(name, w)]) if (name, w) in by_point else "") for w in widths]
+        p = agg["by_workload"].get(name, {"points": 0, "model_correct": 0})
+        out.append(f"| {name} | " + " | ".join(cells) +
+                   f" | {p['model_correct']}/{p['points']} |")
+    out += ["", "## Points the model got wrong", ""]
+    if agg["misses"]:
+        out += ["| workload | rows | cols | measured gain of the split (ms) | predicted (ms) |",
+                "|---|---:|---:|---:|---:|"]
+        for m in agg["misses"]:
+            out.append(f"| {m['workload']} | {m['rows']} | {m['cols']} | "
+                       f"{m['measured_delta_ms']:+.4f} | {m['predicted_delta_ms']:+.4f} |")
+    else:
+        out.append("None.")
+    out += ["", "## HBM rate of each side", "",
+            f"Algorithmic bytes over the median time, and its fraction of {HBM_PEAK_GBPS:.0f} GB/s.",
+            "", "| workload | rows | cols | one-WG variant | one WG GB/s | frac | best P | "
+            "split GB/s | frac | predicted P |", "|---|---:|---:|---|---:|---:|---:|---:|---:|---:|"]
+    for r in sorted(rows, key=lambda r: (str(r["workload"]), int(r["cols"]))):
+        bg, sg = _num(r.get("block_gbps")), _num(r.get("split_gbps"))
+        out.append(f"| {r['workload']} | {int(r['rows'])} | {int(r['cols'])} | "
+                   f"{r.get('block_variant', '')} | {bg:.0f} | {bg / HBM_PEAK_GBPS:.3f} | "
+                   f"{r.get('measured_split', '')} | {sg:.0f} | {sg / HBM_PEAK_GBPS:.3f} | "
+                   f"{r.get('predicted_split', '')} |")
+    return "\n".join(out) + "\n", agg
+
+
+def write_report(output_dir: Path, rows: list[dict[str, Any]],
                  metadata: dict[str, Any]) -> dict[str, Any]:
-    report, aggregate = build_report(summary_rows, metadata)
-    (Path(output_dir) / "REPORT.md").write_text(report, encoding="utf-8")
-    return aggregate
+    text, agg = render(rows, metadata)
+    (Path(output_dir) / "REPORT.md").write_text(text, encoding="utf-8")
+    return agg

@@ -1,130 +1,142 @@
-"""Re-score saved result bundles with the current cost model (the role of
-scripts/rescore_cost_model.py:99-218).
+"""Re-score saved split-sweep bundles with the current cost model.
 
     python -m credit_amd.rescore RUN_DIR [RUN_DIR ...] [--write]
 
-For every cluster_sweep.csv row the prediction is recomputed from the
-bundle's own measurements -- the calibrated device profile in metadata.json,
-the row's measured control overhead and the point's best no-split time --
-so a bundle measured once on an MI355X can be re-scored after a model change
-without the GPU.  A dry run prints old -> new correct counts; --write keeps
-the first pre-rescore copies as summary.prev_model.csv /
-cluster_sweep.prev_model.csv, rewrites both CSVs, REPORT.md and the
-metadata's cost_model and aggregate fields.  Host-only: no GPU is touched.
+The role of the reference's scripts/rescore_cost_model.py:99-218: a bundle
+measured once on an MI355X is judged again, without a GPU, after the model
+changes.  Everything the model needs was saved by the run: the calibrated
+device profile (metadata.json "profile"), each split factor's measured
+control overhead (cluster_sweep.csv) and each point's best no-split time
+(summary.csv).  The measured side -- which variant won -- never changes;
+only the prediction does.
+
+A dry run reports the verdict counts before and after.  ``--write`` rewrites
+summary.csv, cluster_sweep.csv (through credit_amd.bundle's typed schemas),
+REPORT.md and the metadata's cost_model / aggregate fields, and appends one
+JSON line to ``rescore_history.jsonl`` recording the model versions and every
+point whose verdict changed, so the bundle keeps its own audit trail instead
+of copies of the old tables.
 """
 from __future__ import annotations
 
 import argparse
-import csv
 import dataclasses
 import json
-import shutil
-from collections import defaultdict
+import math
+from dataclasses import dataclass
+from datetime import datetime, timezone
 from pathlib import Path
 from typing import Any
 
+from .bundle import Bundle
 from .cost_model import MODEL_VERSION, DeviceProfile, estimate
-from .report import build_report, truth
+from .report import render
 from .workloads import WORKLOADS
 
+HISTORY = "rescore_history.jsonl"
 
-def read_csv(path: Path) -> list[dict[str, str]]:
-    with path.open(newline="", encoding="utf-8") as fh:
-        return list(csv.DictReader(fh))
-
-
-def write_csv(path: Path, rows: list[dict[str, Any]]) -> None:
-    if not rows:
-        return
-    fields: list[str] = []
-    for r in rows:
-        fields += [k for k in r if k not in fields]
-    tmp = path.with_suffix(path.suffix + ".tmp")
-    with tmp.open("w", newline="", encoding="utf-8") as fh:
-        w = csv.DictWriter(fh, fieldnames=fields)
-        w.writeheader()
-        w.writerows(rows)
-    tmp.replace(path)
+PointKey = tuple[str, int, int]
 
 
-def profile_from_metadata(metadata: dict[str, Any]) -> DeviceProfile:
-    """The calibrated profile the runner stored (profile_as_dict)."""
-    raw = metadata.get("profile")
-    if not raw:
-        raise ValueError("metadata.json has no calibrated 'profile' (an incomplete run?)")
-    kinds = {f.name: f.type for f in dataclasses.fields(DeviceProfile)}
-    missing = sorted(set(kinds) - set(raw))
-    if missing:
-        raise ValueError(f"metadata profile lacks {missing}")
-    conv = {"str": str, "int": int, "float": float}
-    return DeviceProfile(**{k: conv[t if isinstance(t, str) else t.__name__](raw[k])
-                            for k, t in kinds.items()})
+@dataclass(frozen=True)
+class Rescore:
+    run: str
+    device: str
+    points: int
+    correct_before: int
+    correct_after: int
+    changed: tuple[dict[str, Any], ...]
 
 
-def rescore(run: Path, write: bool = False) -> dict[str, Any]:
-    run = Path(run).resolve()
-    paths = {n: run / n for n in ("summary.csv", "cluster_sweep.csv", "metadata.json")}
-    missing = [n for n, p in paths.items() if not p.exists()]
-    if missing:
-        raise FileNotFoundError(f"{run}: missing {', '.join(missing)}")
-    metadata = json.loads(paths["metadata.json"].read_text(encoding="utf-8"))
-    profile = profile_from_metadata(metadata)
-    summary: list[dict[str, Any]] = read_csv(paths["summary.csv"])
-    sweep: list[dict[str, Any]] = read_csv(paths["cluster_sweep.csv"])
-    point = {(r["workload"], int(r["rows"]), int(r["cols"])): r for r in summary}
-    old_correct = sum(truth(r.get("model_correct")) for r in summary)
+def saved_profile(metadata: dict[str, Any]) -> DeviceProfile:
+    """The calibrated profile a run stored in its metadata.json."""
+    stored = metadata.get("profile")
+    if not isinstance(stored, dict):
+        raise ValueError("metadata.json carries no calibrated 'profile' (the run did not finish)")
+    values = {}
+    for f in dataclasses.fields(DeviceProfile):
+        if f.name not in stored:
+            raise ValueError(f"the saved profile lacks {f.name!r}")
+        kind = {"str": str, "int": int, "float": float}[f.type if isinstance(f.type, str)
+                                                         else f.type.__name__]
+        values[f.name] = kind(stored[f.name])
+    return DeviceProfile(**values)
 
-    estimates: dict[tuple[str, int, int], list[tuple[float, int, bool]]] = defaultdict(list)
-    for r in sweep:
-        key = (r["workload"], int(r["rows"]), int(r["cols"]))
-        if key not in point:
+
+def _key(row: dict[str, Any]) -> PointKey:
+    return str(row["workload"]), int(row["rows"]), int(row["cols"])
+
+
+def predict(bundle: Bundle, profile: DeviceProfile) -> dict[PointKey, dict[str, Any]]:
+    """New model terms for every sweep row (updated in place) and, per
+    point, the split factor with the largest predicted gain."""
+    block_ms = {_key(r): float(r["block_ms"]) for r in bundle.summary}
+    best: dict[PointKey, dict[str, Any]] = {}
+    for row in bundle.sweep:
+        key = _key(row)
+        if key not in block_ms or not math.isfinite(block_ms[key]) or block_ms[key] <= 0:
             continue
-        spec = dataclasses.replace(WORKLOADS[r["workload"]], rows=key[1])
-        m = estimate(spec, key[2], int(r["split"]), float(r["control_overhead_ms"]), profile,
-                     baseline_ms=float(point[key]["block_ms"]), rows=key[1])
-        r.update({"model_version": MODEL_VERSION, **dataclasses.asdict(m)})
-        estimates[key].append((m.predicted_delta_ms, int(r["split"]), m.predicted_profitable))
+        spec = dataclasses.replace(WORKLOADS[key[0]], rows=key[1])
+        est = estimate(spec, key[2], int(row["split"]), float(row["control_overhead_ms"]),
+                       profile, baseline_ms=block_ms[key], rows=key[1])
+        row.update(dataclasses.asdict(est), model_version=MODEL_VERSION)
+        if key not in best or est.predicted_delta_ms > best[key]["predicted_delta_ms"]:
+            best[key] = {"predicted_split": int(row["split"]),
+                         "predicted_delta_ms": est.predicted_delta_ms,
+                         "predicted_profitable": est.predicted_profitable}
+    return best
 
-    for key, r in point.items():
-        if not estimates[key]:
+
+def rescore(run: Path, write: bool = False) -> Rescore:
+    bundle = Bundle.load(run)
+    profile = saved_profile(bundle.metadata)
+    before = {_key(r): r.get("model_correct") is True for r in bundle.summary}
+    old_version = bundle.metadata.get("cost_model", {}).get("version")
+    best = predict(bundle, profile)
+    changed = []
+    for row in bundle.summary:
+        key = _key(row)
+        if key not in best:
             continue
-        delta, split, profitable = max(estimates[key], key=lambda e: e[0])
-        measured = truth(r["measured_profitable"])
-        r.update({"model_version": MODEL_VERSION, "predicted_split": split,
-                  "predicted_delta_ms": delta, "predicted_profitable": profitable,
-                  "model_correct": profitable == measured})
-    new_correct = sum(truth(r.get("model_correct")) for r in summary)
-    result = {"run": str(run), "device": str(metadata.get("device", "")),
-              "points": len(summary), "old_correct": old_correct, "new_correct": new_correct}
-    if not write:
-        return result
-    for name in ("summary.csv", "cluster_sweep.csv"):
-        backup = run / name.replace(".csv", ".prev_model.csv")
-        if not backup.exists():
-            shutil.copy2(paths[name], backup)
-    write_csv(paths["summary.csv"], summary)
-    write_csv(paths["cluster_sweep.csv"], sweep)
-    report, aggregate = build_report(summary, metadata)
-    (run / "REPORT.md").write_text(report, encoding="utf-8")
-    metadata["cost_model"] = {**metadata.get("cost_model", {}), "version": MODEL_VERSION,
-                              "previous_correct": old_correct, "revised_correct": new_correct,
-                              "points": len(summary)}
-    metadata["report"] = aggregate
-    paths["metadata.json"].write_text(json.dumps(metadata, indent=2) + "\n", encoding="utf-8")
+        row.update(best[key], model_version=MODEL_VERSION)
+        row["model_correct"] = row["predicted_profitable"] == (row["measured_profitable"] is True)
+        if row["model_correct"] != before[key]:
+            changed.append({"workload": key[0], "rows": key[1], "cols": key[2],
+                            "was_correct": before[key], "now_correct": row["model_correct"]})
+    result = Rescore(run=str(bundle.root), device=str(bundle.metadata.get("device", "")),
+                     points=len(bundle.summary), correct_before=sum(before.values()),
+                     correct_after=sum(r.get("model_correct") is True for r in bundle.summary),
+                     changed=tuple(changed))
+    if write:
+        stamp = datetime.now(timezone.utc).isoformat()
+        bundle.save_tables()
+        bundle.metadata["cost_model"] = {**bundle.metadata.get("cost_model", {}),
+                                         "version": MODEL_VERSION, "rescored_utc": stamp,
+                                         "history": HISTORY}
+        text, agg = render(bundle.summary, bundle.metadata)
+        (bundle.root / "REPORT.md").write_text(text, encoding="utf-8")
+        bundle.metadata["report"] = agg
+        bundle.save_metadata()
+        entry = {"utc": stamp, "model_before": old_version, "model_after": MODEL_VERSION,
+                 "points": result.points, "correct_before": result.correct_before,
+                 "correct_after": result.correct_after, "changed": list(changed)}
+        with (bundle.root / HISTORY).open("a", encoding="utf-8") as fh:
+            fh.write(json.dumps(entry) + "\n")
     return result
 
 
 def main(argv=None) -> int:
-    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap = argparse.ArgumentParser(description="re-score split-sweep bundles with the current model")
     ap.add_argument("runs", nargs="+", type=Path)
     ap.add_argument("--write", action="store_true",
-                    help="rewrite the bundles (first copies kept as *.prev_model.csv)")
+                    help="rewrite the bundles and append to their rescore_history.jsonl")
     args = ap.parse_args(argv)
     for run in args.runs:
         r = rescore(run, args.write)
-        print(f"{r['run']}: {r['old_correct']}/{r['points']} -> {r['new_correct']}/{r['points']}")
+        print(f"{r.run}: {r.correct_before}/{r.points} -> {r.correct_after}/{r.points} "
+              f"({len(r.changed)} verdicts changed)")
     if not args.write:
-        print("Dry run; pass --write to update the bundles.")
+        print("dry run: pass --write to update the bundles")
     return 0
 
 

@@ -24,7 +24,6 @@ predicted delta, ``measured_profitable`` is best split < block, and
 from __future__ import annotations
 
 import argparse
-import csv
 import dataclasses
 import json
 import math
@@ -36,14 +35,16 @@ from collections import defaultdict
 from dataclasses import asdict, dataclass
 from datetime import datetime, timezone
 from pathlib import Path
-from typing import Any, Callable, Iterable
+from typing import Any
 
 import torch
 
-from . import hip_lib
+from . import bundle, hip_lib
+from .bundle import write_table
 from .cost_model import MODEL_VERSION, DeviceProfile, estimate, staged_bytes_per_workgroup
 from .profile import format_profile_text, make_device_profile, profile_as_dict, run_microbenchmarks
 from .report import write_report
+from .timing import run_trials
 from .workloads import WORKLOADS, WorkloadSpec
 
 # Workloads with a split variant (the cost model's domain).
@@ -125,58 +126,6 @@ class RunConfig:
                                    warmup=2, iterations=5, trials=1, tensor_bytes=32 << 20)
 
 
-# ------------------------------------------------------------ statistics ---
-
-
-def percentile(samples: Iterable[float], fraction: float) -> float:
-    ordered = sorted(samples)
-    if not ordered:
-        return math.nan
-    pos = fraction * (len(ordered) - 1)
-    lo, hi = int(math.floor(pos)), int(math.ceil(pos))
-    if lo == hi:
-        return ordered[lo]
-    w = pos - lo
-    return ordered[lo] * (1.0 - w) + ordered[hi] * w
-
-
-def summarize(samples: Iterable[float]) -> dict[str, float]:
-    finite = [float(v) for v in samples if math.isfinite(float(v))]
-    if not finite:
-        return {"median": math.nan, "p20": math.nan, "p80": math.nan}
-    return {"median": statistics.median(finite), "p20": percentile(finite, 0.2),
-            "p80": percentile(finite, 0.8)}
-
-
-def benchmark_callable(fn: Callable[[int], object], warmup: int, iterations: int,
-                       trials: int, settle_ms: float = 0.0) -> list[float]:
-    """ms per call, one sample per trial (runner.py:166-182); fn(i) gets the
-    call index so callers can rotate buffer sets.  settle_ms of wall time
-    (synchronised every 8 calls) run before the warmup calls: HBM-bound work
-    after an idle period runs slow for its first 10-20 ms on the MI355X."""
-    t_end = time.perf_counter() + settle_ms / 1e3
-    while time.perf_counter() < t_end:
-        for i in range(8):
-            fn(i)
-        torch.cuda.synchronize()
-    for i in range(warmup):
-        fn(i)
-    torch.cuda.synchronize()
-    samples = []
-    k = warmup
-    for _ in range(trials):
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(iterations):
-            fn(k)
-            k += 1
-        stop.record()
-        stop.synchronize()
-        samples.append(start.elapsed_time(stop) / iterations)
-    return samples
-
-
 # ---------------------------------------------------------------- sweep ----
 
 
@@ -226,14 +175,14 @@ def measure_point(name: str, spec: WorkloadSpec, rows: int, cols: int, cfg: RunC
             # Arguments checked and converted once per buffer set: the timed
             # calls are the library calls alone, not the launcher's Python.
             bound = [hip_lib.bind(name, ins, o, lc) for ins, o in zip(sets, outs)]
-            samples = benchmark_callable(lambda i: bound[i % len(bound)](), cfg.warmup,
-                                         cfg.iterations, cfg.trials, cfg.settle_ms)
+            stats = run_trials(lambda i: bound[i % len(bound)](), cfg.trials, cfg.iterations,
+                               cfg.warmup, cfg.settle_ms)
+            hip_lib.check_watchdog()
+            row.update(ms=stats.median_ms, p20_ms=stats.p20_ms, p80_ms=stats.p80_ms,
+                       samples=stats.trials)
         except hip_lib.CreditError as err:
             row["error"] = f"{err.status}: {err}"
-            samples = []
-        stats = summarize(samples)
-        row.update(ms=stats["median"], p20_ms=stats["p20"], p80_ms=stats["p80"],
-                   samples=len(samples))
+            row.update(ms=math.nan, p20_ms=math.nan, p80_ms=math.nan, samples=0)
         results.append(row)
     del sets, outs, reference
     torch.cuda.empty_cache()
@@ -306,19 +255,6 @@ def build_summary(raw: list[dict[str, Any]], control: dict[tuple[int, int, int],
     return summary, sweep
 
 
-def write_csv(path: Path, rows: list[dict[str, Any]]) -> None:
-    if not rows:
-        return
-    path.parent.mkdir(parents=True, exist_ok=True)
-    fields: list[str] = []
-    for r in rows:  # union of the keys, first-seen order (error rows add one)
-        fields += [k for k in r if k not in fields]
-    with path.open("w", newline="", encoding="utf-8") as fh:
-        w = csv.DictWriter(fh, fieldnames=fields)
-        w.writeheader()
-        w.writerows(rows)
-
-
 def aggregate(summary: list[dict[str, Any]]) -> dict[str, Any]:
     n = len(summary)
     ok = sum(1 for r in summary if r["model_correct"])
@@ -377,13 +313,13 @@ def run_suite(raw_config: dict[str, Any], output_dir: Path,
                 key = (rows, p, spec.barrier_count)
                 if key not in control:
                     control[key] = measure_control(rows, p, spec.barrier_count, cfg)
-            write_csv(output_dir / "raw.csv", raw)
-    write_csv(output_dir / "control.csv",
-              [{"rows": r, "split": p, "barriers": b, "overhead_ms": v}
-               for (r, p, b), v in sorted(control.items())])
+            write_table(output_dir / "raw.csv", raw, bundle.RAW)
+    write_table(output_dir / "control.csv",
+                [{"rows": r, "split": p, "barriers": b, "overhead_ms": v}
+                 for (r, p, b), v in sorted(control.items())], bundle.CONTROL)
     summary, sweep = build_summary(raw, control, profile, cfg)
-    write_csv(output_dir / "summary.csv", summary)
-    write_csv(output_dir / "cluster_sweep.csv", sweep)
+    write_table(output_dir / "summary.csv", summary, bundle.SUMMARY)
+    write_table(output_dir / "cluster_sweep.csv", sweep, bundle.SWEEP)
     metadata.update(status="complete", elapsed_seconds=time.time() - started,
                     profile=profile_as_dict(profile), aggregate=aggregate(summary))
     metadata["report"] = write_report(output_dir, summary, metadata)

@@ -4,24 +4,60 @@
 write ``*_counter_collection.csv`` with one row per dispatch; the values are
 KiB.  On gfx950 the raw FETCH_SIZE reads half of the bytes a kernel fetches
 and WRITE_SIZE reads all of them, so each counter is scaled by what it reads
-for a plain copy kernel of known size (``python -m credit_amd.profile --only
-hbm_copy --hbm-bytes B``, whose every ``mb_copy*`` dispatch reads B bytes
-and writes B bytes).
+for a stream kernel of known size (``python -m credit_amd.profile --only
+hbm_copy --hbm-bytes B``: every ``mb_stream_kernel<1, 1, ...>`` dispatch
+reads B bytes and writes B bytes).
 
     python -m credit_amd.traffic --fetch F.csv --write W.csv \\
         --copy-fetch CF.csv --copy-write CW.csv --copy-bytes B --json out.json
 
 The JSON maps a short kernel name (template arguments kept, namespaces and
-parameter lists dropped) to its mean fetched and written bytes per dispatch;
-bench.py reports the sum as ``roofline.traffic`` for the headline kernel.
+parameter lists dropped) to its mean fetched and written bytes per dispatch,
+and records what it was measured on: the commit and a SHA-256 prefix of
+every kernel source under credit_amd/csrc.  bench.py reports a workload's
+sum as ``roofline.traffic`` only while the sources its kernels are built
+from still hash the same; after a kernel change the figure is stale and is
+reported as null until the counters are collected again.
 """
 from __future__ import annotations
 
 import argparse
 import collections
 import csv
+import hashlib
 import json
+import subprocess
 from pathlib import Path
+
+CSRC = Path(__file__).resolve().parent / "csrc"
+# Headers every kernel source includes: a change there can change any kernel.
+SHARED_SOURCES = ("common.hpp", "api_internal.hpp", "slices.hpp")
+
+
+def source_fingerprints(csrc: Path = CSRC) -> dict[str, str]:
+    """SHA-256 prefix (16 hex digits) of every .hip/.hpp file under csrc."""
+    out = {}
+    for path in sorted(csrc.iterdir()):
+        if path.suffix in (".hip", ".hpp"):
+            out[path.name] = hashlib.sha256(path.read_bytes()).hexdigest()[:16]
+    return out
+
+
+def sources_unchanged(stamped: dict[str, str], source: str, csrc: Path = CSRC) -> bool:
+    """True when `source` and the shared headers hash as they did when the
+    counters were collected (`stamped` = the summary's "sources")."""
+    now = source_fingerprints(csrc)
+    return all(name in stamped and stamped[name] == now.get(name)
+               for name in (source, *SHARED_SOURCES))
+
+
+def current_commit() -> str | None:
+    try:
+        out = subprocess.run(["git", "rev-parse", "--short=12", "HEAD"], capture_output=True,
+                             text=True, cwd=CSRC, check=True)
+        return out.stdout.strip() or None
+    except (OSError, subprocess.CalledProcessError):
+        return None
 
 
 def short_name(kernel: str) -> str:
@@ -49,15 +85,16 @@ def per_kernel_kib(path: str | Path) -> dict[str, tuple[float, int]]:
 
 
 def copy_scale(path: str | Path, copy_bytes: int) -> float:
-    """Bytes per counted KiB, from the mb_copy dispatches of a known size."""
-    vals = [kib for name, (kib, _) in per_kernel_kib(path).items() if name.startswith("mb_copy")]
+    """Bytes per counted KiB, from the 1:1 stream dispatches of a known size."""
+    vals = [kib for name, (kib, _) in per_kernel_kib(path).items()
+            if name.startswith("mb_stream_kernel<1, 1,")]
     if not vals:
-        raise RuntimeError(f"{path}: no mb_copy dispatches")
+        raise RuntimeError(f"{path}: no mb_stream_kernel<1, 1, ...> dispatches")
     return copy_bytes / (sum(vals) / len(vals))
 
 
 def summarize(fetch: str, write: str, copy_fetch: str, copy_write: str,
-              copy_bytes: int) -> dict:
+              copy_bytes: int, commit: str | None = None) -> dict:
     fs = copy_scale(copy_fetch, copy_bytes)
     ws = copy_scale(copy_write, copy_bytes)
     f = per_kernel_kib(fetch)
@@ -69,7 +106,8 @@ def summarize(fetch: str, write: str, copy_fetch: str, copy_write: str,
         kernels[name] = {"fetch_bytes": round(fk[0] * fs), "write_bytes": round(wk[0] * ws),
                          "dispatches": max(fk[1], wk[1])}
     return {"fetch_bytes_per_kib": fs, "write_bytes_per_kib": ws, "copy_bytes": copy_bytes,
-            "kernels": kernels}
+            "commit": commit if commit is not None else current_commit(),
+            "sources": source_fingerprints(), "kernels": kernels}
 
 
 def kernel_stats(path: str | Path) -> dict[str, dict[str, float]]:
@@ -111,10 +149,12 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-write", required=True)
     ap.add_argument("--copy-bytes", type=int, required=True)
     ap.add_argument("--json", required=True)
+    ap.add_argument("--commit", help="commit the counters were collected at (default: git HEAD)")
     ap.add_argument("--stats", help="rocprofv3 --stats kernel summary CSV of the same workload")
     ap.add_argument("--markdown", help="write the per-kernel trace + traffic table here")
     args = ap.parse_args(argv)
-    out = summarize(args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_bytes)
+    out = summarize(args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_bytes,
+                    args.commit)
     Path(args.json).write_text(json.dumps(out, indent=1) + "\n")
     if args.markdown:
         if not args.stats:

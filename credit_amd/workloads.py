@@ -53,6 +53,11 @@ class WorkloadSpec:
     # Widest row the STAGED (no-split, row held on chip) variant takes; 0 when
     # the operation has no split variant.  Wider rows need SPLIT or READ.
     staged_max_cols: int = 0
+    # HBM read:write byte mix of one call, as whole streams (row_sum_max 1:0,
+    # a norm forward 1:1, a backward reading x and dy for dx 2:1, ...): the
+    # mix of the stream ceiling the kernel's rate is compared with.  (0, 0)
+    # for compute-bound work.
+    stream_mix: tuple[int, int] = (0, 0)
 
     @property
     def barrier_count(self) -> int:
@@ -207,6 +212,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=0,
         reductions_per_stage=(2,),
         staged_max_cols=1 << 30,
+        stream_mix=(1, 0),
     ),
     "layernorm_fwd": WorkloadSpec(
         name="layernorm_fwd",
@@ -223,6 +229,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=2,
         reductions_per_stage=(1, 1),
         staged_max_cols=65536,
+        stream_mix=(1, 1),
     ),
     "rmsnorm_fwd": WorkloadSpec(
         name="rmsnorm_fwd",
@@ -239,6 +246,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=2,
         reductions_per_stage=(1,),
         staged_max_cols=65536,
+        stream_mix=(1, 1),
     ),
     "rmsnorm_bwd": WorkloadSpec(
         name="rmsnorm_bwd",
@@ -255,6 +263,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=4,
         reductions_per_stage=(1,),
         staged_max_cols=8192,
+        stream_mix=(2, 1),
     ),
     "softmax_fwd": WorkloadSpec(
         name="softmax_fwd",
@@ -271,6 +280,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=4,
         reductions_per_stage=(2,),
         staged_max_cols=65536,
+        stream_mix=(1, 1),
     ),
     "softmax_bwd": WorkloadSpec(
         name="softmax_bwd",
@@ -287,6 +297,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=8,
         reductions_per_stage=(1,),
         staged_max_cols=32768,
+        stream_mix=(2, 1),
     ),
     "ffn": WorkloadSpec(
         name="ffn",
@@ -328,6 +339,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=4,
         reductions_per_stage=(2, 2),
         staged_max_cols=32768,
+        stream_mix=(2, 1),
     ),
     "layernorm_backward_bf16": WorkloadSpec(
         name="layernorm_backward_bf16",
@@ -345,6 +357,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=2,
         reductions_per_stage=(2, 2),
         staged_max_cols=32768,
+        stream_mix=(2, 1),
     ),
     "softmax_logits_backward": WorkloadSpec(
         name="softmax_logits_backward",
@@ -362,6 +375,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=8,
         reductions_per_stage=(2, 1),
         staged_max_cols=32768,
+        stream_mix=(2, 1),
     ),
     # dsmem_eval/workloads.py:150-154,203-211; metadata
     # dsmem_eval/workload_metadata.py:32-34.  q is bit-exact; the scale is
@@ -382,6 +396,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=4,
         reductions_per_stage=(1,),
         staged_max_cols=65536,
+        stream_mix=(4, 1),
     ),
     # dsmem_eval/workloads.py:128-143,194-202.  This build's READ variant
     # streams w, g, m twice (24 B) and writes w', u (8 B); staging w and u
@@ -402,6 +417,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=8,
         reductions_per_stage=(2,),
         staged_max_cols=32768,
+        stream_mix=(3, 2),
     ),
     # dsmem_eval/workloads.py:64-85,167-175.  One exchange of five sums per
     # row (the reference: three stages, (2, 1, 2)).
@@ -421,6 +437,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=12,
         reductions_per_stage=(5,),
         staged_max_cols=16384,
+        stream_mix=(3, 1),
     ),
     # dsmem_eval/workloads.py:88-112,176-184.  One exchange of five sums per
     # row (the reference: two stages, (2, 3)).
@@ -440,6 +457,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=8,
         reductions_per_stage=(5,),
         staged_max_cols=32768,
+        stream_mix=(2, 2),
     ),
 }
 

@@ -24,12 +24,38 @@
  *  - Streams: work is enqueued on cfg->stream (a hipStream_t; NULL means the
  *    null stream).  cfg itself may be NULL (= all defaults).
  *  - Workspace: split-row variants exchange partial results through a device
- *    scratch buffer.  With cfg->workspace == NULL the library uses a cached
- *    per-device buffer; otherwise cfg->workspace must hold at least
- *    credit_workspace_bytes(...) bytes, be 256-byte aligned and be
- *    zero-filled before its first use.  Every call that completes leaves it
- *    in that state again, so it needs no clearing between calls.  Calls that
- *    share one workspace must not run concurrently.
+ *    buffer: a 256-byte header (the watchdog word), a 1 MiB counter area
+ *    (ticket dispensers, arrival counters), a 4 MiB area of tagged exchange
+ *    slots, then per-call scratch (dweight partials, the FFN's hidden
+ *    activation, ...).
+ *    - cfg->workspace == NULL: the library keeps one buffer per (device,
+ *      stream) and grows it on demand.  Calls on one stream run in order,
+ *      calls on different streams get different buffers, so concurrent
+ *      streams never share partials.  The first call on a stream (and any
+ *      call that needs a larger buffer) allocates with hipMalloc, so such a
+ *      call cannot be captured into a HIP graph; a grown-out buffer is
+ *      retired, not freed, while work queued earlier may still use it.
+ *    - cfg->workspace set: it must hold credit_workspace_bytes(...) bytes,
+ *      be 256-byte aligned, and its first 5 MiB + 256 bytes (header,
+ *      counters, slots) must read zero before its first use.  Calls keep
+ *      those bytes in that state (counters return to zero; slot tags are
+ *      fresh per launch), so no clearing is needed between calls; the
+ *      scratch part is overwritten freely.  Calls that share one caller
+ *      workspace must not run concurrently (on different streams).  Slot
+ *      tags are drawn from a 32-bit process-wide counter: after 2^32 - 1
+ *      exchange stages it restarts, the library then re-zeroes the slot
+ *      areas of its own buffers, and a caller workspace should be re-zeroed
+ *      by its owner.
+ *  - Split launches and co-residency: the SPLIT kernels (and AUTO when it
+ *    splits a row) size their grid to the workgroups the device holds at
+ *    once and wait inside a group for all of its members.  They need the
+ *    device's CUs to themselves: a kernel on another stream that occupies
+ *    CUs meanwhile can delay members until the bounded wait (about 2^21
+ *    polls, 1-2 s) expires.  The launch then finishes with wrong outputs
+ *    and raises the workspace's watchdog word; the call itself returned
+ *    CREDIT_OK when it was enqueued, so callers that run split calls beside
+ *    other work check credit_check_watchdog() (CREDIT_ERR_WATCHDOG) after
+ *    synchronising.
  */
 #ifndef CREDIT_H_
 #define CREDIT_H_
@@ -143,10 +169,15 @@ int credit_row_sum_max_f32(const float* x, float* sum, float* max,
 
 /* --------------------------------------------- C2: LayerNorm forward -----
  * y = (x - mean) * rstd * gamma + beta over each row, bf16 in/out, fp32
- * statistics (two-pass: mean, then mean of squared deviations).  No
- * forward kernel exists in the reference; its statistics follow
+ * statistics: mean and the mean squared deviation about it, formed from
+ * one pass of sum(x) and sum(x^2) (fp64 across lanes) when mean^2 <= var/4,
+ * else from a second pass of squared deviations (rows with a large offset).
+ * No forward kernel exists in the reference; its statistics follow
  * src/workloads/layernorm_backward.cu:286-295 and the eps of
- * dsmem_eval/workloads.py:55. */
+ * dsmem_eval/workloads.py:55.  Variants: STAGED (row in one workgroup's
+ * VGPRs, cols <= 65536), READ (three streaming passes; any shape); SPLIT is
+ * not built.  AUTO: the persistent two-row pipeline for tall matrices of
+ * 16385..32768 columns, else STAGED, else READ. */
 int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamma,
                               const uint16_t* beta, uint16_t* y, float* mean,
                               float* rstd, int64_t rows, int64_t cols,
@@ -330,7 +361,23 @@ int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t rows, int6
  *   EXCHANGE_ROUNDTRIP  : [0] cycles per device-scope atomic round trip
  *                         between two workgroups on one XCD, [1] on two
  *                         XCDs (iters = rounds); the gfx950 stand-in for
- *                         the reference's DSMEM latency/visibility tests */
+ *                         the reference's DSMEM latency/visibility tests
+ *   CACHE_READ          : [0] bytes per cycle per CU read from its vector
+ *                         L1 (16 KiB working set), [1] bytes per cycle per
+ *                         XCD read from L2 (2 MiB working set), [2] that L2
+ *                         rate as device GB/s (iters = passes); replaces
+ *                         l1_bandwidth_kernel / l2_bandwidth_kernel of
+ *                         src/primitive_benchmark.cu:118-158
+ *   EXCHANGE_THROUGHPUT : [0] bytes per cycle per workgroup of device-scope
+ *                         64-bit slot stores (the split exchange's publish)
+ *                         with one workgroup per CU, [1] the same as device
+ *                         GB/s, [2] cycles per ticket draw (device-scope
+ *                         fetch-add with return) on a private line, [3] on
+ *                         one line shared by one workgroup per CU (iters =
+ *                         store rounds); replaces the DSMEM store/load
+ *                         throughput of src/primitive_benchmark.cu:433-503
+ *  HBM_READ/WRITE/COPY run the mixed-stream kernels of credit_stream_ceiling
+ *  (mixes 1:0, 0:1, 1:1). */
 #define CREDIT_MB_HBM_READ 1
 #define CREDIT_MB_HBM_WRITE 2
 #define CREDIT_MB_HBM_COPY 3
@@ -339,8 +386,28 @@ int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t rows, int6
 #define CREDIT_MB_LDS_READ 6
 #define CREDIT_MB_LDS_WRITE 7
 #define CREDIT_MB_EXCHANGE_ROUNDTRIP 8
+#define CREDIT_MB_CACHE_READ 9
+#define CREDIT_MB_EXCHANGE_THROUGHPUT 10
 int credit_microbench(int32_t which, int64_t bytes, int32_t iters, double* results,
                       int32_t n_results);
+
+/* Settled HBM stream ceiling of a read:write byte mix: `reads` source and
+ * `writes` destination streams of call_bytes / (reads + writes) bytes each
+ * (rounded down to 64 KiB), three rotating buffer sets (so the 256 MB MALL
+ * cannot serve a repeated set), every launch shape of the library's stream
+ * kernel with nontemporal and with plain stores.  Each shape runs
+ * back-to-back for settle_ms, then `trials` blocks of `iters` launches;
+ * its time is the median block's per-launch time.  Mixes built: 1:0 0:1
+ * 1:1 2:1 3:1 4:1 3:2 2:2 1:2.  results: [0] best GB/s, [1] its ms per
+ * call, [2] lanes per workgroup, [3] 16-byte vectors per lane and stream,
+ * [4] workgroups per CU, [5] 1 if nontemporal stores, [6] bytes moved per
+ * call, then the GB/s of every (store policy, shape) tried.  The
+ * reference's dram_bandwidth_kernel (src/primitive_benchmark.cu:160-171)
+ * measures the 1:1 mix once; this is the ceiling each wide-row kernel's
+ * HBM rate is compared with at its own mix and size.  Runs on the null
+ * stream of the current device and allocates its own buffers. */
+int credit_stream_ceiling(int32_t reads, int32_t writes, int64_t call_bytes, int32_t trials,
+                          int32_t iters, double settle_ms, double* results, int32_t n_results);
 
 /* Replaces build/cluster_control (src/cluster_control.cu:114-180, read at
  * dsmem_eval/runner.py:313-347): time of a grid of `rows` groups of `split`

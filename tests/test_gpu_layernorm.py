@@ -102,3 +102,20 @@ def test_layernorm_fwd_pipeline_back_to_back(gpu):
         for a, b_ in zip(first, o):
             assert torch.equal(a, b_.cpu())
     check(x, g, b, *(t.float().numpy() for t in first))
+
+
+@pytest.mark.parametrize("shape", [(600, 32768), (520, 24576)])
+def test_layernorm_fwd_offset_rows_take_the_two_pass_statistics(gpu, shape):
+    """Rows whose mean is large against their spread (mean^2 > var/4) leave
+    the one-pass sums for the second pass over squared deviations; rows with
+    a small offset stay on the one-pass path.  Both agree with the float64
+    two-pass oracle at fp32 tolerance, in the pipeline and in STAGED."""
+    x, g, b = SPEC.make_inputs(*shape, seed=41)
+    xf = x.float()
+    xf[0::4] = xf[0::4] * 0.01 + 300.0  # mean^2 / var ~ 1e9: two-pass
+    xf[1::4] = xf[1::4] + 0.4           # mean^2 / var = 0.16: one-pass
+    xf[2::4] = xf[2::4] * 1e-3 - 5e-4   # small values, small offset
+    x = xf.bfloat16()
+    for variant in ("auto", "staged"):
+        print(f"layernorm_fwd offset rows {variant} shape={shape}", flush=True)
+        check(x, g, b, *run(x, g, b, variant, gpu))

@@ -99,3 +99,20 @@ def test_control_overhead_runs_clean(gpu):
     """The barrier microbenchmark takes the same co-resident shape."""
     plain_ms, split_ms = hip_lib.control_overhead(4096, 8, 2, warmup=2, iters=5)
     assert plain_ms > 0 and split_ms > 0
+
+
+def test_split_calls_on_two_streams_use_their_own_workspaces(gpu):
+    """NULL-workspace split calls on a second stream get that stream's own
+    buffer (allocated and zeroed on first use) and the same results; the
+    calls are serialised, so their grids never share the device."""
+    x, w, dy = WORKLOADS["rmsnorm_fwd"].make_inputs(64, 65536, seed=8)
+    xs, ws_ = x.to(gpu), w.to(gpu)
+    results = []
+    for stream in (torch.cuda.current_stream(), torch.cuda.Stream()):
+        with torch.cuda.stream(stream):
+            y, rstd = hip_lib.allocate_outputs("rmsnorm_fwd", (xs, ws_))
+            hip_lib.rmsnorm_fwd(xs, ws_, y, rstd, 1e-6, hip_lib.make_cfg("split", 4))
+            hip_lib.check_watchdog(hip_lib.make_cfg())
+        stream.synchronize()
+        results.append((y.cpu(), rstd.cpu()))
+    assert torch.equal(results[0][0], results[1][0]) and torch.equal(results[0][1], results[1][1])

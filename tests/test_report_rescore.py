@@ -2,14 +2,16 @@
 credit_amd.rescore), the roles of dsmem_eval/report.py:29-139 and
 scripts/rescore_cost_model.py:99-218.  Host-only: a synthetic bundle is
 scored with the nominal MI355X profile."""
-import csv
 import json
 from dataclasses import asdict
 
+import pytest
+
+from credit_amd import bundle
 from credit_amd import rescore as rs
 from credit_amd.cost_model import MI355X_NOMINAL, MODEL_VERSION
-from credit_amd.report import build_report
-from credit_amd.runner import RunConfig, build_summary, write_csv
+from credit_amd.report import render
+from credit_amd.runner import RunConfig, build_summary
 
 
 def synthetic_bundle(tmp_path):
@@ -30,55 +32,62 @@ def synthetic_bundle(tmp_path):
                     control[(rows, p, barriers)] = 0.004
     summary, sweep = build_summary(raw, control, MI355X_NOMINAL, RunConfig())
     run = tmp_path / "bundle"
-    write_csv(run / "summary.csv", summary)
-    write_csv(run / "cluster_sweep.csv", sweep)
+    bundle.write_table(run / "summary.csv", summary, bundle.SUMMARY)
+    bundle.write_table(run / "cluster_sweep.csv", sweep, bundle.SWEEP)
     meta = {"device": "test", "arch": "gfx950", "cost_model": {"version": MODEL_VERSION},
             "profile": asdict(MI355X_NOMINAL)}
     (run / "metadata.json").write_text(json.dumps(meta))
     return run, summary, meta
 
 
-def test_report_counts_and_crossovers(tmp_path):
+def test_report_grid_and_counts(tmp_path):
     _, summary, meta = synthetic_bundle(tmp_path)
-    text, agg = build_report(summary, meta)
+    text, agg = render(summary, meta)
     assert agg["points"] == 4 and agg["split_wins"] == 2
-    assert agg["largest_width"] == 262144
-    assert abs(agg["largest_width_geomean_speedup"] - 0.40 / 0.15) < 1e-9
-    cross = {c["workload"]: c for c in agg["crossovers"]}
-    assert cross["softmax_fwd"]["measured"] == 262144
-    assert "## All points" in text and text.count("| softmax_fwd |") == 2
+    assert agg["model_correct"] == sum(r["model_correct"] for r in summary)
+    assert set(agg["by_workload"]) == {"softmax_fwd", "layernorm_backward"}
+    assert len(agg["misses"]) == 4 - agg["model_correct"]
+    # one grid row per workload, one column per width
+    grid = [l for l in text.splitlines() if l.startswith("| softmax_fwd |")]
+    assert len(grid) == 3  # the decision grid row and two rate rows
+    assert "| 4096 | 262144 |" in text
+    assert "P2 " in grid[0]  # the split (P=2) measured fastest at 262144
 
 
-def test_rescore_reproduces_then_repairs(tmp_path):
+def test_rescore_keeps_verdicts_then_repairs_them(tmp_path):
     run, summary, _ = synthetic_bundle(tmp_path)
     correct = sum(bool(r["model_correct"]) for r in summary)
     r = rs.rescore(run)
-    assert r["old_correct"] == r["new_correct"] == correct  # same model, same verdicts
-    # Corrupt the stored verdicts; a --write rescore recomputes them.
-    path = run / "summary.csv"
-    rows = list(csv.DictReader(path.open()))
-    for row in rows:
-        row["model_correct"] = "False"
-        row["predicted_profitable"] = "garbage"
-    rs.write_csv(path, rows)
+    assert r.correct_before == r.correct_after == correct and not r.changed
+    # Corrupt the stored verdicts; a --write rescore recomputes them and
+    # records every change in the bundle's history.
+    b = bundle.Bundle.load(run)
+    for row in b.summary:
+        row["model_correct"] = False
+        row["predicted_profitable"] = None
+    b.save_tables()
     r = rs.rescore(run, write=True)
-    assert r["old_correct"] == 0 and r["new_correct"] == correct
-    assert (run / "summary.prev_model.csv").exists() and (run / "REPORT.md").exists()
+    assert r.correct_before == 0 and r.correct_after == correct
+    assert len(r.changed) == correct
+    history = [json.loads(l) for l in (run / rs.HISTORY).read_text().splitlines()]
+    assert history[-1]["correct_after"] == correct and history[-1]["model_after"] == MODEL_VERSION
     meta = json.loads((run / "metadata.json").read_text())
-    assert meta["cost_model"]["revised_correct"] == correct
-    assert f"predicts {correct}/4" in (run / "REPORT.md").read_text()
-    # A second --write keeps the first backup.
-    first = (run / "summary.prev_model.csv").read_text()
+    assert meta["report"]["model_correct"] == correct
+    assert f"{correct}/4 points decided correctly" in (run / "REPORT.md").read_text()
+    # A second write appends a history line with nothing changed.
     rs.rescore(run, write=True)
-    assert (run / "summary.prev_model.csv").read_text() == first
+    history = [json.loads(l) for l in (run / rs.HISTORY).read_text().splitlines()]
+    assert len(history) == 2 and history[-1]["changed"] == []
 
 
 def test_rescore_rejects_incomplete_bundles(tmp_path):
     run, _, _ = synthetic_bundle(tmp_path)
     (run / "cluster_sweep.csv").unlink()
-    try:
+    with pytest.raises(FileNotFoundError, match="cluster_sweep.csv"):
         rs.rescore(run)
-    except FileNotFoundError as err:
-        assert "cluster_sweep.csv" in str(err)
-    else:
-        raise AssertionError("missing file accepted")
+    run2, _, _ = synthetic_bundle(tmp_path / "b2")
+    meta = json.loads((run2 / "metadata.json").read_text())
+    del meta["profile"]
+    (run2 / "metadata.json").write_text(json.dumps(meta))
+    with pytest.raises(ValueError, match="profile"):
+        rs.rescore(run2)

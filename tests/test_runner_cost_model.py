@@ -7,7 +7,8 @@ import pytest
 
 from credit_amd import cost_model
 from credit_amd.profile import format_profile_text, make_device_profile, parse_profile_text
-from credit_amd.runner import RunConfig, aggregate, build_summary, percentile, summarize
+from credit_amd.runner import RunConfig, aggregate, build_summary
+from credit_amd.timing import TrialStats
 from credit_amd.workloads import WORKLOADS
 
 PARSED = {
@@ -17,7 +18,10 @@ PARSED = {
     "hbm_latency_cycles": 910.0, "hbm_read_gbps": 6100.0, "hbm_write_gbps": 4600.0,
     "hbm_copy_gbps": 6000.0, "lds_read_bytes_per_cycle_cu": 98.0,
     "lds_write_bytes_per_cycle_cu": 66.0, "exchange_roundtrip_cycles_xcd": 2050.0,
-    "exchange_roundtrip_cycles_cross": 2900.0,
+    "exchange_roundtrip_cycles_cross": 2900.0, "l1_read_bytes_per_cycle_cu": 64.0,
+    "l2_read_bytes_per_cycle_xcd": 1024.0, "l2_read_gbps": 19000.0,
+    "slot_store_bytes_per_cycle_wg": 2.5, "slot_store_gbps": 1500.0,
+    "ticket_cycles_private": 900.0, "ticket_cycles_shared": 4000.0,
 }
 
 
@@ -64,11 +68,18 @@ def test_rows_wider_than_staging_save_rereads():
     assert narrow.saved_reread_ms == 0.0
 
 
-def test_percentile_and_summarize():
-    assert percentile([1, 2, 3, 4], 0.5) == pytest.approx(2.5)
-    s = summarize([3.0, float("nan"), 1.0, 2.0])
-    assert s["median"] == 2.0
-    assert math.isnan(summarize([])["median"])
+def test_trial_stats_quantiles():
+    """Median and inclusive-method 20th/80th percentiles: with samples
+    1..5 the percentiles sit at 0.8 and 3.2 positions of the sorted list."""
+    t = TrialStats((5.0, 1.0, 3.0, 2.0, 4.0), iters=20)
+    assert t.median_ms == 3.0
+    assert t.p20_ms == pytest.approx(1.8) and t.p80_ms == pytest.approx(4.2)
+    assert t.as_dict()["trials"] == 5 and t.as_dict()["iters"] == 20
+    one = TrialStats((2.5,), iters=20)
+    assert one.median_ms == one.p20_ms == one.p80_ms == 2.5
+    nan = TrialStats((float("nan"), 1.0, 3.0), iters=1)
+    assert nan.median_ms == 2.0
+    assert math.isnan(TrialStats((), iters=1).median_ms)
 
 
 def test_run_config_validation_and_quick():
@@ -108,9 +119,23 @@ def test_build_summary_scores_model_like_the_reference():
     assert agg["points"] == 2 and 0 <= agg["model_accuracy"] <= 1
 
 
-def test_write_csv_takes_the_union_of_keys(tmp_path):
-    from credit_amd.runner import write_csv
+def test_bundle_tables_round_trip_typed(tmp_path):
+    """Tables are written in schema order and read back with their types;
+    a missing value reads as None, NaN survives, an unknown column is an
+    error on write."""
+    from credit_amd import bundle
 
-    write_csv(tmp_path / "r.csv", [{"a": 1, "b": 2}, {"a": 3, "error": "x"}])
-    lines = (tmp_path / "r.csv").read_text().splitlines()
-    assert lines[0] == "a,b,error" and lines[2] == "3,,x"
+    rows = [{"workload": "softmax_fwd", "rows": 512, "cols": 262144, "variant": "split",
+             "split": 4, "correct": True, "ms": 0.25, "p20_ms": 0.24, "p80_ms": 0.26,
+             "samples": 5},
+            {"workload": "softmax_fwd", "rows": 512, "cols": 262144, "variant": "split",
+             "split": 64, "ms": float("nan"), "error": "-4: unsupported"}]
+    path = tmp_path / "raw.csv"
+    bundle.write_table(path, rows, bundle.RAW)
+    assert path.read_text().splitlines()[0] == ",".join(n for n, _ in bundle.RAW)
+    back = bundle.read_table(path, bundle.RAW)
+    assert back[0]["correct"] is True and back[0]["split"] == 4 and back[0]["ms"] == 0.25
+    assert back[1]["correct"] is None and math.isnan(back[1]["ms"])
+    assert back[1]["error"] == "-4: unsupported"
+    with pytest.raises(ValueError):
+        bundle.write_table(path, [{"workload": "x", "surprise": 1}], bundle.RAW)
