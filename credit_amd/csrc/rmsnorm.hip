@@ -27,6 +27,8 @@
 // Algorithmic traffic (bytes): forward 2MN (x) + 2N (w) + 2MN (y) + 4M
 // (rstd); backward 4MN (x, dy) + 2N + 4M + 2MN (dx) + 4N (dw).
 #include <initializer_list>
+#include <mutex>
+#include <vector>
 
 #include "api_internal.hpp"
 #include "common.hpp"
@@ -797,6 +799,44 @@ size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
                                bwd_extra_bytes(p, rows, cols));
 }
 
+// ----------------------------------------------- allocation-free variant --
+// credit_rmsnorm_bwd_bf16_noalloc runs the backward with its workspace (the
+// layout of api_internal.hpp: watchdog header, counters, exchange slots,
+// then the dweight partials) in this fixed device array instead of a
+// hipMalloc'd buffer.  40 MiB covers the BASELINE shape (1024 x 131072:
+// 5 MiB of header, counters and slots plus 16 MiB of fp64 partials) and any
+// width up to 262144 at that grouping.  The array is zero at module load,
+// which is the state the header, counters and slots need; every completed
+// call leaves them so (dispensers return to zero, slot tags are fresh per
+// launch), and the partials are written before they are read.
+constexpr size_t kNoAllocScratchBytes = size_t{40} << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_noalloc_mu;
+std::vector<char*> g_noalloc_base;  // per device: scratch's device address
+
+// The device address of `scratch` on the current device, looked up once
+// per device.  The host-side name is only a handle for the lookup, never an
+// address to pass to a kernel.
+int noalloc_scratch(char** out) {
+  int dev = 0;
+  CREDIT_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (static_cast<int>(g_noalloc_base.size()) <= dev) g_noalloc_base.resize(dev + 1, nullptr);
+  if (g_noalloc_base[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return hip_failure(err, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr || reinterpret_cast<uintptr_t>(p) % 256 != 0)
+      return set_error(CREDIT_ERR_HIP, "scratch has no 256-byte aligned device address");
+    g_noalloc_base[dev] = static_cast<char*>(p);
+  }
+  *out = g_noalloc_base[dev];
+  return CREDIT_OK;
+}
+}  // namespace
+
 }  // namespace credit
 
 using namespace credit;
@@ -932,4 +972,32 @@ extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
   rmsnorm_dw_reduce_kernel<<<dim3(reduce_blocks), dim3(256), 0, stream>>>(
       dw_part, dw, static_cast<int>(plan.groups), c);
   return check_launch("rmsnorm_dw_reduce_kernel");
+}
+
+extern "C" int credit_rmsnorm_bwd_bf16_noalloc(const uint16_t* x, const uint16_t* w,
+                                               const uint16_t* dy, const float* rstd,
+                                               uint16_t* dx, float* dw, int64_t rows,
+                                               int64_t cols, const credit_cfg* cfg) {
+  CREDIT_TRY(check_cfg(cfg));
+  if (cfg != nullptr && cfg->workspace != nullptr)
+    return set_error(CREDIT_ERR_BAD_CONFIG,
+                     "rmsnorm_bwd_noalloc takes no cfg->workspace (it uses the library's fixed "
+                     "scratch array); pass the workspace to credit_rmsnorm_bwd_bf16 instead");
+  const DeviceProps* props = nullptr;
+  CREDIT_TRY(current_device_props(&props));
+  const size_t body = rmsnorm_bwd_workspace(rows, cols, cfg_variant(cfg), cfg_split(cfg),
+                                            props->cu_count);
+  const size_t need = kScratchOffset + body;
+  if (need > kNoAllocScratchBytes)
+    return set_error(CREDIT_ERR_WORKSPACE,
+                     "rmsnorm_bwd_noalloc: %lld x %lld needs %zu bytes of scratch, more than "
+                     "the fixed %zu-byte array; use credit_rmsnorm_bwd_bf16",
+                     static_cast<long long>(rows), static_cast<long long>(cols), need,
+                     kNoAllocScratchBytes);
+  char* base = nullptr;
+  CREDIT_TRY(noalloc_scratch(&base));
+  credit_cfg c = cfg != nullptr ? *cfg : credit_cfg{nullptr, CREDIT_VARIANT_AUTO, 0, nullptr, 0};
+  c.workspace = base;
+  c.workspace_bytes = kNoAllocScratchBytes;
+  return credit_rmsnorm_bwd_bf16(x, w, dy, rstd, dx, dw, rows, cols, &c);
 }

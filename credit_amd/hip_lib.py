@@ -117,6 +117,7 @@ SIGNATURES: dict[str, list] = {
     "credit_layernorm_fwd_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_rmsnorm_fwd_bf16": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_rmsnorm_bwd_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _CFG],
+    "credit_rmsnorm_bwd_bf16_noalloc": [_P, _P, _P, _P, _P, _P, _I64, _I64, _CFG],
     "credit_softmax_fwd_f32": [_P, _P, _P, _P, _I64, _I64, _CFG],
     "credit_softmax_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_softmax_logits_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],

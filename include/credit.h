@@ -223,6 +223,23 @@ int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w, const uint16_t
                             const float* rstd, uint16_t* dx, float* dw, int64_t rows,
                             int64_t cols, const credit_cfg* cfg);
 
+/* The same backward, allocating nothing: no counterpart in the reference.
+ * It is for callers that cannot allocate device memory -- code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  The
+ * workspace (header, counters, exchange slots, dweight partials) lives in a
+ * fixed 40 MiB device array the library holds on every GPU it runs on until
+ * the process ends; shapes that need more (more than 40 MiB of workspace by
+ * credit_workspace_bytes, e.g. beyond 1024 x 262144 under AUTO) return
+ * CREDIT_ERR_WORKSPACE, and a cfg->workspace is refused (CREDIT_ERR_BAD_CONFIG).
+ * Outputs equal credit_rmsnorm_bwd_bf16's bit for bit.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other threads) race and must not be issued.  A split-barrier timeout is
+ * not reported (the array's watchdog word has no host-visible reader that
+ * allocates nothing); outputs are then wrong, as with the allocating call. */
+int credit_rmsnorm_bwd_bf16_noalloc(const uint16_t* x, const uint16_t* w, const uint16_t* dy,
+                                    const float* rstd, uint16_t* dx, float* dw, int64_t rows,
+                                    int64_t cols, const credit_cfg* cfg);
+
 /* ------------------------------------- C4: online softmax forward -------
  * m = max_j x, s = sum_j e^(x - m): p = e^(x - m)/s, rowmax = m (NaN-
  * propagating, bit-exact with torch.amax), lse = m + ln s; fp32.  The
