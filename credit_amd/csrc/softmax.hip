@@ -342,6 +342,131 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
   if (i + 2 < r1) step(b2, b0, b1, i + 2);
 }
 
+// Backward group kernel (SPLIT on rows wider than one workgroup): the row
+// pipeline of softmax_fwd_group_kernel with one exchanged value per row,
+// c = sum_j p*dy.  THREADS data lanes hold VPT f32x4 of p and of dy per row
+// in four rotating row buffers; one extra communication wave polls each
+// row's exchange into a 4-entry LDS ring.  At step i a data wave issues the
+// loads of row i+3, reduces row i+2 to its wave partial (the last wave in
+// adds the wave partials in wave order and publishes the member's), then
+// waits for row i's group total and writes dx = p * (dy - c): the exchange
+// round trip has two steps to complete and no workgroup barrier sits in the
+// loop.  Buffer resources cover the member's slice (0 for a row beyond the
+// group), so no load or store is under a branch.
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS + kWave)
+__attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
+    const float* __restrict__ p, const float* __restrict__ dy, float* __restrict__ dx, int rows,
+    int cols, int chunk, int members, int rows_per_group, SplitArgs sa) {
+  constexpr int NW = THREADS / kWave;
+  __shared__ double red[4][NW];  // wave partials of row k at [(k - r0) & 3]
+  __shared__ double ring[4];     // group totals of row k at [(k - r0) & 3]
+  __shared__ uint32_t arrivals[4];
+  __shared__ uint32_t ready;     // rows r0 .. r0 + ready - 1 have totals
+  const int tid = threadIdx.x;
+  if (tid < 4) arrivals[tid] = 0;
+  if (tid == 0) ready = 0;
+  const SplitGroup g = split_join(sa, members, 1);  // its barrier covers the stores above
+  const int r0 = g.group * rows_per_group;
+  if (r0 >= rows) return;  // padding group
+  const int r1 = r0 + rows_per_group < rows ? r0 + rows_per_group : rows;
+  const int nvec = cols >> 2;
+  const int v0 = g.member * chunk;
+  const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  const uint32_t slice_bytes = static_cast<uint32_t>(vlen) * 16u;
+
+  if (__builtin_amdgcn_readfirstlane(tid) >= THREADS) {
+    // ---- communication wave: every row's group total, in row order ----
+    for (int k = r0; k < r1; ++k) {
+      const uint32_t bits = split_poll(g, k - r0, 1);
+      const double dot = split_wave_sum(bits, members, 0);
+      if (tid == THREADS) {
+        ring[(k - r0) & 3] = dot;
+        __hip_atomic_store(&ready, static_cast<uint32_t>(k - r0 + 1), __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+    return;
+  }
+
+  // ---- data waves ----
+  const int wid = tid / kWave;
+  const bool lead = (tid & (kWave - 1)) == 0;
+  const uint32_t lane_off = static_cast<uint32_t>(tid) * 16u;
+  constexpr uint32_t kStride = THREADS * 16u;  // bytes between a lane's vectors
+  struct Row {
+    f32x4 p[VPT], d[VPT];
+  };
+  Row b0, b1, b2, b3;
+  auto load_row = [&](Row& b, int r) {
+    const bool live = r < r1;
+    const size_t off = static_cast<size_t>(live ? r : r0) * cols + 4 * static_cast<size_t>(v0);
+    const buffer_rsrc_t ps = make_rsrc(p + off, live ? slice_bytes : 0u);
+    const buffer_rsrc_t ds = make_rsrc(dy + off, live ? slice_bytes : 0u);
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) {
+      b.p[q] = slice_load(ps, lane_off + q * kStride);
+      b.d[q] = slice_load(ds, lane_off + q * kStride);
+    }
+  };
+  auto publish_row = [&](const Row& b, int k) {
+    float part = 0.0f;  // lanes beyond the slice hold zeros
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) part += dot4(b.p[q], b.d[q]);
+    const double v = wave_reduce_sum_f64(static_cast<double>(part));
+    const int slot = (k - r0) & 3;
+    if (lead) {
+      red[slot][wid] = v;
+      const uint32_t t = __hip_atomic_fetch_add(&arrivals[slot], 1u, __ATOMIC_ACQ_REL,
+                                                __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (t == NW - 1) {
+        double s = red[slot][0];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) s += red[slot][q];
+        arrivals[slot] = 0;
+        split_publish_at(g, k - r0, 0, s);
+      }
+    }
+  };
+  auto wait_total = [&](int i) {
+    const uint32_t need = static_cast<uint32_t>(i - r0 + 1);
+    while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < need)
+      __builtin_amdgcn_s_sleep(1);
+    return ring[(i - r0) & 3];
+  };
+  auto finish_row = [&](const Row& b, int r, double dot) {
+    const float c = static_cast<float>(dot);
+    const size_t off = static_cast<size_t>(r) * cols + 4 * static_cast<size_t>(v0);
+    const buffer_rsrc_t out = make_rsrc(dx + off, slice_bytes);
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) slice_store(out, lane_off + q * kStride, grad4(b.p[q], b.d[q], c));
+  };
+  // Step of row i: cur = row i, r2 = row i+2 (loaded), fut receives row i+3.
+  auto step = [&](Row& cur, Row& r2, Row& fut, int i) {
+    load_row(fut, i + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 2 < r1) publish_row(r2, i + 2);
+    finish_row(cur, i, wait_total(i));
+  };
+
+  load_row(b0, r0);
+  load_row(b1, r0 + 1);
+  load_row(b2, r0 + 2);
+  publish_row(b0, r0);
+  if (r0 + 1 < r1) publish_row(b1, r0 + 1);
+  // Rotate the four buffers through statically named registers.
+  int i = r0;
+  for (; i + 3 < r1; i += 4) {
+    step(b0, b2, b3, i);
+    step(b1, b3, b0, i + 1);
+    step(b2, b0, b1, i + 2);
+    step(b3, b1, b2, i + 3);
+  }
+  if (i < r1) step(b0, b2, b3, i);
+  if (i + 1 < r1) step(b1, b3, b0, i + 1);
+  if (i + 2 < r1) step(b2, b0, b1, i + 2);
+}
+
 // Streaming forward: online (max, sum) pass, then the output pass.  VEC:
 // f32x4 loads (cols % 4 == 0, 16-byte aligned rows); else element loads.
 template <int THREADS, bool VEC>
@@ -662,6 +787,16 @@ const Pick<BwdFn> kLogits[] = {
     {softmax_logits_bwd_slice_kernel<1024, 8>, 1024, 8192},
 };
 
+using BwdGroupFn = void (*)(const float*, const float*, float*, int, int, int, int, int,
+                            SplitArgs);
+const Pick<BwdGroupFn> kBwdGroup[] = {
+    {softmax_bwd_group_kernel<64, 4>, 64, 256},
+    {softmax_bwd_group_kernel<128, 4>, 128, 512},
+    {softmax_bwd_group_kernel<256, 4>, 256, 1024},
+    {softmax_bwd_group_kernel<512, 4>, 512, 2048},
+};
+constexpr int64_t kBwdGroupCapacity = 2048;
+
 constexpr int64_t kFwdCapacity = 16384;
 constexpr int64_t kBwdCapacity = 8192;
 // AUTO slices of the softmax backward on rows wider than one workgroup:
@@ -714,6 +849,33 @@ int resolve_fwd(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
   return resolve(cfg, cols, vec, kFwdCapacity, "softmax_fwd", plan);
 }
 
+// At most 32 members, as the forward: a 64-member launch of the 256-lane
+// kernel (two workgroups per CU, G*P equal to the resident count) ran into
+// the exchange watchdog at 9 x 262144; wider groups take the slice kernel.
+constexpr int kMaxBwdGroupMembers = 32;
+
+bool bwd_group_ok(const Plan& plan) {
+  return plan.variant == CREDIT_VARIANT_SPLIT && plan.members <= kMaxBwdGroupMembers &&
+         plan.chunk <= kBwdGroupCapacity;
+}
+
+// Backward plan.  AUTO on a row wider than one workgroup takes the group
+// kernel with the fewest members (a power of two) whose slices fit it, as
+// the forward does; rows wider than 32 such members cover take slices.
+int resolve_bwd(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
+  const int64_t nvec = cols / 4;
+  if (cfg_variant(cfg) == CREDIT_VARIANT_AUTO && vec && nvec > kBwdCapacity) {
+    int p = 2;
+    while (p * kBwdGroupCapacity < nvec) p *= 2;
+    if (p <= kMaxBwdGroupMembers) {
+      const int64_t chunk = (nvec + p - 1) / p;
+      *plan = Plan{CREDIT_VARIANT_SPLIT, static_cast<int>((nvec + chunk - 1) / chunk), chunk};
+      return CREDIT_OK;
+    }
+  }
+  return resolve(cfg, cols, vec, kBwdCapacity, "softmax_bwd", plan, kBwdAutoSlice);
+}
+
 // Rows per group and groups of a group-kernel launch: as many groups as
 // fit the device at once (a multiple of kDispensers), each taking a
 // contiguous block of rows.
@@ -741,16 +903,16 @@ size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int sp
   credit_cfg c{nullptr, variant, split, nullptr, 0};
   Plan p;
   const int64_t cap = op == CREDIT_OP_SOFTMAX_FWD ? kFwdCapacity : kBwdCapacity;
-  const int st = op == CREDIT_OP_SOFTMAX_FWD
-                     ? resolve_fwd(&c, cols, cols % 4 == 0, &p)
-                     : resolve(&c, cols, cols % 4 == 0, cap, "softmax", &p,
-                               op == CREDIT_OP_SOFTMAX_BWD ? kBwdAutoSlice : 0);
+  const int st = op == CREDIT_OP_SOFTMAX_FWD   ? resolve_fwd(&c, cols, cols % 4 == 0, &p)
+                 : op == CREDIT_OP_SOFTMAX_BWD ? resolve_bwd(&c, cols, cols % 4 == 0, &p)
+                                               : resolve(&c, cols, cols % 4 == 0, cap, "softmax", &p);
   if (st != CREDIT_OK) return 0;
   const int k = op == CREDIT_OP_SOFTMAX_BWD ? 1 : 2;
-  if (op == CREDIT_OP_SOFTMAX_FWD && fwd_group_ok(p)) {
+  if ((op == CREDIT_OP_SOFTMAX_FWD && fwd_group_ok(p)) ||
+      (op == CREDIT_OP_SOFTMAX_BWD && bwd_group_ok(p))) {
     int64_t groups = coresident_groups_bound(p.members, cu_count);
     if (groups > padded_groups(rows)) groups = padded_groups(rows);
-    return split_workspace_bytes(groups, p.members, 2, kGroupRing, 0);
+    return split_workspace_bytes(groups, p.members, k, kGroupRing, 0);
   }
   return slice_workspace(rows, p, k, cu_count);
 }
@@ -821,7 +983,7 @@ extern "C" int credit_softmax_bwd_f32(const float* p, const float* dy, float* dx
   if (rows == 0) return CREDIT_OK;
   const bool vec = vec_ok(cols, {p, dy, dx});
   Plan plan;
-  CREDIT_TRY(resolve(cfg, cols, vec, kBwdCapacity, "softmax_bwd", &plan, kBwdAutoSlice));
+  CREDIT_TRY(resolve_bwd(cfg, cols, vec, &plan));
   hipStream_t stream = cfg_stream(cfg);
   const int c = static_cast<int>(cols);
   const unsigned r = static_cast<unsigned>(rows);
@@ -831,6 +993,22 @@ extern "C" int credit_softmax_bwd_f32(const float* p, const float* dy, float* dx
     else
       softmax_bwd_read_kernel<256, false><<<r, 256, 0, stream>>>(p, dy, dx, c);
     return check_launch("softmax_bwd_read_kernel");
+  }
+  if (bwd_group_ok(plan)) {
+    const Pick<BwdGroupFn>* gk = pick_for(kBwdGroup, plan.chunk);
+    const int threads = gk->threads + kWave;
+    int rpg = 0;
+    int64_t groups = 0;
+    CREDIT_TRY(plan_row_groups(reinterpret_cast<const void*>(gk->fn), threads, plan.members, rows,
+                               &rpg, &groups, "softmax_bwd_group_kernel"));
+    SplitWorkspace ws;
+    CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 1, kGroupRing, 0, &ws));
+    const uint32_t total = static_cast<uint32_t>(groups * plan.members);
+    hipLaunchKernelGGL(gk->fn, dim3(total), dim3(threads), 0, stream, p, dy, dx,
+                       static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members, rpg,
+                       SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
+                                 next_split_epoch(static_cast<uint32_t>(rpg)), kGroupRing});
+    return check_launch("softmax_bwd_group_kernel");
   }
   const Pick<BwdFn>* pk = pick_for(kBwd, plan.chunk);
   return launch_slices<BwdFn>(

@@ -185,3 +185,17 @@ def test_softmax_fwd_full_config(gpu, c4_case, variant, split):
 def test_softmax_bwd_full_config(gpu, c4_case, variant, split):
     _, dy, _, _, _, p32, edx = c4_case
     np.testing.assert_allclose(bwd(p32, dy, variant, split, gpu), edx, **FP32)
+
+
+@pytest.mark.parametrize("shape,split", [((300, 65536), 32), ((77, 65540), 16), ((1030, 16384), 4),
+                                         ((9, 262144), 32), ((130, 24576), 3)])
+def test_softmax_bwd_group_kernel_rows(gpu, shape, split):
+    """The backward group kernel (SPLIT with slices of at most 2048 vectors):
+    ragged last members (65540 columns over 16), rows that end the four-row
+    rotation at each of its steps, more rows per group than the 16-row slot
+    ring, fewer rows than groups."""
+    print(f"softmax_bwd group split={split} shape={shape}", flush=True)
+    x, dy = SPEC.make_inputs(*shape, seed=shape[0] + split)
+    p32 = ref.softmax_fwd(x.numpy())[0].astype(np.float32)
+    dx = bwd(p32, dy, "split", split, gpu)
+    np.testing.assert_allclose(dx, ref.softmax_bwd(p32, dy.numpy()), **FP32)

@@ -45,7 +45,7 @@ def test_softmax_fwd_back_to_back(gpu, split):
     np.testing.assert_allclose(lse.cpu().numpy(), el, **FP32)
 
 
-@pytest.mark.parametrize("split", [2, 8])
+@pytest.mark.parametrize("split", [2, 8, 32])
 def test_softmax_bwd_back_to_back(gpu, split):
     x, dy = WORKLOADS["softmax_bwd"].make_inputs(2048, 16384, seed=4)
     p32 = ref.softmax_fwd(x.numpy())[0].astype(np.float32)
