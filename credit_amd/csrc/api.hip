@@ -307,6 +307,9 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
     case CREDIT_OP_RMSNORM_FWD:
       body = rmsnorm_fwd_workspace(rows, cols, variant, split, cus);
       break;
+    case CREDIT_OP_LAYERNORM_FWD:
+      body = layernorm_fwd_workspace(rows, cols, variant, split, cus);
+      break;
     case CREDIT_OP_RMSNORM_BWD:
       body = rmsnorm_bwd_workspace(rows, cols, variant, split, cus);
       break;

@@ -179,6 +179,7 @@ size_t layernorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int spli
 size_t softmax_workspace(int op, int64_t rows, int64_t cols, int variant, int split,
                          int cu_count);
 size_t rmsnorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split, int cu_count);
+size_t layernorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split, int cu_count);
 size_t rowwise_quant_workspace(int64_t rows, int64_t cols, int variant, int split, int cu_count);
 size_t lars_workspace(int64_t rows, int64_t cols, int variant, int split, int cu_count);
 size_t wvar_bwd_workspace(int64_t rows, int64_t cols, int variant, int split, int cu_count);

@@ -234,7 +234,97 @@ __global__ __launch_bounds__(THREADS) void layernorm_fwd_pipe_kernel(
   }
 }
 
-template <int THREADS>
+// ----------------------------------------------------------------- SPLIT --
+// P = members > 1 workgroups per row (one co-resident wave of ticketed
+// groups, each looping over rows group, group + G, ...), every member
+// holding a slice of VPT vectors per lane in registers.  Stage 1 exchanges
+// the slice's (sum x, sum x^2); every member forms the same totals in member
+// order, so every member takes the same branch: the one-pass variance when
+// mean^2 <= var/4, else a second stage exchanging the slice's sum of squared
+// deviations about the mean.  Partials travel as fp32 (the block sums before
+// them are fp64).  One HBM read of x, one write of y.
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void layernorm_fwd_slice_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
+    const uint16_t* __restrict__ beta, uint16_t* __restrict__ y,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int cols, int chunk,
+    int members, int rows, float eps, SplitArgs sa) {
+  constexpr int NW = THREADS / kWave;
+  constexpr uint32_t kOnes = 0x3f803f80u;  // bf16 (1.0, 1.0)
+  __shared__ double red[2][3][NW];
+  SplitGroup g = split_join(sa, members, 2);
+  const int step = static_cast<int>(sa.grid) / members;
+  const int nvec = cols >> 3;
+  const int v0 = g.member * chunk;
+  const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  const uint32_t slice_bytes = static_cast<uint32_t>(vlen) * 16u;
+  const uint32_t lane_off = threadIdx.x * 16u;
+  constexpr uint32_t kStride = THREADS * 16u;
+  const buffer_rsrc_t grs = make_rsrc(gamma + 8 * static_cast<size_t>(v0), slice_bytes);
+  const buffer_rsrc_t brs = make_rsrc(beta + 8 * static_cast<size_t>(v0), slice_bytes);
+  int parity = 0;
+  for (int row = g.group; row < rows; row += step, parity ^= 1) {
+    double (*slots)[NW] = red[parity];
+    const size_t off = static_cast<size_t>(row) * cols + 8 * static_cast<size_t>(v0);
+    const buffer_rsrc_t xrs = make_rsrc(x + off, slice_bytes);
+    u32x4 v[VPT];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) v[k] = buffer_load_nt(xrs, lane_off + k * kStride);
+    float s0 = 0.0f, s1 = 0.0f, q0 = 0.0f, q1 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      s0 = dot2_bf16(v[k].x, kOnes, s0);
+      q0 = dot2_bf16(v[k].x, v[k].x, q0);
+      s1 = dot2_bf16(v[k].y, kOnes, s1);
+      q1 = dot2_bf16(v[k].y, v[k].y, q1);
+      s0 = dot2_bf16(v[k].z, kOnes, s0);
+      q0 = dot2_bf16(v[k].z, v[k].z, q0);
+      s1 = dot2_bf16(v[k].w, kOnes, s1);
+      q1 = dot2_bf16(v[k].w, v[k].w, q1);
+    }
+    double sums[2] = {static_cast<double>(s0) + s1, static_cast<double>(q0) + q1};
+    block_reduce_sum_f64_multi<NW, 2>(sums, slots);
+    if (threadIdx.x == 0) {
+      split_publish(g, 0, sums[0]);
+      split_publish(g, 1, sums[1]);
+    }
+    split_exchange(g, 2);
+    const double mean = split_sum(g, 0) / cols;
+    const float mu = static_cast<float>(mean);
+    double var = split_sum(g, 1) / cols - mean * mean;
+    if (mean * mean > 0.25 * var) {
+      float q = 0.0f;
+#pragma unroll
+      for (int k = 0; k < VPT; ++k) {
+        const float d = sqdev8(v[k], mu);
+        q += lane_off + k * kStride < slice_bytes ? d : 0.0f;
+      }
+      const double sq = block_reduce_sum_f64<NW>(static_cast<double>(q), slots[2]);
+      if (threadIdx.x == 0) split_publish(g, 0, sq);
+      split_exchange(g, 1);
+      const double dmu = static_cast<double>(mu) - mean;
+      var = split_sum(g, 0) / cols - dmu * dmu;
+    }
+    const float rs = static_cast<float>(1.0 / __builtin_sqrt((var > 0.0 ? var : 0.0) + eps));
+    const buffer_rsrc_t yrs = make_rsrc(y + off, slice_bytes);
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const uint32_t o = lane_off + k * kStride;
+      buffer_store_nt(yrs, o, norm8(v[k], buffer_load(grs, o), buffer_load(brs, o), mu, rs));
+    }
+    if (g.member == 0 && threadIdx.x == 0) {
+      mean_out[row] = static_cast<float>(mean);
+      rstd_out[row] = rs;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ READ --
+// One workgroup per row streaming it three times (sum; squared deviations
+// about the mean; output).  VEC: 16-byte vectors of 8 bf16, four in flight
+// per lane (cols % 8 == 0, 16-byte aligned x, y, gamma, beta); else 2-byte
+// element loads for any width and alignment.
+template <int THREADS, bool VEC>
 __global__ __launch_bounds__(THREADS) void layernorm_fwd_read_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
     const uint16_t* __restrict__ beta, uint16_t* __restrict__ y,
@@ -246,23 +336,79 @@ __global__ __launch_bounds__(THREADS) void layernorm_fwd_read_kernel(
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const uint16_t* xr = x + static_cast<size_t>(row) * cols;
+  uint16_t* yr = y + static_cast<size_t>(row) * cols;
+  const int nvec = VEC ? cols >> 3 : 0;
+  const u32x4* xv = reinterpret_cast<const u32x4*>(xr);
   double s = 0.0;
-  for (int c = tid; c < cols; c += THREADS) s += bf16_to_f32(xr[c]);
+  if (VEC) {
+    constexpr uint32_t kOnes = 0x3f803f80u;
+    int i = tid;
+    for (; i + 3 * THREADS < nvec; i += 4 * THREADS) {
+      const u32x4 a = xv[i], b = xv[i + THREADS], c = xv[i + 2 * THREADS],
+                  d = xv[i + 3 * THREADS];
+      float t = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        t = dot2_bf16(a[e], kOnes, t);
+        t = dot2_bf16(b[e], kOnes, t);
+        t = dot2_bf16(c[e], kOnes, t);
+        t = dot2_bf16(d[e], kOnes, t);
+      }
+      s += t;
+    }
+    for (; i < nvec; i += THREADS) {
+      const u32x4 a = xv[i];
+      float t = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t = dot2_bf16(a[e], kOnes, t);
+      s += t;
+    }
+  } else {
+    for (int c = tid; c < cols; c += THREADS) s += bf16_to_f32(xr[c]);
+  }
   const double total = block_reduce_sum_f64<NW>(s, red0);
   const double mean = total / cols;
-  double q = 0.0;
-  for (int c = tid; c < cols; c += THREADS) {
-    const double d = bf16_to_f32(xr[c]) - mean;
-    q += d * d;
-  }
-  const double var = block_reduce_sum_f64<NW>(q, red1) / cols;
-  const float rs = static_cast<float>(1.0 / __builtin_sqrt(var + eps));
   const float mu = static_cast<float>(mean);
-  uint16_t* yr = y + static_cast<size_t>(row) * cols;
-  for (int c = tid; c < cols; c += THREADS) {
-    const float v = (bf16_to_f32(xr[c]) - mu) * rs * bf16_to_f32(gamma[c]) +
-                    bf16_to_f32(beta[c]);
-    yr[c] = f32_to_bf16(v);
+  double q = 0.0;
+  if (VEC) {
+    int i = tid;
+    for (; i + 3 * THREADS < nvec; i += 4 * THREADS)
+      q += static_cast<double>((sqdev8(xv[i], mu) + sqdev8(xv[i + THREADS], mu)) +
+                               (sqdev8(xv[i + 2 * THREADS], mu) + sqdev8(xv[i + 3 * THREADS], mu)));
+    for (; i < nvec; i += THREADS) q += static_cast<double>(sqdev8(xv[i], mu));
+  } else {
+    for (int c = tid; c < cols; c += THREADS) {
+      const double d = bf16_to_f32(xr[c]) - mean;
+      q += d * d;
+    }
+  }
+  // Deviations taken from the fp32 mean: remove (mu - mean)^2 (VEC), or
+  // exact fp64 deviations (scalar path).
+  const double dmu = VEC ? static_cast<double>(mu) - mean : 0.0;
+  const double var = block_reduce_sum_f64<NW>(q, red1) / cols - dmu * dmu;
+  const float rs = static_cast<float>(1.0 / __builtin_sqrt((var > 0.0 ? var : 0.0) + eps));
+  if (VEC) {
+    const u32x4* gv = reinterpret_cast<const u32x4*>(gamma);
+    const u32x4* bv = reinterpret_cast<const u32x4*>(beta);
+    u32x4* yv = reinterpret_cast<u32x4*>(yr);
+    int i = tid;
+    for (; i + 3 * THREADS < nvec; i += 4 * THREADS) {
+      const u32x4 a = load_nt(xv + i), b = load_nt(xv + i + THREADS),
+                  c = load_nt(xv + i + 2 * THREADS), d = load_nt(xv + i + 3 * THREADS);
+      store_nt(yv + i, norm8(a, gv[i], bv[i], mu, rs));
+      store_nt(yv + i + THREADS, norm8(b, gv[i + THREADS], bv[i + THREADS], mu, rs));
+      store_nt(yv + i + 2 * THREADS,
+               norm8(c, gv[i + 2 * THREADS], bv[i + 2 * THREADS], mu, rs));
+      store_nt(yv + i + 3 * THREADS,
+               norm8(d, gv[i + 3 * THREADS], bv[i + 3 * THREADS], mu, rs));
+    }
+    for (; i < nvec; i += THREADS) store_nt(yv + i, norm8(load_nt(xv + i), gv[i], bv[i], mu, rs));
+  } else {
+    for (int c = tid; c < cols; c += THREADS) {
+      const float v = (bf16_to_f32(xr[c]) - mu) * rs * bf16_to_f32(gamma[c]) +
+                      bf16_to_f32(beta[c]);
+      yr[c] = f32_to_bf16(v);
+    }
   }
   if (tid == 0) {
     mean_out[row] = mu;
@@ -291,7 +437,85 @@ const StagedPick kStaged[] = {
     {layernorm_fwd_staged_kernel<1024, 8>, 1024, 8192},
 };
 
+using SliceFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*,
+                        float*, int, int, int, int, float, SplitArgs);
+struct SlicePick {
+  SliceFn fn;
+  int threads;
+  int max_vec;
+};
+// Member slices of the SPLIT kernel, smallest footprint first.
+const SlicePick kSlice[] = {
+    {layernorm_fwd_slice_kernel<256, 4>, 256, 1024},
+    {layernorm_fwd_slice_kernel<256, 8>, 256, 2048},
+    {layernorm_fwd_slice_kernel<512, 8>, 512, 4096},
+    {layernorm_fwd_slice_kernel<1024, 8>, 1024, 8192},
+};
+constexpr int64_t kSliceCapacity = 8192;  // vectors per member
+constexpr int kMaxSliceMembers = kMaxExchangeValues / 2;  // (sum, sum of squares)
+
+struct Plan {
+  int variant;
+  int members;
+  int64_t chunk;
+};
+
+// READ: explicit, or shapes without the 16-byte vector layout.  STAGED /
+// pipeline: rows of at most 65536 columns.  SPLIT: explicit, or AUTO on a
+// wider row, with just enough members that every slice fits one workgroup.
+int resolve(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
+  const int variant = cfg_variant(cfg);
+  const int64_t nvec = cols / 8;
+  if (variant == CREDIT_VARIANT_READ || (!vec && variant == CREDIT_VARIANT_AUTO)) {
+    *plan = Plan{CREDIT_VARIANT_READ, 1, nvec};
+    return CREDIT_OK;
+  }
+  if (!vec)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "layernorm_fwd staged/split variants need cols %% 8 == 0 and 16-byte "
+                     "aligned buffers");
+  if (variant == CREDIT_VARIANT_STAGED || (variant == CREDIT_VARIANT_AUTO && nvec <= kSliceCapacity)) {
+    if (nvec > kSliceCapacity)
+      return set_error(CREDIT_ERR_UNSUPPORTED, "layernorm_fwd staged variant holds at most %lld columns",
+                       static_cast<long long>(kSliceCapacity * 8));
+    *plan = Plan{CREDIT_VARIANT_STAGED, 1, nvec};
+    return CREDIT_OK;
+  }
+  int p = variant == CREDIT_VARIANT_SPLIT ? cfg_split(cfg) : 0;
+  if (p == 0) p = static_cast<int>((nvec + kSliceCapacity - 1) / kSliceCapacity);
+  if (p < 2) p = 2;
+  if (p > nvec) p = static_cast<int>(nvec);
+  const int64_t chunk = (nvec + p - 1) / p;
+  const int members = static_cast<int>((nvec + chunk - 1) / chunk);
+  if (chunk > kSliceCapacity)
+    return set_error(CREDIT_ERR_UNSUPPORTED, "layernorm_fwd split %d leaves %lld vectors per member",
+                     p, static_cast<long long>(chunk));
+  if (members > kMaxSliceMembers)
+    return set_error(CREDIT_ERR_UNSUPPORTED, "layernorm_fwd split of %d members (at most %d)",
+                     members, kMaxSliceMembers);
+  *plan = members < 2 ? Plan{CREDIT_VARIANT_STAGED, 1, nvec} : Plan{CREDIT_VARIANT_SPLIT, members, chunk};
+  return CREDIT_OK;
+}
+
+const SlicePick* slice_for(int64_t chunk) {
+  for (const SlicePick& p : kSlice)
+    if (chunk <= p.max_vec) return &p;
+  return nullptr;
+}
+
 }  // namespace
+
+size_t layernorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split,
+                               int cu_count) {
+  credit_cfg c{nullptr, variant, split, nullptr, 0};
+  Plan p;
+  if (resolve(&c, cols, cols % 8 == 0, &p) != CREDIT_OK || p.variant != CREDIT_VARIANT_SPLIT)
+    return 0;
+  int64_t groups = coresident_groups_bound(p.members, cu_count);
+  if (groups > padded_groups(rows)) groups = padded_groups(rows);
+  return split_workspace_bytes(groups, p.members, 2, kSplitRing, 0);
+}
+
 }  // namespace credit
 
 using namespace credit;
@@ -313,10 +537,6 @@ extern "C" int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamm
   if (!(eps >= 0.0f))
     return set_error(CREDIT_ERR_BAD_CONFIG, "eps must be >= 0");
   if (rows == 0) return CREDIT_OK;
-  int variant = cfg_variant(cfg);
-  if (variant == CREDIT_VARIANT_SPLIT)
-    return set_error(CREDIT_ERR_UNSUPPORTED,
-                     "layernorm_fwd: split-row variant not built");
   hipStream_t stream = cfg_stream(cfg);
   const int c = static_cast<int>(cols);
   const bool vec_ok = (cols % 8 == 0) &&
@@ -325,28 +545,51 @@ extern "C" int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamm
                       reinterpret_cast<uintptr_t>(gamma) % 16 == 0 &&
                       reinterpret_cast<uintptr_t>(beta) % 16 == 0;
   const int64_t nvec = cols / 8;
-  const StagedPick* pick = nullptr;
-  if (vec_ok) {
-    for (const StagedPick& p : kStaged) {
-      if (nvec <= p.max_vec) {
-        pick = &p;
-        break;
-      }
-    }
-  }
-  if (variant == CREDIT_VARIANT_STAGED && pick == nullptr)
-    return set_error(CREDIT_ERR_UNSUPPORTED,
-                     "layernorm_fwd staged variant needs cols %% 8 == 0, "
-                     "16-byte aligned buffers and cols <= 65536");
-  if (variant == CREDIT_VARIANT_READ || pick == nullptr) {
-    layernorm_fwd_read_kernel<256><<<dim3(static_cast<unsigned>(rows)), dim3(256), 0,
-                                     stream>>>(x, gamma, beta, y, mean, rstd, c, eps);
+  Plan plan;
+  CREDIT_TRY(resolve(cfg, cols, vec_ok, &plan));
+  const dim3 row_grid(static_cast<unsigned>(rows));
+  if (plan.variant == CREDIT_VARIANT_READ) {
+    if (vec_ok)
+      layernorm_fwd_read_kernel<256, true><<<row_grid, dim3(256), 0, stream>>>(
+          x, gamma, beta, y, mean, rstd, c, eps);
+    else
+      layernorm_fwd_read_kernel<256, false><<<row_grid, dim3(256), 0, stream>>>(
+          x, gamma, beta, y, mean, rstd, c, eps);
     return check_launch("layernorm_fwd_read_kernel");
+  }
+  if (plan.variant == CREDIT_VARIANT_SPLIT) {
+    const SlicePick* sp = slice_for(plan.chunk);
+    int64_t groups = 0;
+    CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(sp->fn), sp->threads, 0,
+                                 plan.members, &groups));
+    if (groups == 0)
+      return set_error(CREDIT_ERR_UNSUPPORTED,
+                       "layernorm_fwd: %d groups of %d members do not fit the device",
+                       kDispensers, plan.members);
+    if (groups > padded_groups(rows)) groups = padded_groups(rows);
+    const int64_t per_group = (rows + groups - 1) / groups;
+    SplitWorkspace ws;
+    CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 2, kSplitRing, 0, &ws));
+    const uint32_t total = static_cast<uint32_t>(groups * plan.members);
+    // Two stages per row at most (the second only for offset rows).
+    const SplitArgs sa{ws.counters, ws.slots, ws.watchdog, total,
+                       next_split_epoch(static_cast<uint32_t>(2 * per_group)), kSplitRing};
+    hipLaunchKernelGGL(sp->fn, dim3(total), dim3(sp->threads), 0, stream, x, gamma, beta, y,
+                       mean, rstd, c, static_cast<int>(plan.chunk), plan.members,
+                       static_cast<int>(rows), eps, sa);
+    return check_launch("layernorm_fwd_slice_kernel");
+  }
+  const StagedPick* pick = nullptr;
+  for (const StagedPick& p : kStaged) {
+    if (nvec <= p.max_vec) {
+      pick = &p;
+      break;
+    }
   }
   const DeviceProps* props = nullptr;
   CREDIT_TRY(current_device_props(&props));
   // AUTO: the pipeline once every CU has at least two rows to overlap.
-  if (variant == CREDIT_VARIANT_AUTO && nvec > kPipeVec / 2 && nvec <= kPipeVec &&
+  if (cfg_variant(cfg) == CREDIT_VARIANT_AUTO && nvec > kPipeVec / 2 && nvec <= kPipeVec &&
       rows >= 2 * static_cast<int64_t>(props->cu_count) &&
       rows <= INT32_MAX - 2 * static_cast<int64_t>(props->cu_count)) {  // row + 2G fits an int
     static const hipError_t attr = hipFuncSetAttribute(
@@ -358,7 +601,7 @@ extern "C" int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamm
                        stream, x, gamma, beta, y, mean, rstd, static_cast<int>(rows), c, eps);
     return check_launch("layernorm_fwd_pipe_kernel");
   }
-  hipLaunchKernelGGL(pick->fn, dim3(static_cast<unsigned>(rows)), dim3(pick->threads),
-                     0, stream, x, gamma, beta, y, mean, rstd, c, eps);
+  hipLaunchKernelGGL(pick->fn, row_grid, dim3(pick->threads), 0, stream, x, gamma, beta, y, mean,
+                     rstd, c, eps);
   return check_launch("layernorm_fwd_staged_kernel");
 }

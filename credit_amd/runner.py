@@ -50,6 +50,7 @@ from .workloads import WORKLOADS, WorkloadSpec
 # Workloads with a split variant (the cost model's domain).
 SWEEP_WORKLOADS = (
     "row_sum_max",
+    "layernorm_fwd",
     "rmsnorm_fwd",
     "rmsnorm_bwd",
     "softmax_fwd",
@@ -130,7 +131,8 @@ class RunConfig:
 
 
 def sweep_rows(spec: WorkloadSpec, cols: int, tensor_bytes: int) -> int:
-    elem = 2 if spec.name in ("rmsnorm_fwd", "rmsnorm_bwd", "layernorm_backward_bf16") else 4
+    elem = 2 if spec.name in ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd",
+                              "layernorm_backward_bf16") else 4
     return int(max(tensor_bytes // (cols * elem), 8))
 
 

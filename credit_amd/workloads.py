@@ -224,10 +224,10 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         output_names=("y", "mean", "rstd"),
         algorithmic_bytes=lambda r, c: 2 * r * c + 2 * r * c + 4 * c + 8 * r,
         tolerances=(BF16_TOL, FP32_TOL, FP32_TOL),
-        modeled_bytes_per_element=8.0,  # read x twice (stats, output) + write y
+        modeled_bytes_per_element=8.0,  # READ: x three times (sum, deviations, output) + y
         reread_bytes_per_element=4.0,   # the second and third reads of x
         staged_bytes_per_element=2,
-        reductions_per_stage=(1, 1),
+        reductions_per_stage=(2,),      # SPLIT: one stage of (sum, sum of squares)
         staged_max_cols=65536,
         stream_mix=(1, 1),
     ),

@@ -41,8 +41,9 @@ def test_layernorm_fwd_shapes(gpu, variant, shape):
 
 @pytest.mark.parametrize("shape", [(5, 1004), (3, 3), (2, 140000), (2, 131072)])
 def test_layernorm_fwd_read_only_shapes(gpu, shape):
-    """Shapes the staged layout does not cover fall back to the READ kernel
-    under AUTO and are rejected under an explicit STAGED request."""
+    """Shapes the staged layout does not cover (cols % 8 != 0: the READ
+    kernel's element loads; rows wider than 65536 columns: SPLIT) run under
+    AUTO and are rejected under an explicit STAGED request."""
     x, g, b = SPEC.make_inputs(*shape, seed=4)
     check(x, g, b, *run(x, g, b, "auto", gpu))
     with pytest.raises(hip_lib.CreditError) as err:
@@ -119,3 +120,54 @@ def test_layernorm_fwd_offset_rows_take_the_two_pass_statistics(gpu, shape):
     for variant in ("auto", "staged"):
         print(f"layernorm_fwd offset rows {variant} shape={shape}", flush=True)
         check(x, g, b, *run(x, g, b, variant, gpu))
+
+
+@pytest.mark.parametrize("shape,variant,split", [((2, 140000), "auto", 0), ((256, 262144), "auto", 0),
+                                                 ((5, 131072), "split", 2), ((5, 131072), "split", 3),
+                                                 ((9, 65536), "split", 8), ((300, 100000), "auto", 0),
+                                                 ((3, 140000), "read", 0)])
+def test_layernorm_fwd_wide_rows(gpu, shape, variant, split):
+    """Rows wider than one workgroup holds: the SPLIT kernel (members
+    exchanging (sum, sum of squares); ragged last members at 140000 and
+    100000 columns; more rows than resident groups at 300 x 100000) and the
+    vectorised READ kernel, against the float64 two-pass oracle."""
+    print(f"layernorm_fwd wide {variant} P={split} shape={shape}", flush=True)
+    x, g, b = SPEC.make_inputs(*shape, seed=shape[0] + split)
+    y, mean, rstd = run_split(x, g, b, variant, split, gpu)
+    check(x, g, b, y, mean, rstd)
+
+
+def test_layernorm_fwd_split_offset_and_constant_rows(gpu):
+    """The SPLIT kernel's second exchange stage (squared deviations) for
+    rows with a large offset, and constant rows, mixed with one-pass rows."""
+    x, g, b = SPEC.make_inputs(40, 139264, seed=5)
+    xf = x.float()
+    xf[0::3] = xf[0::3] * 0.01 + 300.0
+    xf[1] = 2.25
+    x = xf.bfloat16()
+    for variant, split in (("auto", 0), ("split", 5)):
+        print(f"layernorm_fwd offset rows {variant} P={split}", flush=True)
+        y, mean, rstd = run_split(x, g, b, variant, split, gpu)
+        check(x, g, b, y, mean, rstd)
+        assert mean[1] == 2.25
+        np.testing.assert_allclose(y[1], b.float().numpy(), atol=1e-6)
+
+
+def test_layernorm_fwd_split_rejections(gpu):
+    x, g, b = SPEC.make_inputs(2, 65536, seed=1)
+    with pytest.raises(hip_lib.CreditError) as err:
+        run_split(x, g, b, "split", 33, gpu)  # 33 members exchange 66 partials
+    assert err.value.status == -4
+    x, g, b = SPEC.make_inputs(2, 65544 + 4, seed=1)  # cols % 8 != 0
+    with pytest.raises(hip_lib.CreditError) as err:
+        run_split(x, g, b, "split", 2, gpu)
+    assert err.value.status == -4
+
+
+def run_split(x, g, b, variant, split, gpu):
+    ins = tuple(t.to(gpu) for t in (x, g, b))
+    y, mean, rstd = hip_lib.allocate_outputs("layernorm_fwd", ins)
+    hip_lib.layernorm_fwd(*ins, y, mean, rstd, EPS, hip_lib.make_cfg(variant, split))
+    torch.cuda.synchronize()
+    hip_lib.check_watchdog()
+    return y.float().cpu().numpy(), mean.cpu().numpy(), rstd.cpu().numpy()
