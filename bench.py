@@ -64,6 +64,8 @@ CALL_KERNELS = {
     "rmsnorm_fwd": ("rmsnorm.hip", ["rmsnorm_fwd_slice_kernel<1024, 8>"]),
     "rmsnorm_bwd": ("rmsnorm.hip", ["rmsnorm_bwd_group_kernel<512, 2>",
                                     "rmsnorm_dw_reduce_kernel"]),
+    "rmsnorm_fwd_bwd": ("rmsnorm.hip", ["rmsnorm_fused_group_kernel<512, 2>",
+                                        "rmsnorm_dw_reduce_kernel"]),
     "softmax_fwd": ("softmax.hip", ["softmax_fwd_group_kernel<512, 8>"]),
     "softmax_bwd": ("softmax.hip", ["softmax_bwd_slice_kernel<512, 8>"]),
     "softmax_logits_backward": ("softmax.hip", ["softmax_logits_bwd_slice_kernel<1024, 8>"]),

@@ -313,6 +313,9 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
     case CREDIT_OP_RMSNORM_BWD:
       body = rmsnorm_bwd_workspace(rows, cols, variant, split, cus);
       break;
+    case CREDIT_OP_RMSNORM_FWD_BWD:
+      body = rmsnorm_fused_workspace(rows, cols, variant, split, cus);
+      break;
     case CREDIT_OP_LAYERNORM_BWD:
       body = layernorm_bwd_workspace(rows, cols, variant, split, 4, cus);
       break;

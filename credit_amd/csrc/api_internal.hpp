@@ -186,6 +186,8 @@ size_t wvar_bwd_workspace(int64_t rows, int64_t cols, int variant, int split, in
 size_t pearson_bwd_workspace(int64_t rows, int64_t cols, int variant, int split, int cu_count);
 size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
                              int cu_count);
+size_t rmsnorm_fused_workspace(int64_t rows, int64_t cols, int variant, int split,
+                               int cu_count);
 
 // CU count of the current device, or 256 (MI355X) when none is visible.
 int cu_count_or_default();

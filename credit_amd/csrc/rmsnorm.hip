@@ -37,10 +37,10 @@ namespace credit {
 namespace {
 
 // ------------------------------------------------------- bf16x8 helpers --
+// Sum of squares of 8 packed bf16: four v_dot2_f32_bf16 (products exact in
+// fp32).
 __device__ __forceinline__ float sumsq8(u32x4 v) {
-  const float a = bf16_lo(v.x), b = bf16_hi(v.x), c = bf16_lo(v.y), d = bf16_hi(v.y);
-  const float e = bf16_lo(v.z), f = bf16_hi(v.z), g = bf16_lo(v.w), h = bf16_hi(v.w);
-  return ((a * a + b * b) + (c * c + d * d)) + ((e * e + f * f) + (g * g + h * h));
+  return dot2_bf16(v.w, v.w, dot2_bf16(v.z, v.z, dot2_bf16(v.y, v.y, dot2_bf16(v.x, v.x, 0.0f))));
 }
 
 __device__ __forceinline__ uint32_t scale2(uint32_t xv, uint32_t wv, float rs) {
@@ -336,24 +336,28 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
 // and stores in order; a load under a branch makes the count
 // path-dependent and the wait after the join a full drain).  dw
 // accumulators: fp64 in LDS, [8*VPT][THREADS], one owner lane each.
-template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS + kWave)
-__attribute__((amdgpu_waves_per_eu(VPT == 1 ? 4 : 3, 8))) void rmsnorm_bwd_group_kernel(
+// The group pipeline of the backward and of the fused forward + backward.
+// FUSED: the row's sum of squares travels in the same exchange as
+// sum(dy*w*x) (two values per member), rstd comes from it instead of the
+// forward, and y = x * rstd * w is written beside dx.
+template <int THREADS, int VPT, bool FUSED>
+__device__ __forceinline__ void rmsnorm_group_body(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    const uint16_t* __restrict__ dy, const float* __restrict__ rstd, uint16_t* __restrict__ dx,
-    double* __restrict__ dw_part, int rows, int cols, int chunk, int members,
-    int rows_per_group, SplitArgs sa) {
+    const uint16_t* __restrict__ dy, const float* __restrict__ rstd, float* __restrict__ rstd_out,
+    uint16_t* __restrict__ y, uint16_t* __restrict__ dx, double* __restrict__ dw_part, int rows,
+    int cols, int chunk, int members, int rows_per_group, float eps, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
+  constexpr int K = FUSED ? 2 : 1;  // values per member per row
   constexpr int kSlots = 8 * VPT;
   extern __shared__ double dw_lds[];  // [kSlots][THREADS]
-  __shared__ double red[4][NW];       // wave partials of row k at [(k - r0) & 3]
-  __shared__ double ring[4];          // group totals of row k at [(k - r0) & 3]
+  __shared__ double red[4][K][NW];    // wave partials of row k at [(k - r0) & 3]
+  __shared__ double ring[4][K];       // group totals of row k at [(k - r0) & 3]
   __shared__ uint32_t arrivals[4];
   __shared__ uint32_t ready;          // rows r0 .. r0 + ready - 1 have totals
   const int tid = threadIdx.x;
   if (tid < 4) arrivals[tid] = 0;
   if (tid == 0) ready = 0;
-  const SplitGroup g = split_join(sa, members, 1);  // its barrier covers the stores above
+  const SplitGroup g = split_join(sa, members, K);  // its barrier covers the stores above
   const int r0 = g.group * rows_per_group;
   if (r0 >= rows) return;  // padding group
   const int r1 = r0 + rows_per_group < rows ? r0 + rows_per_group : rows;
@@ -365,10 +369,12 @@ __attribute__((amdgpu_waves_per_eu(VPT == 1 ? 4 : 3, 8))) void rmsnorm_bwd_group
   if (__builtin_amdgcn_readfirstlane(tid) >= THREADS) {
     // ---- communication wave: poll every row's exchange in order ----
     for (int k = r0; k < r1; ++k) {
-      const uint32_t bits = split_poll(g, k - r0, 1);
+      const uint32_t bits = split_poll(g, k - r0, K);
       const double dot = split_wave_sum(bits, members, 0);
+      const double ssq = FUSED ? split_wave_sum(bits, members, 1) : 0.0;
       if (tid == THREADS) {
-        ring[(k - r0) & 3] = dot;
+        ring[(k - r0) & 3][0] = dot;
+        if (FUSED) ring[(k - r0) & 3][K - 1] = ssq;
         __hip_atomic_store(&ready, static_cast<uint32_t>(k - r0 + 1), __ATOMIC_RELEASE,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
       }
@@ -404,21 +410,29 @@ __attribute__((amdgpu_waves_per_eu(VPT == 1 ? 4 : 3, 8))) void rmsnorm_bwd_group
   for (int q = 0; q < VPT; ++q) wk[q] = buffer_load(wrs, lane_off + q * kStride);
   // Reduce row k to a wave partial; the last wave in publishes the member's.
   auto publish_row = [&](const Row& b, int k) {
-    float part = 0.0f;
+    float part = 0.0f, ss = 0.0f;
 #pragma unroll
-    for (int q = 0; q < VPT; ++q) part += gx8(b.x[q], b.d[q], wk[q]);
+    for (int q = 0; q < VPT; ++q) {
+      part += gx8(b.x[q], b.d[q], wk[q]);
+      if (FUSED) ss += sumsq8(b.x[q]);
+    }
     const double v = wave_reduce_sum_f64(static_cast<double>(part));
+    const double vs = FUSED ? wave_reduce_sum_f64(static_cast<double>(ss)) : 0.0;
     const int slot = (k - r0) & 3;
     if (lead) {
-      red[slot][wid] = v;
+      red[slot][0][wid] = v;
+      if (FUSED) red[slot][K - 1][wid] = vs;
       const uint32_t t = __hip_atomic_fetch_add(&arrivals[slot], 1u, __ATOMIC_ACQ_REL,
                                                 __HIP_MEMORY_SCOPE_WORKGROUP);
       if (t == NW - 1) {
-        double s = red[slot][0];
 #pragma unroll
-        for (int q = 1; q < NW; ++q) s += red[slot][q];
+        for (int e = 0; e < K; ++e) {
+          double s = red[slot][e][0];
+#pragma unroll
+          for (int q = 1; q < NW; ++q) s += red[slot][e][q];
+          split_publish_at(g, k - r0, e, s);
+        }
         arrivals[slot] = 0;
-        split_publish_at(g, k - r0, 0, s);
       }
     }
   };
@@ -426,16 +440,30 @@ __attribute__((amdgpu_waves_per_eu(VPT == 1 ? 4 : 3, 8))) void rmsnorm_bwd_group
     const uint32_t need = static_cast<uint32_t>(i - r0 + 1);
     while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < need)
       __builtin_amdgcn_s_sleep(1);
-    return ring[(i - r0) & 3];
+    return (i - r0) & 3;
   };
   const double inv_cols = 1.0 / cols;
-  auto finish_row = [&](const Row& b, int r, double dot) {
-    const float rs = rstd[r];
+  auto finish_row = [&](const Row& b, int r, int slot) {
+    const double dot = ring[slot][0];
+    float rs;
+    if (FUSED) {
+      const double ms = ring[slot][K - 1] / cols;
+      rs = static_cast<float>(1.0 / __builtin_sqrt(ms + eps));
+    } else {
+      rs = rstd[r];
+    }
     // c = mean(g * xhat) = rs * sum(dy*w*x) / cols
     const float c = static_cast<float>(dot * (rs * inv_cols));
     const double rsd = static_cast<double>(rs);
     const size_t off = static_cast<size_t>(r) * cols + 8 * static_cast<size_t>(v0);
     const buffer_rsrc_t out = make_rsrc(dx + off, slice_bytes);
+    if (FUSED) {
+      const buffer_rsrc_t yrs = make_rsrc(y + off, slice_bytes);
+#pragma unroll
+      for (int q = 0; q < VPT; ++q)
+        buffer_store_nt(yrs, lane_off + q * kStride, scale8(b.x[q], wk[q], rs));
+      if (g.member == 0 && tid == 0) rstd_out[r] = rs;
+    }
 #pragma unroll
     for (int q = 0; q < VPT; ++q) {
       buffer_store_nt(out, lane_off + q * kStride, dx8(b.x[q], b.d[q], wk[q], rs, c));
@@ -489,6 +517,29 @@ __attribute__((amdgpu_waves_per_eu(VPT == 1 ? 4 : 3, 8))) void rmsnorm_bwd_group
       buffer_store(prs, (lane_off + v * kStride) * 4u + 16u * q,
                    __builtin_bit_cast(u32x4, f64x2{dw_lds[(v * 8 + 2 * q) * THREADS + tid],
                                                    dw_lds[(v * 8 + 2 * q + 1) * THREADS + tid]}));
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS + kWave)
+__attribute__((amdgpu_waves_per_eu(VPT == 1 ? 4 : 3, 8))) void rmsnorm_bwd_group_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ dy, const float* __restrict__ rstd, uint16_t* __restrict__ dx,
+    double* __restrict__ dw_part, int rows, int cols, int chunk, int members,
+    int rows_per_group, SplitArgs sa) {
+  rmsnorm_group_body<THREADS, VPT, false>(x, w, dy, rstd, nullptr, nullptr, dx, dw_part, rows,
+                                          cols, chunk, members, rows_per_group, 0.0f, sa);
+}
+
+// Forward and backward in one pass: x, dy, w in; y, rstd, dx, dweight out.
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS + kWave)
+__attribute__((amdgpu_waves_per_eu(VPT == 1 ? 4 : 3, 8))) void rmsnorm_fused_group_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ dy, float* __restrict__ rstd, uint16_t* __restrict__ y,
+    uint16_t* __restrict__ dx, double* __restrict__ dw_part, int rows, int cols, int chunk,
+    int members, int rows_per_group, float eps, SplitArgs sa) {
+  rmsnorm_group_body<THREADS, VPT, true>(x, w, dy, nullptr, rstd, y, dx, dw_part, rows, cols,
+                                         chunk, members, rows_per_group, eps, sa);
 }
 
 // READ variant pre-pass: rowdot[r] = sum_j dy*w*x over the row, streamed.
@@ -596,6 +647,26 @@ const BwdGroupPick kBwdGroup[] = {
     {rmsnorm_bwd_group_kernel<960, 1>, 960, 960, 1},
     {rmsnorm_bwd_group_kernel<512, 2>, 512, 1024, 1},
 };
+// Fused forward + backward: the same shapes, the sum of squares riding in
+// the same exchange (two values per member, so at most 32 members).
+using FusedGroupFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, float*,
+                              uint16_t*, uint16_t*, double*, int, int, int, int, int, float,
+                              SplitArgs);
+struct FusedGroupPick {
+  FusedGroupFn fn;
+  int threads;
+  int capacity;
+  int lds_bytes() const { return capacity * 8 * static_cast<int>(sizeof(double)); }
+};
+const FusedGroupPick kFusedGroup[] = {
+    {rmsnorm_fused_group_kernel<64, 1>, 64, 64},
+    {rmsnorm_fused_group_kernel<128, 1>, 128, 128},
+    {rmsnorm_fused_group_kernel<192, 1>, 192, 192},
+    {rmsnorm_fused_group_kernel<448, 1>, 448, 448},
+    {rmsnorm_fused_group_kernel<960, 1>, 960, 960},
+    {rmsnorm_fused_group_kernel<512, 2>, 512, 1024},
+};
+constexpr int kMaxFusedMembers = kMaxExchangeValues / 2;
 constexpr int kFwdMaxCapacity = 8192;
 constexpr int kBwdMaxCapacity = 1024;      // slice kernels (STAGED, READ tiles)
 constexpr int kBwdGroupCapacity = 1024;    // group kernel (SPLIT): largest member slice
@@ -790,6 +861,24 @@ size_t rmsnorm_fwd_workspace(int64_t rows, int64_t cols, int variant, int split,
   return split_workspace_bytes(groups, p.members, 1, kSplitRing, 0);
 }
 
+size_t rmsnorm_fused_workspace(int64_t rows, int64_t cols, int variant, int split,
+                               int cu_count) {
+  // Without a device query the group count is bounded by the resident
+  // workgroups of the widest pick (one per CU): every shape's figure is an
+  // upper bound of what the call acquires.
+  if (cols % 8 != 0 || rows <= 0) return 0;
+  const int64_t nvec = cols / 8;
+  const int need = static_cast<int>((nvec + kBwdGroupCapacity - 1) / kBwdGroupCapacity);
+  int p = split > 0 ? split : 1;
+  while (split == 0 && p < need) p *= 2;
+  if (p < need || p > kMaxFusedMembers) return 0;
+  (void)variant;
+  int64_t groups = coresident_groups_bound(p, cu_count);
+  if (groups > padded_groups(rows)) groups = padded_groups(rows);
+  return split_workspace_bytes(groups, p, 2, kBwdRing,
+                               align_up(static_cast<size_t>(groups) * cols * sizeof(double), 256));
+}
+
 size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
                              int cu_count) {
   credit_cfg c{nullptr, variant, split, nullptr, 0};
@@ -797,6 +886,58 @@ size_t rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int split,
   if (resolve_bwd(&c, rows, cols, cols % 8 == 0, cu_count, &p) != CREDIT_OK) return 0;
   return split_workspace_bytes(padded_groups(p.groups), p.members, 1, bwd_ring(p),
                                bwd_extra_bytes(p, rows, cols));
+}
+
+// Fused plan: the group kernel with the fewest members (a power of two, or
+// cfg->split) whose slices hold at most kBwdGroupCapacity vectors; one
+// member when the row fits one workgroup.
+struct FusedPlan {
+  int members;
+  int64_t chunk;
+  int rows_per_group;
+  int64_t groups;       // groups with rows
+  int64_t grid_groups;  // padded to a multiple of kDispensers
+};
+
+int resolve_fused(const credit_cfg* cfg, int64_t rows, int64_t cols, int cu_count,
+                  const FusedGroupPick** pick, FusedPlan* plan) {
+  const int64_t nvec = cols / 8;
+  const int need = static_cast<int>((nvec + kBwdGroupCapacity - 1) / kBwdGroupCapacity);
+  int p = cfg_split(cfg);
+  if (p == 0) {
+    p = 1;
+    while (p < need) p *= 2;
+  }
+  if (p < need)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "rmsnorm_fwd_bwd split %d leaves more than %d vectors per member", p,
+                     kBwdGroupCapacity);
+  if (p > nvec) p = static_cast<int>(nvec);
+  const Plan sp = plan_split(nvec, p);
+  if (sp.members > kMaxFusedMembers)
+    return set_error(CREDIT_ERR_UNSUPPORTED, "rmsnorm_fwd_bwd: %d members (at most %d)",
+                     sp.members, kMaxFusedMembers);
+  *pick = pick_for(kFusedGroup, sp.chunk);
+  int64_t fit = 0;
+  CREDIT_TRY(credit::coresident_groups(reinterpret_cast<const void*>((*pick)->fn),
+                                       (*pick)->threads + kWave, (*pick)->lds_bytes(),
+                                       sp.members, &fit));
+  (void)cu_count;
+  if (fit == 0)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "rmsnorm_fwd_bwd: %d groups of %d members do not fit the device at once",
+                     kDispensers, sp.members);
+  const int64_t g = fit < padded_groups(rows) ? fit : padded_groups(rows);
+  const int64_t r = (rows + g - 1) / g;
+  if (r > (int64_t{1} << 30))
+    return set_error(CREDIT_ERR_BAD_SHAPE, "rmsnorm_fwd_bwd: %lld rows per group",
+                     static_cast<long long>(r));
+  plan->members = sp.members;
+  plan->chunk = sp.chunk;
+  plan->rows_per_group = static_cast<int>(r);
+  plan->groups = (rows + r - 1) / r;
+  plan->grid_groups = padded_groups(plan->groups);
+  return CREDIT_OK;
 }
 
 // ----------------------------------------------- allocation-free variant --
@@ -1000,4 +1141,67 @@ extern "C" int credit_rmsnorm_bwd_bf16_noalloc(const uint16_t* x, const uint16_t
   c.workspace = base;
   c.workspace_bytes = kNoAllocScratchBytes;
   return credit_rmsnorm_bwd_bf16(x, w, dy, rstd, dx, dw, rows, cols, &c);
+}
+
+extern "C" int credit_rmsnorm_fwd_bwd_bf16(const uint16_t* x, const uint16_t* w,
+                                           const uint16_t* dy, uint16_t* y, float* rstd,
+                                           uint16_t* dx, float* dw, int64_t rows, int64_t cols,
+                                           float eps, const credit_cfg* cfg) {
+  CREDIT_TRY(check_row_ptr(x, "x", rows));
+  CREDIT_TRY(check_ptr(w, "w"));
+  CREDIT_TRY(check_row_ptr(dy, "dy", rows));
+  CREDIT_TRY(check_row_ptr(y, "y", rows));
+  CREDIT_TRY(check_row_ptr(rstd, "rstd", rows));
+  CREDIT_TRY(check_row_ptr(dx, "dx", rows));
+  CREDIT_TRY(check_ptr(dw, "dw"));
+  CREDIT_TRY(check_shape(rows, cols, int64_t{1} << 30));
+  CREDIT_TRY(check_cfg(cfg));
+  if (!(eps >= 0.0f)) return set_error(CREDIT_ERR_BAD_CONFIG, "eps must be >= 0");
+  if (rows > (int64_t{1} << 24))
+    return set_error(CREDIT_ERR_BAD_SHAPE, "rmsnorm_fwd_bwd supports at most 2^24 rows");
+  const int variant = cfg_variant(cfg);
+  if (variant == CREDIT_VARIANT_STAGED)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "rmsnorm_fwd_bwd: STAGED is not a variant of the fused call (AUTO, SPLIT, "
+                     "or READ = the forward then the backward)");
+  const bool vec = vec_ok(cols, {x, w, dy, y, dx, dw});
+  if (variant == CREDIT_VARIANT_READ || (!vec && variant == CREDIT_VARIANT_AUTO) || rows == 0) {
+    // The two passes: the forward's rstd feeds the backward.
+    credit_cfg c = cfg != nullptr ? *cfg : credit_cfg{nullptr, 0, 0, nullptr, 0};
+    c.variant = CREDIT_VARIANT_AUTO;
+    c.split = 0;
+    if (rows > 0) CREDIT_TRY(credit_rmsnorm_fwd_bf16(x, w, y, rstd, rows, cols, eps, &c));
+    if (variant == CREDIT_VARIANT_READ) c.variant = CREDIT_VARIANT_READ;
+    return credit_rmsnorm_bwd_bf16(x, w, dy, rstd, dx, dw, rows, cols, &c);
+  }
+  if (!vec)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "rmsnorm_fwd_bwd SPLIT needs cols %% 8 == 0 and 16-byte aligned buffers");
+  const DeviceProps* props = nullptr;
+  CREDIT_TRY(current_device_props(&props));
+  const FusedGroupPick* pick = nullptr;
+  FusedPlan plan;
+  CREDIT_TRY(resolve_fused(cfg, rows, cols, props->cu_count, &pick, &plan));
+  if (plan.grid_groups > kMaxGroupsPerLaunch)
+    return set_error(CREDIT_ERR_BAD_SHAPE, "rmsnorm_fwd_bwd: %lld row groups exceed %d",
+                     static_cast<long long>(plan.groups), kMaxGroupsPerLaunch);
+  SplitWorkspace ws;
+  CREDIT_TRY(acquire_split_workspace(
+      cfg, plan.grid_groups, plan.members, 2, kBwdRing,
+      align_up(static_cast<size_t>(plan.groups) * cols * sizeof(double), 256), &ws));
+  double* dw_part = reinterpret_cast<double*>(ws.extra);
+  hipStream_t stream = cfg_stream(cfg);
+  const int c = static_cast<int>(cols);
+  const uint32_t total = static_cast<uint32_t>(plan.grid_groups * plan.members);
+  hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads + kWave), pick->lds_bytes(),
+                     stream, x, w, dy, rstd, y, dx, dw_part, static_cast<int>(rows), c,
+                     static_cast<int>(plan.chunk), plan.members, plan.rows_per_group, eps,
+                     SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
+                               next_split_epoch(static_cast<uint32_t>(plan.rows_per_group)),
+                               kBwdRing});
+  CREDIT_TRY(check_launch("rmsnorm_fused_group_kernel"));
+  const unsigned reduce_blocks = static_cast<unsigned>((cols / 2 + 255) / 256);
+  rmsnorm_dw_reduce_kernel<<<dim3(reduce_blocks), dim3(256), 0, stream>>>(
+      dw_part, dw, static_cast<int>(plan.groups), c);
+  return check_launch("rmsnorm_dw_reduce_kernel");
 }

@@ -57,6 +57,7 @@ OPS = {
     "lars_momentum": 12,
     "weighted_var_backward": 13,
     "pearson_backward": 14,
+    "rmsnorm_fwd_bwd": 15,
 }
 
 
@@ -118,6 +119,7 @@ SIGNATURES: dict[str, list] = {
     "credit_rmsnorm_fwd_bf16": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_rmsnorm_bwd_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _CFG],
     "credit_rmsnorm_bwd_bf16_noalloc": [_P, _P, _P, _P, _P, _P, _I64, _I64, _CFG],
+    "credit_rmsnorm_fwd_bwd_bf16": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_softmax_fwd_f32": [_P, _P, _P, _P, _I64, _I64, _CFG],
     "credit_softmax_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_softmax_logits_bwd_f32": [_P, _P, _P, _I64, _I64, _CFG],
@@ -370,6 +372,21 @@ def rmsnorm_bwd(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, rstd: torch.
     )
 
 
+def rmsnorm_fwd_bwd(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, y: torch.Tensor,
+                    rstd: torch.Tensor, dx: torch.Tensor, dw: torch.Tensor, eps: float,
+                    cfg: CreditCfg) -> None:
+    """Forward and backward of RMSNorm in one call: y, rstd, dx, dw."""
+    rows, cols = _rows_cols(x)
+    check(
+        load_library().credit_rmsnorm_fwd_bwd_bf16(
+            _ptr(x, "x", torch.bfloat16), _ptr(w, "w", torch.bfloat16),
+            _ptr(dy, "dy", torch.bfloat16), _ptr(y, "y", torch.bfloat16),
+            _ptr(rstd, "rstd", torch.float32), _ptr(dx, "dx", torch.bfloat16),
+            _ptr(dw, "dw", torch.float32), rows, cols, float(eps), ctypes.byref(cfg)),
+        "credit_rmsnorm_fwd_bwd_bf16",
+    )
+
+
 def softmax_fwd(x: torch.Tensor, p: torch.Tensor, rowmax: torch.Tensor, lse: torch.Tensor,
                 cfg: CreditCfg) -> None:
     rows, cols = _rows_cols(x)
@@ -590,6 +607,13 @@ def launch_rmsnorm_bwd(inputs, outputs, config: LaunchConfig = LaunchConfig()) -
     rmsnorm_bwd(x, w, dy, rstd, dx, dw, make_cfg(config.variant, config.split))
 
 
+def launch_rmsnorm_fwd_bwd(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    """inputs: (x, w, dy); outputs: (y, rstd, dx, dw)."""
+    x, w, dy = inputs
+    y, rstd, dx, dw = outputs
+    rmsnorm_fwd_bwd(x, w, dy, y, rstd, dx, dw, RMSNORM_EPS, make_cfg(config.variant, config.split))
+
+
 def launch_softmax_fwd(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
     x = inputs[0]
     p, rowmax, lse = outputs
@@ -670,6 +694,7 @@ HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
     "layernorm_fwd": launch_layernorm_fwd,
     "rmsnorm_fwd": launch_rmsnorm_fwd,
     "rmsnorm_bwd": launch_rmsnorm_bwd,
+    "rmsnorm_fwd_bwd": launch_rmsnorm_fwd_bwd,
     "softmax_fwd": launch_softmax_fwd,
     "softmax_bwd": launch_softmax_bwd,
     "softmax_logits_backward": launch_softmax_logits_backward,
@@ -771,6 +796,9 @@ def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch
         return torch.empty_like(x), torch.empty(rows, **f32)
     if name == "rmsnorm_bwd":
         return torch.empty_like(x), torch.empty(x.shape[1], **f32)
+    if name == "rmsnorm_fwd_bwd":
+        return (torch.empty_like(x), torch.empty(rows, **f32), torch.empty_like(x),
+                torch.empty(x.shape[1], **f32))
     if name == "softmax_fwd":
         return torch.empty_like(x), torch.empty(rows, **f32), torch.empty(rows, **f32)
     if name == "rowwise_quant":

@@ -265,6 +265,20 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_max_cols=8192,
         stream_mix=(2, 1),
     ),
+    # C3's forward and backward in one call (credit_rmsnorm_fwd_bwd_bf16):
+    # x, dy, w in; y, rstd, dx, dweight out.
+    "rmsnorm_fwd_bwd": WorkloadSpec(
+        name="rmsnorm_fwd_bwd",
+        label="RMSNorm forward + backward fused (bf16)",
+        category="normalization",
+        rows=1024,
+        cols=131072,
+        input_factory=make_rmsnorm_inputs,
+        output_names=("y", "rstd", "dx", "dweight"),
+        algorithmic_bytes=lambda r, c: 2 * r * c * 4 + 2 * c + 4 * c + 4 * r,
+        tolerances=(BF16_TOL, FP32_TOL, BF16_TOL, FP32_TOL),
+        stream_mix=(2, 2),
+    ),
     "softmax_fwd": WorkloadSpec(
         name="softmax_fwd",
         label="Online softmax forward (fp32)",

@@ -112,6 +112,7 @@ typedef struct credit_cfg {
 #define CREDIT_OP_LARS_MOMENTUM 12
 #define CREDIT_OP_WEIGHTED_VAR_BWD 13
 #define CREDIT_OP_PEARSON_BWD 14
+#define CREDIT_OP_RMSNORM_FWD_BWD 15
 
 /* ------------------------------------------------------------ library --- */
 
@@ -222,6 +223,21 @@ int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, f
 int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* dy,
                             const float* rstd, uint16_t* dx, float* dw, int64_t rows,
                             int64_t cols, const credit_cfg* cfg);
+
+/* --------------------------------- C3: RMSNorm forward + backward fused --
+ * The forward and the backward in one pass over x and dy: y = x * rstd * w,
+ * rstd (fp32), dx and dw as credit_rmsnorm_bwd_bf16 -- 2 reads and 2 writes
+ * per element instead of the separate calls' 1 + 1 and 2 + 1 (C3: 1.07 GB
+ * against 1.34 GB).  The row's sum of squares travels in the same exchange
+ * as sum(dy*w*x).  AUTO / SPLIT: the group kernel, cfg->split or the fewest
+ * power-of-two members with slices of at most 8192 columns (at most 32
+ * members; one member for rows of at most 8192 columns); READ (and AUTO on
+ * shapes without cols % 8 == 0 and 16-byte aligned buffers): the forward
+ * then the backward.  STAGED is refused.  No counterpart in the reference
+ * (it has no RMSNorm); the fusion BASELINE's C3 names. */
+int credit_rmsnorm_fwd_bwd_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* dy,
+                                uint16_t* y, float* rstd, uint16_t* dx, float* dw, int64_t rows,
+                                int64_t cols, float eps, const credit_cfg* cfg);
 
 /* The same backward, allocating nothing: no counterpart in the reference.
  * It is for callers that cannot allocate device memory -- code under HIP

@@ -140,6 +140,19 @@ def rmsnorm_bwd(x, w, dy, rstd):
     return dx, dw
 
 
+def rmsnorm_fwd_bwd(x, w, dy, eps: float = 1.0e-6, rstd_fp32: bool = True):
+    """(y, rstd, dx, dweight) of the fused forward + backward: the forward,
+    then the backward from its rstd.  rstd_fp32: the backward takes rstd
+    rounded to fp32, as the fused kernel carries it (its y, dx and dweight
+    all use the fp32 rstd); False keeps it in float64 (the form pinned to
+    autograd)."""
+    y, rstd = rmsnorm_fwd(x, w, eps)
+    r = rstd.astype(np.float32) if rstd_fp32 else rstd
+    y = f64(x) * f64(r)[..., None] * f64(w) if rstd_fp32 else y
+    dx, dw = rmsnorm_bwd(x, w, dy, r)
+    return y, rstd, dx, dw
+
+
 # --------------------------------------------------------------- softmax --
 
 

@@ -129,6 +129,8 @@ FUNCTIONS = {
     "layernorm_fwd": layernorm_fwd,
     "rmsnorm_fwd": lambda x, w, dy: rmsnorm_fwd(x, w),
     "rmsnorm_bwd": lambda x, w, dy: rmsnorm_bwd(x, w, dy, rmsnorm_fwd(x, w)[1]),
+    "rmsnorm_fwd_bwd": lambda x, w, dy: (lambda f: (f, rmsnorm_bwd(x, w, dy, f[1])))(
+        rmsnorm_fwd(x, w)),
     "softmax_fwd": lambda x, dy: softmax_fwd(x),
     "softmax_bwd": lambda x, dy: softmax_bwd(torch.softmax(x, dim=-1), dy),
     "layernorm_backward": layernorm_backward,

@@ -125,6 +125,22 @@ def rmsnorm():
          ["bf16", "f32"])
 
 
+def rmsnorm_fused():
+    seed = 115
+    rows, cols = 3, 8192
+    x, w, dy = WORKLOADS["rmsnorm_fwd_bwd"].make_inputs(rows, cols, seed=seed)
+    x64 = d64(x).requires_grad_()
+    w64 = d64(w).requires_grad_()
+    y = F.rms_norm(x64, (cols,), w64, 1e-6)
+    y.backward(d64(dy))
+    rstd = torch.rsqrt(d64(x).pow(2).mean(-1) + 1e-6)
+    save("rmsnorm_fwd_bwd_3x8192", "rmsnorm_fwd_bwd", [["auto", 0], ["read", 0], ["split", 2]],
+         (x, w, dy), (y.detach().numpy(), rstd.numpy(), x64.grad.numpy(), w64.grad.numpy()),
+         [BF16, FP32, BF16, FP32],
+         "F.rms_norm and its autograd in float64 (y, rstd, dx, dweight) for upstream grad dy",
+         seed, ["bf16", "f32", "bf16", "f32"])
+
+
 def softmax():
     seed = 105
     rows, cols = 3, 5000
@@ -240,7 +256,8 @@ def ffn():
 
 def main() -> None:
     torch.manual_seed(0)
-    for fn in (row_sum_max, layernorm_fwd, rmsnorm, softmax, layernorm_backward, rowwise_quant,
+    for fn in (row_sum_max, layernorm_fwd, rmsnorm, rmsnorm_fused, softmax, layernorm_backward,
+               rowwise_quant,
                lars_momentum, weighted_var_backward, pearson_backward, ffn):
         fn()
 

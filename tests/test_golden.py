@@ -31,6 +31,9 @@ def oracle_outputs(name, ins):
         return ref.rmsnorm_fwd(a[0], a[1], 1e-6), [TIGHT, TIGHT]
     if name == "rmsnorm_bwd":
         return ref.rmsnorm_bwd(a[0], a[1], a[2], a[3]), [None, None]
+    if name == "rmsnorm_fwd_bwd":
+        # float64 rstd: the fixture is float64 autograd end to end
+        return ref.rmsnorm_fwd_bwd(a[0], a[1], a[2], 1e-6, rstd_fp32=False), [TIGHT] * 4
     if name == "softmax_fwd":
         return ref.softmax_fwd(a[0]), [TIGHT, None, TIGHT]
     if name == "softmax_bwd":

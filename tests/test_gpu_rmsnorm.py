@@ -220,3 +220,68 @@ def test_rmsnorm_bwd_back_to_back_launches(gpu, c3_case, variant, split):
     hip_lib.check_watchdog()
     np.testing.assert_allclose(dw.cpu().numpy(), edw, **FP32)
     np.testing.assert_allclose(dx.float().cpu().numpy(), edx, **BF16)
+
+
+def fused(x, w, dy, variant, split, gpu):
+    ins = [t.to(gpu) for t in (x, w, dy)]
+    y = torch.empty_like(ins[0])
+    rstd = torch.full((x.shape[0],), float("nan"), device=gpu)
+    dx = torch.empty_like(ins[0])
+    dw = torch.full((x.shape[1],), float("nan"), device=gpu)
+    hip_lib.rmsnorm_fwd_bwd(*ins, y, rstd, dx, dw, EPS, hip_lib.make_cfg(variant, split))
+    torch.cuda.synchronize()
+    hip_lib.check_watchdog()
+    return (y.float().cpu().numpy(), rstd.cpu().numpy(), dx.float().cpu().numpy(),
+            dw.cpu().numpy())
+
+
+def check_fused(x, w, dy, y, rstd, dx, dw):
+    """rstd against the float64 forward; y, dx and dweight against the
+    oracle given the kernel's own fp32 rstd (as the backward tests give it
+    the rstd input): a 1-ulp difference of rstd in a row moves dweight's
+    cancelling columns by more than fp32's atol, and is no error of the
+    backward arithmetic."""
+    xf, wf, dyf = x.float().numpy(), w.float().numpy(), dy.float().numpy()
+    _, er = ref.rmsnorm_fwd(xf, wf, EPS)
+    np.testing.assert_allclose(rstd, er, **FP32)
+    edx, edw = ref.rmsnorm_bwd(xf, wf, dyf, rstd)
+    np.testing.assert_allclose(dw, edw, **FP32)
+    np.testing.assert_allclose(y, xf.astype(np.float64) * rstd[:, None] * wf, **BF16)
+    np.testing.assert_allclose(dx, edx, **BF16)
+
+
+@pytest.mark.parametrize("shape,variant,split", [((16, 8192), "auto", 0), ((5, 65536), "split", 8),
+                                                 ((77, 65544), "auto", 0), ((300, 16384), "split", 2),
+                                                 ((9, 4096), "read", 0), ((33, 24), "auto", 0),
+                                                 ((130, 262144), "auto", 0)])
+def test_rmsnorm_fwd_bwd_shapes(gpu, shape, variant, split):
+    """The fused call: one member per row (8192 columns), ragged last members
+    (65544 = 8193 vectors over 16), more rows than groups, the two-call READ
+    path, a row too narrow for 16-byte vectors (AUTO takes the two calls),
+    and 32 members at 262144 columns."""
+    print(f"rmsnorm_fwd_bwd {variant} P={split} shape={shape}", flush=True)
+    x, w, dy = SPEC.make_inputs(*shape, seed=shape[0] + 3)
+    check_fused(x, w, dy, *fused(x, w, dy, variant, split, gpu))
+
+
+@pytest.mark.parametrize("variant,split", [("auto", 0), ("split", 32), ("read", 0)])
+def test_rmsnorm_fwd_bwd_full_config(gpu, c3_case, variant, split):
+    x, w, dy, *_ = c3_case
+    check_fused(x, w, dy, *fused(x, w, dy, variant, split, gpu))
+
+
+def test_rmsnorm_fwd_bwd_back_to_back_and_rejections(gpu, c3_case):
+    x, w, dy, ey, er, r32, edx, edw = c3_case
+    ins = [t.to(gpu) for t in (x, w, dy)]
+    y, rstd, dx, dw = hip_lib.allocate_outputs("rmsnorm_fwd_bwd", ins)
+    cfg = hip_lib.make_cfg("auto")
+    for _ in range(6):
+        hip_lib.rmsnorm_fwd_bwd(*ins, y, rstd, dx, dw, EPS, cfg)
+    torch.cuda.synchronize()
+    hip_lib.check_watchdog()
+    check_fused(x, w, dy, y.float().cpu().numpy(), rstd.cpu().numpy(), dx.float().cpu().numpy(),
+                dw.cpu().numpy())
+    for variant, split in (("staged", 0), ("split", 8), ("split", 64)):
+        with pytest.raises(hip_lib.CreditError) as err:
+            hip_lib.rmsnorm_fwd_bwd(*ins, y, rstd, dx, dw, EPS, hip_lib.make_cfg(variant, split))
+        assert err.value.status == -4

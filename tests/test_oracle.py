@@ -101,6 +101,29 @@ def test_rmsnorm_bwd_matches_autograd():
     np.testing.assert_allclose(dw, tw.grad.numpy(), rtol=1e-10, atol=1e-12)
 
 
+def test_rmsnorm_fwd_bwd_matches_autograd():
+    """The fused oracle (float64 rstd) against one autograd pass of
+    F.rms_norm with upstream grad dy; with the fp32 rstd it moves by about
+    the fp32 rounding of rstd (relative 6e-8, more on dx entries that
+    cancel: atol scaled to the largest entry)."""
+    x = RNG.standard_normal((5, 257))
+    w = RNG.normal(1, 0.02, 257)
+    dy = RNG.standard_normal((5, 257))
+    tx = t64(x).requires_grad_()
+    tw = t64(w).requires_grad_()
+    ty = F.rms_norm(tx, (257,), tw, 1e-6)
+    ty.backward(t64(dy))
+    y, rstd, dx, dw = ref.rmsnorm_fwd_bwd(x, w, dy, 1e-6, rstd_fp32=False)
+    np.testing.assert_allclose(y, ty.detach().numpy(), rtol=1e-12)
+    np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dw, tw.grad.numpy(), rtol=1e-10, atol=1e-12)
+    y32, rstd32, dx32, dw32 = ref.rmsnorm_fwd_bwd(x, w, dy, 1e-6)
+    np.testing.assert_array_equal(rstd32, rstd)
+    for a, b in ((y32, y), (dx32, dx), (dw32, dw)):
+        np.testing.assert_allclose(a, b, rtol=2e-7, atol=2e-7 * np.abs(b).max())
+        assert not np.array_equal(a, b)
+
+
 # ---------------------------------------------------------------- C4 ------
 
 
