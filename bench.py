@@ -26,6 +26,8 @@ measured the same way and reported under "suite".  Per workload:
   (credit_stream_ceiling) at the workload's read:write byte mix and call
   size, over the same number of rotating sets; ``frac`` of it is reported
   beside the fraction of the 8 TB/s peak;
+  for the FFN, the attainable dense bf16 MFMA rate (back-to-back MFMA
+  chains on every CU, no memory traffic) and the shader clock it ran at;
 * ``roofline.traffic``: HBM bytes per call from the committed rocprofv3 PMC
   summary, or null when the kernels' sources changed after it was taken;
 * ``cpu_baseline``: the reference's PyTorch path on the host cores.
@@ -290,6 +292,13 @@ def measure(name, args, hip_lib, torch, dev, with_cpu):
                              "frac_median": round(flops / (trials.median_ms * 1e-3) / 1e12
                                                   / BF16_PEAK_TFLOPS, 4),
                              "traffic": traffic, "traffic_source": traffic_note})
+        if not args.no_ceiling:
+            try:
+                ceiling = hip_lib.mfma_ceiling()
+                ceiling["frac"] = round(achieved / ceiling["TFLOPs"], 4)
+            except hip_lib.CreditError as err:
+                ceiling = {"error": str(err)}
+            out["roofline"]["ceiling"] = ceiling
     else:
         nbytes = spec.algorithmic_bytes(spec.rows, spec.cols)
         achieved = nbytes / (kernel_ms * 1e-3) / 1e9

@@ -301,6 +301,52 @@ __global__ __launch_bounds__(64) void mb_ticket_kernel(uint32_t* lines, int draw
   cycles[blockIdx.x] = t1 - t0 + (t >> 31);
 }
 
+// ------------------------------------------------------ MFMA rate ---
+// Dense bf16 MFMA issue rate: every wave runs `iters` rounds of CHAINS
+// independent v_mfma_f32_32x32x16_bf16 (no memory traffic in the loop), and
+// records its shader-clock and 100 MHz constant-clock deltas.  Operands are
+// small constants so the accumulators stay finite; the sums are stored so
+// the chains are not dead code.
+typedef __bf16 mb_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float mb_f32x16 __attribute__((ext_vector_type(16)));
+constexpr int kMfmaChains = 8;
+
+__global__ __launch_bounds__(512) void mb_mfma_kernel(int iters, float* sink, uint64_t* clocks) {
+  extern __shared__ char hold[];  // sized by the launch to keep one workgroup per CU
+  const int lane = threadIdx.x & 63;
+  mb_bf16x8 a, b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a[e] = static_cast<__bf16>(1.0f / 1024.0f * static_cast<float>((lane + e) & 7));
+    b[e] = static_cast<__bf16>(1.0f / 4096.0f * static_cast<float>((lane * 3 + e) & 7));
+  }
+  mb_f32x16 acc[kMfmaChains];
+#pragma unroll
+  for (int c = 0; c < kMfmaChains; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[c][r] = 0.0f;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int c = 0; c < kMfmaChains; ++c)
+      acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[c], 0, 0, 0);
+  }
+  const uint64_t t1 = __builtin_amdgcn_s_memtime();
+  const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kMfmaChains; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += acc[c][r];
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  sink[blockIdx.x * blockDim.x + threadIdx.x] = s + static_cast<float>(hold[0] & 0);
+  if (lane == 0) {
+    clocks[2 * wave] = t1 - t0;
+    clocks[2 * wave + 1] = r1 - r0;
+  }
+}
+
 struct Events {
   hipEvent_t a = nullptr, b = nullptr;
   ~Events() {
@@ -568,6 +614,61 @@ int bench_cache(int passes, double* results, int n) {
   return CREDIT_OK;
 }
 
+// Dense bf16 MFMA rate with one workgroup per CU of 4 waves (one per
+// SIMD) and of 8 waves (two per SIMD), each settled for about 100 ms and
+// timed as the median of five launches of about 5 ms.  results: [0] best
+// TFLOP/s, [1] the mean shader clock of its waves during the MFMA loop
+// (MHz, from s_memtime against the 100 MHz s_memrealtime), [2] its flops per
+// shader cycle per CU, [3] waves per SIMD of the best, [4] TFLOP/s with 4
+// waves, [5] with 8.
+int bench_mfma(int iters, double* results, int n) {
+  const DeviceProps* props = nullptr;
+  CREDIT_TRY(current_device_props(&props));
+  if (iters <= 0) iters = 20000;
+  constexpr int kHold = 96 << 10;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(mb_mfma_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kHold);
+  if (attr != hipSuccess) return hip_failure(attr, "hipFuncSetAttribute(mb_mfma_kernel)");
+  const int cus = props->cu_count;
+  DevBuf sink, clk;
+  CREDIT_TRY(sink.alloc(sizeof(float) * cus * 512));
+  CREDIT_TRY(clk.alloc(sizeof(uint64_t) * 2 * cus * 8));
+  double best = 0.0, best_mhz = 0.0, best_waves = 0.0, rate[2] = {0.0, 0.0};
+  for (int v = 0; v < 2; ++v) {
+    const int threads = 256 << v;
+    auto launch = [&](int) -> int {
+      mb_mfma_kernel<<<cus, threads, kHold>>>(iters, static_cast<float*>(sink.p),
+                                              static_cast<uint64_t*>(clk.p));
+      return check_launch("mb_mfma_kernel");
+    };
+    double ms = 0.0;
+    CREDIT_TRY(settled_median_ms(launch, 100.0, 5, 1, &ms));
+    const double flops = 2.0 * 32 * 32 * 16 * kMfmaChains * static_cast<double>(iters) *
+                         (threads / 64) * cus;
+    rate[v] = flops / (ms * 1e-3) / 1e12;
+    const int waves = cus * threads / 64;
+    std::vector<uint64_t> h(static_cast<size_t>(2) * waves);
+    CREDIT_HIP(hipMemcpy(h.data(), clk.p, sizeof(uint64_t) * h.size(), hipMemcpyDeviceToHost));
+    double mhz = 0.0;
+    for (int w = 0; w < waves; ++w)
+      mhz += static_cast<double>(h[2 * w]) / (static_cast<double>(h[2 * w + 1]) / 100.0);
+    mhz /= waves;
+    if (rate[v] > best) {
+      best = rate[v];
+      best_mhz = mhz;
+      best_waves = (threads / 64) / 4;
+    }
+  }
+  results[0] = best;
+  if (n > 1) results[1] = best_mhz;
+  if (n > 2) results[2] = best * 1e12 / (best_mhz * 1e6) / cus;
+  if (n > 3) results[3] = best_waves;
+  if (n > 4) results[4] = rate[0];
+  if (n > 5) results[5] = rate[1];
+  return CREDIT_OK;
+}
+
 // [0] bytes per cycle per workgroup of device-scope slot stores with one
 // workgroup per CU, [1] the same stores as GB/s over the device, [2] cycles
 // per ticket draw on a workgroup's own line, [3] cycles per draw when one
@@ -710,6 +811,8 @@ extern "C" int credit_microbench(int32_t which, int64_t bytes, int32_t iters, do
       return bench_cache(iters, results, n_results);
     case CREDIT_MB_EXCHANGE_THROUGHPUT:
       return bench_exchange_throughput(iters, results, n_results);
+    case CREDIT_MB_MFMA_BF16:
+      return bench_mfma(iters, results, n_results);
     default:
       return set_error(CREDIT_ERR_BAD_CONFIG, "unknown microbenchmark %d", which);
   }

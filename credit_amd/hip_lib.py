@@ -260,6 +260,7 @@ MICROBENCH = {
     "exchange_roundtrip": 8,
     "cache_read": 9,
     "exchange_throughput": 10,
+    "mfma_bf16": 11,
 }
 
 
@@ -269,6 +270,16 @@ def microbench(name: str, nbytes: int = 0, iters: int = 0, n_results: int = 16) 
     check(load_library().credit_microbench(MICROBENCH[name], nbytes, iters, out, n_results),
           "credit_microbench")
     return list(out)
+
+
+def mfma_ceiling(iters: int = 20000) -> dict:
+    """Attainable dense bf16 MFMA rate (CREDIT_MB_MFMA_BF16): TFLOP/s of
+    back-to-back v_mfma_f32_32x32x16_bf16 chains on every CU, the shader
+    clock the waves ran at, and the waves per SIMD that reached it."""
+    r = microbench("mfma_bf16", 0, iters, 6)
+    return {"TFLOPs": round(r[0], 1), "clock_MHz": round(r[1], 1),
+            "flops_per_cycle_cu": round(r[2], 1), "waves_per_simd": int(r[3]),
+            "TFLOPs_by_waves_per_simd": {"1": round(r[4], 1), "2": round(r[5], 1)}}
 
 
 def stream_ceiling(reads: int, writes: int, call_bytes: int, trials: int = 5, iters: int = 20,

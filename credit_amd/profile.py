@@ -57,6 +57,8 @@ TEXT_KEYS: tuple[tuple[str, str, str], ...] = (
     ("slot_store_gbps", "Exchange slot store throughput (device)", "GB/s"),
     ("ticket_cycles_private", "Ticket draw private line", "cycles"),
     ("ticket_cycles_shared", "Ticket draw shared line", "cycles"),
+    ("mfma_bf16_tflops", "MFMA bf16 rate", "TFLOP/s"),
+    ("mfma_clock_mhz", "MFMA shader clock", "MHz"),
 )
 
 
@@ -73,6 +75,7 @@ def run_microbenchmarks(hbm_bytes: int = 1 << 30, iters: int = 20) -> dict[str, 
     rt = hip_lib.microbench("exchange_roundtrip", 0, 2000, 2)
     cache = hip_lib.microbench("cache_read", 0, 64, 3)
     xput = hip_lib.microbench("exchange_throughput", 0, 4096, 4)
+    mfma = hip_lib.microbench("mfma_bf16", 0, 20000, 6)
     return {
         "name": info["name"],
         "arch": info["arch"],
@@ -102,6 +105,8 @@ def run_microbenchmarks(hbm_bytes: int = 1 << 30, iters: int = 20) -> dict[str, 
         "slot_store_gbps": xput[1],
         "ticket_cycles_private": xput[2],
         "ticket_cycles_shared": xput[3],
+        "mfma_bf16_tflops": mfma[0],
+        "mfma_clock_mhz": mfma[1],
     }
 
 

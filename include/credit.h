@@ -409,6 +409,17 @@ int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t rows, int6
  *                         one line shared by one workgroup per CU (iters =
  *                         store rounds); replaces the DSMEM store/load
  *                         throughput of src/primitive_benchmark.cu:433-503
+ *   MFMA_BF16           : [0] dense bf16 MFMA TFLOP/s (v_mfma_f32_32x32x16_bf16
+ *                         chains, no memory traffic, one workgroup per CU,
+ *                         best of 4 and 8 waves per workgroup), [1] the mean
+ *                         shader clock of its waves during the loop (MHz),
+ *                         [2] flops per shader cycle per CU, [3] waves per
+ *                         SIMD of the best, [4] TFLOP/s at 4 waves, [5] at 8
+ *                         (iters = rounds of 8 MFMAs per wave); the
+ *                         reference has no counterpart (its workloads have
+ *                         no GEMM): the attainable rate the FFN GEMMs are
+ *                         measured against, beside the 2.5 PFLOP/s datasheet
+ *                         peak
  *  HBM_READ/WRITE/COPY run the mixed-stream kernels of credit_stream_ceiling
  *  (mixes 1:0, 0:1, 1:1). */
 #define CREDIT_MB_HBM_READ 1
@@ -421,6 +432,7 @@ int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t rows, int6
 #define CREDIT_MB_EXCHANGE_ROUNDTRIP 8
 #define CREDIT_MB_CACHE_READ 9
 #define CREDIT_MB_EXCHANGE_THROUGHPUT 10
+#define CREDIT_MB_MFMA_BF16 11
 int credit_microbench(int32_t which, int64_t bytes, int32_t iters, double* results,
                       int32_t n_results);
 

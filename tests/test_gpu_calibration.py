@@ -62,3 +62,14 @@ def test_stream_ceiling_rejects_unbuilt_mixes(gpu):
         hip_lib.stream_ceiling(3, 3, 1 << 26)
     with pytest.raises(hip_lib.CreditError):
         hip_lib.stream_ceiling(1, 1, 1024)  # under 64 KiB per stream
+
+
+def test_mfma_rate_is_physical(gpu):
+    """The MFMA rate the FFN is compared with: positive, at most the
+    datasheet 2.5 PFLOP/s (plus noise), and per shader cycle at most the
+    4 SIMDs x 1024 flops a CU's matrix cores issue."""
+    c = hip_lib.mfma_ceiling(4000)
+    print(f"MFMA bf16 {c}", flush=True)
+    assert 500.0 < c["TFLOPs"] < 2500.0 * 1.05
+    assert 500.0 < c["clock_MHz"] < 3000.0
+    assert c["flops_per_cycle_cu"] < 4096 * 1.05

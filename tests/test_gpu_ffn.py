@@ -56,10 +56,12 @@ def test_transpose_is_exact(gpu, shape):
 # d allows, GEMM2) on the 256-tile direct-to-LDS kernel (M and N multiples
 # of 256, K of 128, tile count a multiple of 8).  (512, 128, 1024) gives it
 # the shortest K (two 64-wide steps), (2048, 384, 256) an odd number of
-# step pairs (six steps).
+# step pairs (six steps), (4096, 256, 4608) GEMM1 288 tiles: more than one
+# workgroup per CU, so a second, partial wave of tiles.
 @pytest.mark.parametrize("rows,d,f", [(128, 128, 128), (128, 256, 384), (256, 128, 512),
                                       (384, 512, 256), (512, 1024, 1024), (256, 2048, 2048),
-                                      (1024, 512, 4096), (512, 128, 1024), (2048, 384, 256)])
+                                      (1024, 512, 4096), (512, 128, 1024), (2048, 384, 256),
+                                      (4096, 256, 4608)])
 def test_ffn_small_shapes(gpu, rows, d, f):
     print(f"ffn rows={rows} d={d} f={f}", flush=True)
     x, w1, w2 = make(rows, d, f, seed=rows + d + f)
