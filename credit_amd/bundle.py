@@ -8,7 +8,9 @@ A bundle is the directory ``credit_amd.runner.run_suite`` writes:
 * ``summary.csv``     -- one row per (workload, rows, cols) point: best
                          no-split variant, best split, the model's verdict;
 * ``cluster_sweep.csv`` -- one row per split factor of every point, with the
-                         cost model's terms;
+                         cost model's terms, its predicted traffic and (once
+                         credit_amd.counters merged a counter pass) the
+                         measured HBM bytes and L2 requests beside them;
 * ``REPORT.md``       -- credit_amd.report.
 
 The column sets of summary.csv and cluster_sweep.csv are the contract the
@@ -61,6 +63,12 @@ SWEEP: Schema = (
     ("split_p80_ms", float), ("control_overhead_ms", float), ("model_version", str),
     *((f.name, _ESTIMATE_TYPES[f.type]) for f in dataclasses.fields(ModelEstimate)),
     ("measured_delta_vs_block_ms", float), ("measured_profitable_vs_block", bool),
+    # cost_model.predict_traffic, and beside it the counters of one call of
+    # the same variant (credit_amd.counters; empty until merged).
+    ("predicted_hbm_bytes", float), ("predicted_block_hbm_bytes", float),
+    ("predicted_l2_requests", float), ("predicted_lds_bytes", float),
+    ("measured_hbm_bytes", float), ("measured_block_hbm_bytes", float),
+    ("measured_l2_requests", float), ("counter_source", str),
 )
 
 TABLES: dict[str, Schema] = {

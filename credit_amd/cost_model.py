@@ -34,6 +34,11 @@ L2-resident workspace.  The terms become:
 
 ``estimate()`` keeps the reference's signature and result shape so the
 runner's summary logic (dsmem_eval/runner.py:444-620) carries over.
+
+``predict_traffic()`` states the bytes behind those terms -- HBM bytes of
+the split and of the best no-split variant, L2 requests of the split and the
+LDS bytes its exchange and replay move -- so a sweep can put hardware
+counters (credit_amd.counters) beside them.
 """
 from __future__ import annotations
 
@@ -216,3 +221,60 @@ def estimate(
         predicted_delta_ms=delta,
         predicted_profitable=delta > 0.0,
     )
+
+
+# L2 request sizes the traffic prediction counts in: a wave's streaming
+# read asks the L2 for whole 128-byte lines, its writes arrive as 64-byte
+# requests (TCC_REQ of the read-only row reduction is its line count; of a
+# 1:1 read:write stream, 1.5 times it).
+L2_LINE_BYTES = 128
+L2_WRITE_REQUEST_BYTES = 64
+
+
+@dataclass(frozen=True)
+class TrafficPrediction:
+    hbm_bytes: float          # split variant: one HBM pass plus the exchange slots
+    block_hbm_bytes: float    # best no-split variant: plus the re-read when the row does not fit
+    l2_requests: float        # split variant: streamed reads and writes plus exchange traffic
+    lds_bytes: float          # split variant: exchange copies plus the spilled-slice replay
+    exchange_bytes: float     # split variant: slot stores and one poll per member and stage
+
+
+def predict_traffic(spec, cols: int, split: int, profile: DeviceProfile,
+                    rows: int | None = None) -> TrafficPrediction:
+    """Bytes one call moves under the model's assumptions (the same ones
+    estimate() prices): every member reads its slice once, so the split
+    moves the algorithmic bytes; the no-split variant re-reads
+    ``reread_bytes_per_element`` when the row does not fit one workgroup;
+    every exchange stage costs each member one 8-byte slot store per
+    partial and one poll of the group's slots (the minimum: a poll that
+    finds a partial missing is repeated).  Slot stores and polls are
+    device-scope accesses that pass the L2 to the memory side, so the HBM
+    counters see them with the streamed bytes.  The exchanged values are
+    copied once into each member's LDS; a slice beyond the register budget
+    is replayed from LDS once per extra pass."""
+    row_count = spec.rows if rows is None else rows
+    p = int(split)
+    compulsory = float(spec.algorithmic_bytes(row_count, cols))
+    reads, writes = getattr(spec, "stream_mix", (1, 0))
+    if reads + writes <= 0:
+        reads, writes = 1, 0
+    write_share = writes / (reads + writes)
+    reread = 0.0 if row_fits_one_workgroup(spec, cols, profile) else \
+        float(row_count) * cols * spec.reread_bytes_per_element
+    k = max(int(spec.partial_count), 1)
+    stages = float(row_count) * max(int(spec.barrier_count), 1)
+    slot_bytes = stages * p * (8.0 * k + 8.0 * k * p)  # stores + one poll per member
+    exchange_requests = stages * p * (k + math.ceil(8.0 * k * p / L2_LINE_BYTES))
+    spilled = max(staged_bytes_per_workgroup(spec, cols, p) - REGISTER_STAGING_BYTES, 0)
+    extra_passes = max(int(spec.barrier_count) - 1, 0)
+    lds = stages * p * (4.0 * k * p) + float(row_count) * p * spilled * extra_passes
+    return TrafficPrediction(
+        hbm_bytes=compulsory + slot_bytes,
+        block_hbm_bytes=compulsory + reread,
+        l2_requests=(compulsory * (1.0 - write_share) / L2_LINE_BYTES +
+                     compulsory * write_share / L2_WRITE_REQUEST_BYTES + exchange_requests),
+        lds_bytes=lds,
+        exchange_bytes=slot_bytes,
+    )
+

@@ -307,10 +307,21 @@ __global__ __launch_bounds__(THREADS) void layernorm_fwd_slice_kernel(
     }
     const float rs = static_cast<float>(1.0 / __builtin_sqrt((var > 0.0 ? var : 0.0) + eps));
     const buffer_rsrc_t yrs = make_rsrc(y + off, slice_bytes);
+    // Output in groups of four vectors: gamma and beta of one group in
+    // flight at a time (all of them at once, 16 VGPRs per vector, would
+    // push the 1024-lane shape past its 128 VGPRs into scratch).
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-      const uint32_t o = lane_off + k * kStride;
-      buffer_store_nt(yrs, o, norm8(v[k], buffer_load(grs, o), buffer_load(brs, o), mu, rs));
+    for (int k0 = 0; k0 < VPT; k0 += 4) {
+      u32x4 gv[4], bv[4];
+#pragma unroll
+      for (int j = 0; j < 4 && k0 + j < VPT; ++j) {
+        gv[j] = buffer_load(grs, lane_off + (k0 + j) * kStride);
+        bv[j] = buffer_load(brs, lane_off + (k0 + j) * kStride);
+      }
+#pragma unroll
+      for (int j = 0; j < 4 && k0 + j < VPT; ++j)
+        buffer_store_nt(yrs, lane_off + (k0 + j) * kStride, norm8(v[k0 + j], gv[j], bv[j], mu, rs));
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (g.member == 0 && threadIdx.x == 0) {
       mean_out[row] = static_cast<float>(mean);
@@ -449,9 +460,11 @@ const SlicePick kSlice[] = {
     {layernorm_fwd_slice_kernel<256, 4>, 256, 1024},
     {layernorm_fwd_slice_kernel<256, 8>, 256, 2048},
     {layernorm_fwd_slice_kernel<512, 8>, 512, 4096},
-    {layernorm_fwd_slice_kernel<1024, 8>, 1024, 8192},
 };
-constexpr int64_t kSliceCapacity = 8192;  // vectors per member
+// No 1024-lane slice shape: at 128 VGPRs per lane its row, exchange and
+// output state spill to scratch (the counters saw 2.4x the HBM bytes).
+constexpr int64_t kSliceCapacity = 8192;       // vectors of the STAGED kernel
+constexpr int64_t kSplitSliceCapacity = 4096;  // vectors per SPLIT member
 constexpr int kMaxSliceMembers = kMaxExchangeValues / 2;  // (sum, sum of squares)
 
 struct Plan {
@@ -482,14 +495,15 @@ int resolve(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
     return CREDIT_OK;
   }
   int p = variant == CREDIT_VARIANT_SPLIT ? cfg_split(cfg) : 0;
-  if (p == 0) p = static_cast<int>((nvec + kSliceCapacity - 1) / kSliceCapacity);
+  if (p == 0) p = static_cast<int>((nvec + kSplitSliceCapacity - 1) / kSplitSliceCapacity);
   if (p < 2) p = 2;
   if (p > nvec) p = static_cast<int>(nvec);
   const int64_t chunk = (nvec + p - 1) / p;
   const int members = static_cast<int>((nvec + chunk - 1) / chunk);
-  if (chunk > kSliceCapacity)
-    return set_error(CREDIT_ERR_UNSUPPORTED, "layernorm_fwd split %d leaves %lld vectors per member",
-                     p, static_cast<long long>(chunk));
+  if (chunk > kSplitSliceCapacity)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "layernorm_fwd split %d leaves %lld vectors per member (at most %lld)", p,
+                     static_cast<long long>(chunk), static_cast<long long>(kSplitSliceCapacity));
   if (members > kMaxSliceMembers)
     return set_error(CREDIT_ERR_UNSUPPORTED, "layernorm_fwd split of %d members (at most %d)",
                      members, kMaxSliceMembers);

@@ -29,7 +29,7 @@ from pathlib import Path
 from typing import Any
 
 from .bundle import Bundle
-from .cost_model import MODEL_VERSION, DeviceProfile, estimate
+from .cost_model import MODEL_VERSION, DeviceProfile, estimate, predict_traffic
 from .report import render
 from .workloads import WORKLOADS
 
@@ -79,7 +79,10 @@ def predict(bundle: Bundle, profile: DeviceProfile) -> dict[PointKey, dict[str, 
         spec = dataclasses.replace(WORKLOADS[key[0]], rows=key[1])
         est = estimate(spec, key[2], int(row["split"]), float(row["control_overhead_ms"]),
                        profile, baseline_ms=block_ms[key], rows=key[1])
-        row.update(dataclasses.asdict(est), model_version=MODEL_VERSION)
+        tp = predict_traffic(spec, key[2], int(row["split"]), profile, rows=key[1])
+        row.update(dataclasses.asdict(est), model_version=MODEL_VERSION,
+                   predicted_hbm_bytes=tp.hbm_bytes, predicted_block_hbm_bytes=tp.block_hbm_bytes,
+                   predicted_l2_requests=tp.l2_requests, predicted_lds_bytes=tp.lds_bytes)
         if key not in best or est.predicted_delta_ms > best[key]["predicted_delta_ms"]:
             best[key] = {"predicted_split": int(row["split"]),
                          "predicted_delta_ms": est.predicted_delta_ms,

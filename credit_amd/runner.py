@@ -41,7 +41,8 @@ import torch
 
 from . import bundle, hip_lib
 from .bundle import write_table
-from .cost_model import MODEL_VERSION, DeviceProfile, estimate, staged_bytes_per_workgroup
+from .cost_model import (MODEL_VERSION, DeviceProfile, estimate, predict_traffic,
+                         staged_bytes_per_workgroup)
 from .profile import format_profile_text, make_device_profile, profile_as_dict, run_microbenchmarks
 from .report import write_report
 from .timing import run_trials
@@ -224,6 +225,7 @@ def build_summary(raw: list[dict[str, Any]], control: dict[tuple[int, int, int],
             if not math.isfinite(ctl):
                 continue
             m = estimate(spec, cols, r["split"], ctl, profile, baseline_ms=block["ms"], rows=rows)
+            tp = predict_traffic(spec, cols, r["split"], profile, rows=rows)
             candidates.append((m.predicted_delta_ms, r["split"], m))
             sweep.append({
                 "workload": name, "rows": rows, "cols": cols, "split": r["split"],
@@ -233,6 +235,9 @@ def build_summary(raw: list[dict[str, Any]], control: dict[tuple[int, int, int],
                 **{k: v for k, v in asdict(m).items()},
                 "measured_delta_vs_block_ms": block["ms"] - r["ms"],
                 "measured_profitable_vs_block": r["ms"] < block["ms"],
+                "predicted_hbm_bytes": tp.hbm_bytes,
+                "predicted_block_hbm_bytes": tp.block_hbm_bytes,
+                "predicted_l2_requests": tp.l2_requests, "predicted_lds_bytes": tp.lds_bytes,
             })
         if not candidates:
             continue
@@ -344,6 +349,8 @@ def main(argv=None) -> int:
     ap.add_argument("--trials", type=int, default=5)
     ap.add_argument("--settle-ms", type=float, default=20.0,
                     help="wall time each variant runs before its warmup calls")
+    ap.add_argument("--tensor-bytes", type=int, default=DEFAULT_TENSOR_BYTES,
+                    help="rows per point: as many as make one input tensor this large")
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--profile-only", action="store_true")
     ap.add_argument("--profile-text", type=Path,
@@ -355,7 +362,8 @@ def main(argv=None) -> int:
         w.strip() for w in args.workloads.split(",") if w.strip())
     config = {"workloads": workloads, "n_values": args.n_values, "splits": args.splits,
               "warmup": args.warmup, "iterations": args.iterations, "trials": args.trials,
-              "settle_ms": args.settle_ms, "quick": args.quick, "profile_only": args.profile_only}
+              "settle_ms": args.settle_ms, "quick": args.quick, "profile_only": args.profile_only,
+              "tensor_bytes": args.tensor_bytes}
     text = args.profile_text.read_text() if args.profile_text else None
     meta = run_suite(config, args.output_dir.resolve(), text)
     print(f"Status: {meta['status']}")

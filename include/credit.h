@@ -176,9 +176,13 @@ int credit_row_sum_max_f32(const float* x, float* sum, float* max,
  * No forward kernel exists in the reference; its statistics follow
  * src/workloads/layernorm_backward.cu:286-295 and the eps of
  * dsmem_eval/workloads.py:55.  Variants: STAGED (row in one workgroup's
- * VGPRs, cols <= 65536), READ (three streaming passes; any shape); SPLIT is
- * not built.  AUTO: the persistent two-row pipeline for tall matrices of
- * 16385..32768 columns, else STAGED, else READ. */
+ * VGPRs, cols <= 65536), SPLIT (P workgroups per row of at most 32768
+ * columns each, at most 32 members, exchanging (sum, sum of squares) once,
+ * plus squared deviations for offset rows: one read of x; the split form of
+ * src/workloads/layernorm_backward.cu:376-438), READ (vectorised streaming
+ * passes; any shape).  AUTO: the persistent two-row pipeline for tall
+ * matrices of 16385..32768 columns, STAGED up to 65536 columns, SPLIT with
+ * the fewest members beyond, READ for cols % 8 != 0 or unaligned buffers. */
 int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamma,
                               const uint16_t* beta, uint16_t* y, float* mean,
                               float* rstd, int64_t rows, int64_t cols,

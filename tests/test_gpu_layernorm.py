@@ -123,7 +123,7 @@ def test_layernorm_fwd_offset_rows_take_the_two_pass_statistics(gpu, shape):
 
 
 @pytest.mark.parametrize("shape,variant,split", [((2, 140000), "auto", 0), ((256, 262144), "auto", 0),
-                                                 ((5, 131072), "split", 2), ((5, 131072), "split", 3),
+                                                 ((5, 131072), "split", 4), ((5, 131072), "split", 5),
                                                  ((9, 65536), "split", 8), ((300, 100000), "auto", 0),
                                                  ((3, 140000), "read", 0)])
 def test_layernorm_fwd_wide_rows(gpu, shape, variant, split):
@@ -157,6 +157,10 @@ def test_layernorm_fwd_split_rejections(gpu):
     x, g, b = SPEC.make_inputs(2, 65536, seed=1)
     with pytest.raises(hip_lib.CreditError) as err:
         run_split(x, g, b, "split", 33, gpu)  # 33 members exchange 66 partials
+    assert err.value.status == -4
+    x, g, b = SPEC.make_inputs(2, 131072, seed=1)
+    with pytest.raises(hip_lib.CreditError) as err:
+        run_split(x, g, b, "split", 2, gpu)  # 8192 vectors per member: at most 4096
     assert err.value.status == -4
     x, g, b = SPEC.make_inputs(2, 65544 + 4, seed=1)  # cols % 8 != 0
     with pytest.raises(hip_lib.CreditError) as err:
