@@ -308,8 +308,8 @@ __global__ __launch_bounds__(THREADS) void layernorm_fwd_slice_kernel(
     const float rs = static_cast<float>(1.0 / __builtin_sqrt((var > 0.0 ? var : 0.0) + eps));
     const buffer_rsrc_t yrs = make_rsrc(y + off, slice_bytes);
     // Output in groups of four vectors: gamma and beta of one group in
-    // flight at a time (all of them at once, 16 VGPRs per vector, would
-    // push the 1024-lane shape past its 128 VGPRs into scratch).
+    // flight at a time (the compiler otherwise hoists all of them, 8 VGPRs
+    // per vector, above the first store).
 #pragma unroll
     for (int k0 = 0; k0 < VPT; k0 += 4) {
       u32x4 gv[4], bv[4];

@@ -110,6 +110,27 @@ def run_microbenchmarks(hbm_bytes: int = 1 << 30, iters: int = 20) -> dict[str, 
     }
 
 
+# Read:write stream mixes credit_stream_ceiling builds (workloads.py's
+# stream_mix of every workload is one of them).
+CEILING_MIXES = ((1, 0), (0, 1), (1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (2, 2), (1, 2))
+
+
+def ceiling_table(sizes: list[int], trials: int = 5, iters: int = 20) -> str:
+    """Markdown: best settled GB/s (and its launch shape) per mix and call size."""
+    lines = ["| mix (read:write) | " + " | ".join(f"{s / 2**20:.0f} MiB per call" for s in sizes)
+             + " |", "|---|" + "---|" * len(sizes)]
+    for r, w in CEILING_MIXES:
+        cells = []
+        for s in sizes:
+            c = hip_lib.stream_ceiling(r, w, s, trials=trials, iters=iters, settle_ms=20.0)
+            sh = c["shape"]
+            cells.append(f"{c['GBps']:.0f} GB/s ({sh['lanes']}x{sh['vectors_per_lane']}, "
+                         f"{sh['workgroups_per_cu']}/CU{', nt' if sh['nontemporal_stores'] else ''})")
+        lines.append(f"| {r}:{w} | " + " | ".join(cells) + " |")
+        print(f"ceiling {r}:{w} done", file=sys.stderr, flush=True)
+    return "\n".join(lines) + "\n"
+
+
 def run_control_sweep(rows: int = 1024, splits=(2, 4, 8, 16), barriers=(1, 2, 3),
                       warmup: int = 3, iters: int = 20) -> list[dict[str, Any]]:
     """credit_control_overhead over (P, barriers) with the plain ticketed
@@ -212,6 +233,9 @@ def main(argv=None) -> int:
     ap.add_argument("--only", choices=sorted(hip_lib.MICROBENCH),
                     help="run just this microbenchmark (e.g. hbm_copy of --hbm-bytes as the "
                          "known-size reference for PMC byte counters) and print its results")
+    ap.add_argument("--ceilings", metavar="BYTES[,BYTES...]",
+                    help="settled HBM stream ceilings (credit_stream_ceiling) of every built "
+                         "read:write mix at these bytes per call, as a markdown table")
     ap.add_argument("--ffn-reference", action="store_true",
                     help="run the C5 FFN forward twice, then hipBLASLt (torch.matmul) on GEMM1's "
                          "shape twice: the workload of the FFN-against-library counter runs")
@@ -220,6 +244,9 @@ def main(argv=None) -> int:
 
     if args.ffn_reference:
         run_ffn_reference()
+        return 0
+    if args.ceilings:
+        sys.stdout.write(ceiling_table([int(b) for b in args.ceilings.split(",") if b.strip()]))
         return 0
     if args.only:
         res = hip_lib.microbench(args.only, args.hbm_bytes, args.iters)
