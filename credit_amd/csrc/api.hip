@@ -170,8 +170,49 @@ uint32_t next_split_epoch(uint32_t stages) {
   }
 }
 
+std::atomic<uint32_t> g_spin_limit{kSpinLimit};
+
+uint32_t split_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
+
+// One host-mapped word per device, raised by a split launch whose bounded
+// wait expired (common.hpp, split_poll), read by the host without a sync.
+struct HostFlag {
+  int device;
+  volatile uint32_t* host;
+  uint32_t* dev;
+};
+std::mutex g_host_flag_mu;
+std::vector<HostFlag> g_host_flags;
+
+int host_watchdog_flag(int device, HostFlag* out) {
+  std::lock_guard<std::mutex> lock(g_host_flag_mu);
+  for (const HostFlag& f : g_host_flags)
+    if (f.device == device) {
+      *out = f;
+      return CREDIT_OK;
+    }
+  void* p = nullptr;
+  CREDIT_HIP(hipHostMalloc(&p, 64, hipHostMallocMapped));
+  *static_cast<volatile uint32_t*>(p) = 0;
+  void* d = nullptr;
+  CREDIT_HIP(hipHostGetDevicePointer(&d, p, 0));
+  g_host_flags.push_back(HostFlag{device, static_cast<volatile uint32_t*>(p),
+                                  static_cast<uint32_t*>(d)});
+  *out = g_host_flags.back();
+  return CREDIT_OK;
+}
+
 int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
                             int k_values, int ring, size_t extra_bytes, SplitWorkspace* out) {
+  int device = 0;
+  CREDIT_HIP(hipGetDevice(&device));
+  HostFlag flag;
+  CREDIT_TRY(host_watchdog_flag(device, &flag));
+  if (*flag.host != 0)
+    return set_error(CREDIT_ERR_WATCHDOG,
+                     "an earlier split launch on device %d gave up waiting for its group (its "
+                     "outputs are wrong); credit_check_watchdog() reports and clears this",
+                     device);
   if (members * k_values > kMaxExchangeValues)
     return set_error(CREDIT_ERR_UNSUPPORTED,
                      "split of %d members exchanges %d partials per stage (at most %d)", members,
@@ -188,6 +229,7 @@ int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
   out->watchdog = ws_watchdog(base);
   out->slots = ws_slots(base);
   out->extra = ws_scratch(base);
+  out->host_flag = flag.dev;
   return CREDIT_OK;
 }
 
@@ -362,19 +404,40 @@ int credit_check_watchdog(const credit_cfg* cfg) {
     int dev = 0;
     CREDIT_HIP(hipGetDevice(&dev));
     base = workspace_cache().peek(dev, cfg_stream(cfg));
-    if (base == nullptr) return CREDIT_OK;  // no call on this stream used a workspace
+    if (base == nullptr) {  // no call on this stream used a workspace
+      CREDIT_HIP(hipDeviceSynchronize());
+      HostFlag hf;
+      CREDIT_TRY(host_watchdog_flag(dev, &hf));
+      if (*hf.host == 0) return CREDIT_OK;
+      *hf.host = 0;
+      return set_error(CREDIT_ERR_WATCHDOG, "a split-row barrier exceeded its spin limit");
+    }
   }
   uint32_t flag = 0;
   CREDIT_HIP(hipStreamSynchronize(cfg_stream(cfg)));
   CREDIT_HIP(hipMemcpy(&flag, base, sizeof(flag), hipMemcpyDeviceToHost));
+  // The device-wide host word: cleared here, so split calls run again.
+  int device = 0;
+  CREDIT_HIP(hipGetDevice(&device));
+  HostFlag hf;
+  CREDIT_TRY(host_watchdog_flag(device, &hf));
+  const bool device_flag = *hf.host != 0;
+  *hf.host = 0;
   if (flag != 0) {
     // A barrier that gave up leaves its counters mid-protocol: return the
     // whole header and counter area to the zero state.
     CREDIT_HIP(hipMemset(base, 0, kScratchOffset));
     CREDIT_HIP(hipDeviceSynchronize());
+  }
+  if (flag != 0 || device_flag)
     return set_error(CREDIT_ERR_WATCHDOG,
                      "a split-row barrier exceeded its spin limit");
-  }
+  return CREDIT_OK;
+}
+
+int credit_set_spin_limit(uint32_t polls, uint32_t* previous) {
+  const uint32_t old = g_spin_limit.exchange(polls, std::memory_order_relaxed);
+  if (previous != nullptr) *previous = old;
   return CREDIT_OK;
 }
 

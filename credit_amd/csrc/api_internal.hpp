@@ -126,7 +126,10 @@ struct SplitWorkspace {
   uint32_t* watchdog = nullptr;
   uint64_t* slots = nullptr;
   char* extra = nullptr;
+  uint32_t* host_flag = nullptr;  // device address of the device's host-mapped watchdog word
 };
+// Polls a split wait makes before it gives up (credit_set_spin_limit).
+uint32_t split_spin_limit();
 // Scratch bytes (after kScratchOffset) of a split launch, never 0 so that
 // credit_workspace_bytes reports that the launch needs a workspace.
 inline size_t split_workspace_bytes(int64_t groups, int members, int k_values, int ring,

@@ -337,8 +337,9 @@ __device__ __forceinline__ uint32_t counter_read(const uint32_t* counter) {
 // combines them in member order: all members, and every run, get
 // bit-identical results.  Partials travel as fp32 (the block reductions
 // before them are fp64); the combination is fp64.  The poll is bounded: on
-// expiry it raises *watchdog and continues, so a broken launch ends with a
-// reported error instead of a hung GPU.
+// expiry it raises *watchdog (and the device's host-mapped watchdog word)
+// and continues, so a broken launch ends with a reported error instead of a
+// hung GPU.
 constexpr uint32_t kSpinLimit = 1u << 21;  // ~1 s of s_sleep polling
 constexpr int kMaxExchange = kMaxExchangeValues;  // members * values per stage
 static_assert(kMaxExchange <= kWave, "one wave polls a stage's slots");
@@ -351,7 +352,19 @@ struct SplitArgs {
   uint32_t grid;       // gridDim.x, a multiple of kDispensers * members
   uint32_t epoch;      // tag of stage 0; stage s carries epoch + s
   int ring;            // slot rows per group (stages modulo ring)
+  uint32_t spin_limit = kSpinLimit;  // polls before a wait gives up
+  uint32_t* host_flag = nullptr;     // host-mapped word raised with the watchdog
 };
+
+// The product launches' arguments: the process-wide spin limit and the
+// device's host-mapped watchdog word (credit_set_spin_limit, api.hip).
+inline SplitArgs make_split_args(const SplitWorkspace& ws, uint32_t grid, uint32_t epoch,
+                                 int ring) {
+  SplitArgs a{ws.counters, ws.slots, ws.watchdog, grid, epoch, ring};
+  a.spin_limit = split_spin_limit();
+  a.host_flag = ws.host_flag;
+  return a;
+}
 
 struct SplitGroup {
   int group;
@@ -363,6 +376,8 @@ struct SplitGroup {
   uint32_t epoch;
   uint64_t* slots;    // this group's slots
   uint32_t* watchdog;
+  uint32_t spin_limit;
+  uint32_t* host_flag;
 };
 
 // Draw a ticket and derive (group, member).  Every thread calls it; it
@@ -393,6 +408,8 @@ __device__ __forceinline__ SplitGroup split_join(const SplitArgs& a, int members
   g.epoch = a.epoch;
   g.slots = a.slots + static_cast<size_t>(g.group) * a.ring * k_values * members;
   g.watchdog = a.watchdog;
+  g.spin_limit = a.spin_limit;
+  g.host_flag = a.host_flag;
   return g;
 }
 
@@ -428,9 +445,14 @@ __device__ __forceinline__ uint32_t split_poll(const SplitGroup& g, int stage, i
       ok = static_cast<uint32_t>(word >> 32) == tag;
     }
     if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
-    if (++spins > kSpinLimit) {
-      if (lane == 0)
+    if (++spins > g.spin_limit) {
+      if (lane == 0) {
         __hip_atomic_store(g.watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // Also in host memory, so the next split call on this device reports
+        // it without synchronising (api.hip, acquire_split_workspace).
+        if (g.host_flag != nullptr)
+          __hip_atomic_store(g.host_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
       break;
     }
     __builtin_amdgcn_s_sleep(1);

@@ -586,8 +586,8 @@ extern "C" int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamm
     CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 2, kSplitRing, 0, &ws));
     const uint32_t total = static_cast<uint32_t>(groups * plan.members);
     // Two stages per row at most (the second only for offset rows).
-    const SplitArgs sa{ws.counters, ws.slots, ws.watchdog, total,
-                       next_split_epoch(static_cast<uint32_t>(2 * per_group)), kSplitRing};
+    const SplitArgs sa = make_split_args(
+        ws, total, next_split_epoch(static_cast<uint32_t>(2 * per_group)), kSplitRing);
     hipLaunchKernelGGL(sp->fn, dim3(total), dim3(sp->threads), 0, stream, x, gamma, beta, y,
                        mean, rstd, c, static_cast<int>(plan.chunk), plan.members,
                        static_cast<int>(rows), eps, sa);

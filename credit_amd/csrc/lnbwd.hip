@@ -365,9 +365,9 @@ int layernorm_bwd(const T* x, const T* dy, const T* gamma, T* dx, int64_t rows, 
   const uint32_t total = static_cast<uint32_t>(groups * plan.members);
   hipLaunchKernelGGL(pk->fn, dim3(total), dim3(pk->threads), 0, stream, x, dy, gamma, dx, c,
                      static_cast<int>(plan.chunk), plan.members, static_cast<int>(rows), eps,
-                     SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
-                               next_split_epoch(static_cast<uint32_t>(per_group * 2)),
-                               kSplitRing});
+                     make_split_args(ws, total,
+                                     next_split_epoch(static_cast<uint32_t>(per_group * 2)),
+                                     kSplitRing));
   return check_launch("layernorm_bwd_slice_kernel(split)");
 }
 

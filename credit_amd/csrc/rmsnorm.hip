@@ -1027,8 +1027,8 @@ extern "C" int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uin
   SplitWorkspace ws;
   CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 1, kSplitRing, 0, &ws));
   const uint32_t total = static_cast<uint32_t>(groups * plan.members);
-  const SplitArgs sa{ws.counters, ws.slots, ws.watchdog, total,
-                     next_split_epoch(static_cast<uint32_t>(per_group)), kSplitRing};
+  const SplitArgs sa =
+      make_split_args(ws, total, next_split_epoch(static_cast<uint32_t>(per_group)), kSplitRing);
   hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), 0, stream, x, w, y, rstd, c,
                      static_cast<int>(plan.chunk), plan.members, static_cast<int>(rows), eps,
                      sa);
@@ -1097,9 +1097,9 @@ extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
                        pick->lds_bytes(), stream, x, w, dy, rstd, dx, dw_part,
                        static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members,
                        plan.rows_per_group,
-                       SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
-                                 next_split_epoch(static_cast<uint32_t>(plan.rows_per_group)),
-                                 kBwdRing});
+                       make_split_args(ws, total,
+                                       next_split_epoch(static_cast<uint32_t>(plan.rows_per_group)),
+                                       kBwdRing));
     CREDIT_TRY(check_launch("rmsnorm_bwd_group_kernel"));
   } else {
     const BwdPick* pick = pick_for(kBwd, plan.chunk);
@@ -1196,9 +1196,9 @@ extern "C" int credit_rmsnorm_fwd_bwd_bf16(const uint16_t* x, const uint16_t* w,
   hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads + kWave), pick->lds_bytes(),
                      stream, x, w, dy, rstd, y, dx, dw_part, static_cast<int>(rows), c,
                      static_cast<int>(plan.chunk), plan.members, plan.rows_per_group, eps,
-                     SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
-                               next_split_epoch(static_cast<uint32_t>(plan.rows_per_group)),
-                               kBwdRing});
+                     make_split_args(ws, total,
+                                     next_split_epoch(static_cast<uint32_t>(plan.rows_per_group)),
+                                     kBwdRing));
   CREDIT_TRY(check_launch("rmsnorm_fused_group_kernel"));
   const unsigned reduce_blocks = static_cast<unsigned>((cols / 2 + 255) / 256);
   rmsnorm_dw_reduce_kernel<<<dim3(reduce_blocks), dim3(256), 0, stream>>>(

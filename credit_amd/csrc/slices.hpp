@@ -138,9 +138,9 @@ int launch_slices(const credit_cfg* cfg, int64_t rows, const Plan& plan, const P
   SplitWorkspace ws;
   CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, k_values, kSplitRing, 0, &ws));
   const uint32_t total = static_cast<uint32_t>(groups * plan.members);
-  launch(total, SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
-                          next_split_epoch(static_cast<uint32_t>(per_group * stages)),
-                          kSplitRing});
+  launch(total, make_split_args(ws, total,
+                                next_split_epoch(static_cast<uint32_t>(per_group * stages)),
+                                kSplitRing));
   return check_launch(name);
 }
 

@@ -956,8 +956,8 @@ extern "C" int credit_softmax_fwd_f32(const float* x, float* p, float* rowmax, f
     const uint32_t total = static_cast<uint32_t>(groups * plan.members);
     hipLaunchKernelGGL(gk->fn, dim3(total), dim3(threads), 0, stream, x, p, rowmax, lse,
                        static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members, rpg,
-                       SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
-                                 next_split_epoch(static_cast<uint32_t>(rpg)), kGroupRing});
+                       make_split_args(ws, total, next_split_epoch(static_cast<uint32_t>(rpg)),
+                                       kGroupRing));
     return check_launch("softmax_fwd_group_kernel");
   }
   const Pick<FwdFn>* pk = pick_for(kFwd, plan.chunk);
@@ -1006,8 +1006,8 @@ extern "C" int credit_softmax_bwd_f32(const float* p, const float* dy, float* dx
     const uint32_t total = static_cast<uint32_t>(groups * plan.members);
     hipLaunchKernelGGL(gk->fn, dim3(total), dim3(threads), 0, stream, p, dy, dx,
                        static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members, rpg,
-                       SplitArgs{ws.counters, ws.slots, ws.watchdog, total,
-                                 next_split_epoch(static_cast<uint32_t>(rpg)), kGroupRing});
+                       make_split_args(ws, total, next_split_epoch(static_cast<uint32_t>(rpg)),
+                                       kGroupRing));
     return check_launch("softmax_bwd_group_kernel");
   }
   const Pick<BwdFn>* pk = pick_for(kBwd, plan.chunk);

@@ -114,6 +114,7 @@ SIGNATURES: dict[str, list] = {
     "credit_query_device": [ctypes.c_int32, ctypes.POINTER(DeviceInfo)],
     "credit_workspace_bytes": [ctypes.c_int32, _I64, _I64, ctypes.c_int32, ctypes.c_int32],
     "credit_check_watchdog": [_CFG],
+    "credit_set_spin_limit": [ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32)],
     "credit_row_sum_max_f32": [_P, _P, _P, _I64, _I64, _CFG],
     "credit_layernorm_fwd_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_rmsnorm_fwd_bf16": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
@@ -231,6 +232,16 @@ def workspace_bytes(op: str, rows: int, cols: int, variant: str = "auto", split:
 def check_watchdog(cfg: CreditCfg | None = None) -> None:
     cfg = cfg if cfg is not None else make_cfg()
     check(load_library().credit_check_watchdog(ctypes.byref(cfg)), "credit_check_watchdog")
+
+
+def set_spin_limit(polls: int) -> int:
+    """Polls a split launch's bounded wait makes before giving up, for
+    launches enqueued from now on (credit_set_spin_limit); returns the old
+    value.  0 forces the failure path: wrong outputs and CREDIT_ERR_WATCHDOG."""
+    prev = ctypes.c_uint32(0)
+    check(load_library().credit_set_spin_limit(int(polls), ctypes.byref(prev)),
+          "credit_set_spin_limit")
+    return prev.value
 
 
 def _ptr(t: torch.Tensor, name: str, dtype: torch.dtype) -> int:

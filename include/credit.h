@@ -52,10 +52,12 @@
  *    device's CUs to themselves: a kernel on another stream that occupies
  *    CUs meanwhile can delay members until the bounded wait (about 2^21
  *    polls, 1-2 s) expires.  The launch then finishes with wrong outputs
- *    and raises the workspace's watchdog word; the call itself returned
- *    CREDIT_OK when it was enqueued, so callers that run split calls beside
- *    other work check credit_check_watchdog() (CREDIT_ERR_WATCHDOG) after
- *    synchronising.
+ *    and raises the workspace's watchdog word and a host-mapped word of the
+ *    device; the call itself returned CREDIT_OK when it was enqueued.  The
+ *    host word makes it sticky without a synchronisation: once the failed
+ *    launch has run, every later split call on that device refuses with
+ *    CREDIT_ERR_WATCHDOG, until credit_check_watchdog() (which synchronises,
+ *    reports CREDIT_ERR_WATCHDOG and clears both words) is called.
  */
 #ifndef CREDIT_H_
 #define CREDIT_H_
@@ -154,10 +156,20 @@ size_t credit_workspace_bytes(int32_t op, int64_t rows, int64_t cols,
                               int32_t variant, int32_t split);
 
 /* Waits for cfg->stream, then reports CREDIT_ERR_WATCHDOG (and clears the
- * flag) if a split-row barrier of an earlier call on this workspace gave up
- * waiting.  The reference's cluster.sync() cannot time out; this is the
- * host-visible form of the bounded spin that replaces it. */
+ * flags) if a split-row barrier of an earlier call on this workspace -- or
+ * any split launch on this device -- gave up waiting.  The reference's
+ * cluster.sync() cannot time out; this is the host-visible form of the
+ * bounded spin that replaces it. */
 int credit_check_watchdog(const credit_cfg* cfg);
+
+/* Polls a split launch's bounded wait makes before it gives up (default
+ * 2^21, about 1-2 s of polling); applies to launches enqueued afterwards,
+ * process-wide.  0 gives up at the first poll that finds a member's partial
+ * missing: the failure path (wrong outputs, CREDIT_ERR_WATCHDOG) on demand,
+ * for tests and for callers that prefer a fast error to a long wait.
+ * *previous (if not NULL) receives the old value.  No counterpart in the
+ * reference, whose cluster barriers cannot time out. */
+int credit_set_spin_limit(uint32_t polls, uint32_t* previous);
 
 /* ------------------------------------------------ C1: row sum and max ---
  * sum[r] = sum_j x[r, j] (accumulated in fp64, rounded once to fp32) and
