@@ -54,33 +54,43 @@ constexpr int kEpiStore = 4;
 constexpr int kEpiStoreF32 = 5;
 
 // GELU with the tanh approximation, z = sqrt(2/pi) (v + 0.044715 v^3):
-// 0.5 (1 + tanh z) = sigmoid(2z) = 1 - r with r = 1 / (e^(2z) + 1), so
-// GELU(v) = v - v r.  e^(2z) = 2^(2z log2 e) is one hardware exp2 and r one
-// hardware reciprocal (about 1 ulp each): relative error near 1e-6, far
-// below the bf16 rounding of h and du (4e-3) that follows every use here.
-// Saturates correctly: e -> inf gives r = 0 (GELU = v, GELU' = 1), e -> 0
-// gives r = 1 (GELU = 0, GELU' = 0).  Against the correctly rounded division
-// and double-float exp it replaces: GEMM1's epilogue is ~4x cheaper.
+// 0.5 (1 + tanh z) = sigmoid(2z) = s = e r with e = e^(2z) and
+// r = 1 / (e + 1) = 1 - s, so GELU(v) = v s.  e = 2^(2z log2 e) is one
+// hardware exp2 and r one hardware reciprocal (about 1 ulp each); s = e r
+// has no cancellation on either side (1 - r would cancel on the negative
+// tail, where r is within an ulp of 1 below v of about -4), so GELU and
+// GELU' keep a relative error of a few ulp everywhere, far below the bf16
+// rounding of h and du (4e-3) that follows every use.  The exponent is
+// capped at 64 (v above about 6.6): e stays finite, s rounds to 1 and r
+// to 2^-64, so GELU = v and GELU' = 1 up to rounding, and +inf gives +inf.
+// Against the correctly rounded division and double-float exp it replaces:
+// GEMM1's epilogue is ~4x cheaper.
 constexpr float kGeluC = 0.7978845608028654f;   // sqrt(2/pi)
 constexpr float kGeluC2 = 2.302208198144325f;   // 2 sqrt(2/pi) log2(e)
 constexpr float kGeluA = 0.044715f;
 
-__device__ __forceinline__ float gelu_sigmoid_r(float v, float v2) {
-  const float e = __builtin_amdgcn_exp2f(kGeluC2 * v * __builtin_fmaf(kGeluA, v2, 1.0f));
-  return __builtin_amdgcn_rcpf(e + 1.0f);
+struct GeluParts {
+  float r;  // 1 / (e + 1) = 1 - s
+  float s;  // sigmoid(2z) = 0.5 (1 + tanh z)
+};
+
+__device__ __forceinline__ GeluParts gelu_parts(float v, float v2) {
+  const float arg = kGeluC2 * v * __builtin_fmaf(kGeluA, v2, 1.0f);
+  const float e = __builtin_amdgcn_exp2f(arg < 64.0f ? arg : 64.0f);
+  GeluParts g;
+  g.r = __builtin_amdgcn_rcpf(e + 1.0f);
+  g.s = e * g.r;
+  return g;
 }
 
-__device__ __forceinline__ float gelu_tanh(float v) {
-  const float r = gelu_sigmoid_r(v, v * v);
-  return __builtin_fmaf(-v, r, v);
-}
+__device__ __forceinline__ float gelu_tanh(float v) { return v * gelu_parts(v, v * v).s; }
 
-// d/dv GELU = s + 2 v r s dz/dv with s = 1 - r, dz/dv = sqrt(2/pi) (1 + 3 * 0.044715 v^2).
+// d/dv GELU = s + 2 v r s dz/dv, dz/dv = sqrt(2/pi) (1 + 3 * 0.044715 v^2).
 __device__ __forceinline__ float gelu_tanh_grad(float v) {
   const float v2 = v * v;
-  const float r = gelu_sigmoid_r(v, v2);
-  const float s = 1.0f - r;
-  return __builtin_fmaf(2.0f * kGeluC * v * r * s, __builtin_fmaf(3.0f * kGeluA, v2, 1.0f), s);
+  const GeluParts g = gelu_parts(v, v2);
+  return __builtin_fmaf(2.0f * kGeluC * v * g.r * g.s, __builtin_fmaf(3.0f * kGeluA, v2, 1.0f),
+                        g.s);
 }
 
 // One output element of every epilogue.  s is the row scale still to apply

@@ -247,9 +247,19 @@ def pearson_backward(x, y, grad, eps: float = 1.0e-6):
 # -------------------------------------------------------------------- FFN --
 
 
+def _sigmoid(a):
+    """1 / (1 + e^-a) without overflow or cancellation on either side."""
+    ea = np.exp(-np.abs(a))
+    return np.where(a >= 0, 1.0 / (1.0 + ea), ea / (1.0 + ea))
+
+
 def gelu_tanh(v):
+    """0.5 v (1 + tanh z), z = sqrt(2/pi) (v + 0.044715 v^3), evaluated as
+    v * sigmoid(2z) (the same function: 0.5 (1 + tanh z) = sigmoid(2z)), so
+    the negative tail keeps its relative accuracy where 1 + tanh z would
+    cancel in float64 (v below about -6)."""
     v = f64(v)
-    return 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v**3)))
+    return v * _sigmoid(2.0 * np.sqrt(2.0 / np.pi) * (v + 0.044715 * v**3))
 
 
 def ffn_rmsnorm_gelu(x, w1, w2, eps: float = 1.0e-6, round_h: bool = True):
@@ -269,11 +279,14 @@ def ffn_rmsnorm_gelu(x, w1, w2, eps: float = 1.0e-6, round_h: bool = True):
 
 def gelu_tanh_grad(v):
     """d/dv of gelu_tanh: 0.5 (1 + tanh z) + 0.5 v (1 - tanh^2 z) dz/dv,
-    z = sqrt(2/pi) (v + 0.044715 v^3)."""
+    z = sqrt(2/pi) (v + 0.044715 v^3); with s = sigmoid(2z) = 0.5 (1 + tanh z)
+    and r = 1 - s = sigmoid(-2z), 0.5 (1 - tanh^2 z) = 2 s r, so the
+    derivative is s + 2 v s r dz/dv, free of cancellation on both tails."""
     v = f64(v)
     c = np.sqrt(2.0 / np.pi)
-    t = np.tanh(c * (v + 0.044715 * v**3))
-    return 0.5 * (1.0 + t) + 0.5 * v * (1.0 - t * t) * c * (1.0 + 3.0 * 0.044715 * v * v)
+    z2 = 2.0 * c * (v + 0.044715 * v**3)
+    s, r = _sigmoid(z2), _sigmoid(-z2)
+    return s + 2.0 * v * s * r * c * (1.0 + 3.0 * 0.044715 * v * v)
 
 
 def ffn_rmsnorm_gelu_backward(x, w1, w2, dout, eps: float = 1.0e-6, rounding: bool = True):

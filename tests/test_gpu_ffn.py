@@ -82,6 +82,27 @@ def test_ffn_structured_inputs_pin_layout(gpu, rows, d):
     np.testing.assert_allclose(out, oracle(x, w1, w2), **BF16)
 
 
+@pytest.mark.parametrize("rows", [128, 2048])
+def test_ffn_gelu_negative_tail(gpu, rows):
+    """GELU far out on its negative tail, where 0.5 (1 + tanh z) is a tiny
+    sigmoid and 1 - r would cancel: x = 1 (a = x rstd = 1), W1 = -diag(c)
+    with c from 3 to 9 (h = GELU(-c) from -4e-3 down to -1e-28) and W2 =
+    diag(2 / |GELU(-c)|), so out = 1 + h * 2 / |h| = -1 where h keeps its
+    relative accuracy and 1 where it was flushed to zero.  rows 128 takes the
+    128-tile kernels, 2048 the 256-tile ones."""
+    d = 256
+    c = np.linspace(3.0, 9.0, d)
+    w1 = torch.from_numpy(-np.diag(c)).to(torch.bfloat16)
+    cb = -w1.float().numpy().diagonal().astype(np.float64)  # c as bf16 holds it
+    g = ref.gelu_tanh(-cb)
+    w2 = torch.from_numpy(np.diag(2.0 / np.abs(g))).to(torch.bfloat16)
+    x = torch.ones(rows, d, dtype=torch.bfloat16)
+    out = run_ffn(x, w1, w2, gpu)
+    expect = oracle(x, w1, w2)
+    assert np.all(np.abs(expect + 1.0) < 2e-2)  # the oracle itself sees h
+    np.testing.assert_allclose(out, expect, **BF16)
+
+
 def test_ffn_rejects_unsupported_shapes(gpu):
     x, w1, w2 = make(100, 128, 128, seed=3)
     with pytest.raises(hip_lib.CreditError) as err:

@@ -334,3 +334,29 @@ def test_reference_init_restatements():
     assert dy[0, 1] == np.float32((346 & 4095) / 2048 - 1)
     x, y, grad = ref.pearson_backward_init(18, 1)
     assert grad.shape == (18, 1) and grad[17, 0] == np.float32(0.75) and grad[16, 0] == np.float32(0.75 + 16 * 0.03125)
+
+
+def test_gelu_tanh_pinned_to_torch_and_on_its_tails():
+    """gelu_tanh / gelu_tanh_grad against torch's float64 tanh-form GELU on
+    [-6, 6], and on the tails (where 1 + tanh z cancels in float64) against
+    the same formula evaluated with 60-digit decimals."""
+    import decimal
+
+    v = np.linspace(-6.0, 6.0, 2001)
+    tv = torch.tensor(v, dtype=torch.float64, requires_grad=True)
+    tg = F.gelu(tv, approximate="tanh")
+    tg.sum().backward()
+    np.testing.assert_allclose(ref.gelu_tanh(v), tg.detach().numpy(), rtol=1e-13, atol=1e-15)
+    # torch evaluates 1 - tanh^2 and 1 + tanh directly: absolute agreement on the tail
+    np.testing.assert_allclose(ref.gelu_tanh_grad(v), tv.grad.numpy(), rtol=1e-12, atol=1e-14)
+
+    ctx = decimal.Context(prec=60)
+    c = ctx.sqrt(decimal.Decimal(2) / ctx.divide(decimal.Decimal(
+        "3.14159265358979323846264338327950288419716939937510582097494"), 1))
+    for x in (-7.0, -9.0, -12.0, 8.0):
+        d = decimal.Decimal(x)
+        z = c * (d + decimal.Decimal("0.044715") * d * d * d)
+        e2 = ctx.exp(2 * z)
+        tanh = (e2 - 1) / (e2 + 1)
+        exact = float(decimal.Decimal("0.5") * d * (1 + tanh))
+        assert ref.gelu_tanh(np.array([x]))[0] == pytest.approx(exact, rel=1e-12)
