@@ -51,8 +51,9 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 # Workloads whose tensors are bf16 (fp32 accumulation); the rest compute in fp32.
-BF16_WORKLOADS = ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd", "ffn", "ffn_backward",
-                  "layernorm_backward_bf16")
+BF16_WORKLOADS = ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd", "ffn", "ffn_baseline_layout",
+                  "ffn_backward", "layernorm_backward_bf16")
+FFN_WORKLOADS = ("ffn", "ffn_baseline_layout", "ffn_backward")
 
 # Kernels one AUTO call launches at the BASELINE shape (names as rocprofv3
 # reports them) and the source file they are built from; the committed PMC
@@ -71,7 +72,10 @@ CALL_KERNELS = {
     "softmax_fwd": ("softmax.hip", ["softmax_fwd_group_kernel<512, 8>"]),
     "softmax_bwd": ("softmax.hip", ["softmax_bwd_group_kernel<512, 4>"]),
     "softmax_logits_backward": ("softmax.hip", ["softmax_logits_bwd_slice_kernel<1024, 8>"]),
-    "ffn": ("ffn.hip", ["ffn_rstd_kernel", "ffn_gemm256_kernel<0>", "ffn_gemm256_kernel<1>"]),
+    "ffn": ("ffn.hip", ["ffn_rstd_kernel", "ffn_gemm256_kernel<0, false>",
+                        "ffn_gemm256_kernel<1, false>"]),
+    "ffn_baseline_layout": ("ffn.hip", ["ffn_rstd_kernel", "ffn_gemm256_kernel<0, true>",
+                                        "ffn_gemm256_kernel<1, true>"]),
     "layernorm_backward": ("lnbwd.hip", ["layernorm_bwd_slice_kernel<float, 1024, 8>"]),
     "layernorm_backward_bf16": ("lnbwd.hip",
                                 ["layernorm_bwd_slice_kernel<unsigned short, 512, 8>"]),
@@ -215,7 +219,7 @@ def cpu_baseline(name, cpu_inputs, spec, seconds):
     t0 = time.perf_counter()
     fn(*args)
     one = time.perf_counter() - t0
-    while one > seconds / 4 and sample_rows > 8 and name not in ("ffn", "ffn_backward"):
+    while one > seconds / 4 and sample_rows > 8 and name not in FFN_WORKLOADS:
         sample_rows //= 2
         args = tuple(a[:sample_rows] if a.dim() == 2 and a.shape[0] == rows else a for a in args)
         if name == "rmsnorm_bwd":
@@ -233,7 +237,7 @@ def cpu_baseline(name, cpu_inputs, spec, seconds):
             break
     runs.sort()
     med = runs[len(runs) // 2]
-    if name in ("ffn", "ffn_backward"):
+    if name in FFN_WORKLOADS:
         work = spec_ffn_flops(sample_rows, cpu_inputs[0].shape[1], name)
         value, unit = work / med / 1e12, "TFLOP/s"
     else:
@@ -281,7 +285,7 @@ def measure(name, args, hip_lib, torch, dev, with_cpu):
     traffic, traffic_note = measured_traffic(name)
     out = {"rows": spec.rows, "cols": spec.cols, "ms_per_step": round(ms_step, 6),
            "kernel_ms": round(kernel_ms, 6), "trials": trials.as_dict(), "watchdog": "ok"}
-    if name in ("ffn", "ffn_backward"):
+    if name in FFN_WORKLOADS:
         flops = spec_ffn_flops(spec.rows, spec.cols, name)
         achieved = flops / (kernel_ms * 1e-3) / 1e12
         out.update(metric="MFMA TFLOP/s", value=round(flops / (ms_step * 1e-3) / 1e12, 2),

@@ -154,10 +154,15 @@ __global__ __launch_bounds__(256) void ffn_rstd_kernel(const uint16_t* __restric
 }
 
 // C[m, n] = epi(sum_k A[m, k] * B[n, k]).  A [M, K] and B [N, K] row-major
-// bf16; M % 128 == 0, N % 128 == 0, K % 64 == 0 (checked on the host).
+// bf16 (KN: B [K, N], element (n, k) at B[k * N + n]); M % 128 == 0,
+// N % 128 == 0, K % 64 == 0 (checked on the host).
 //  kEpiGelu:     A rows scaled by a_scale[m] on load; C = bf16(gelu(acc)).
 //  kEpiResidual: C = bf16(acc + R[m, n]).
-template <int EPI>
+// KN: thread t stages 16-byte chunk t % 16 (8 columns) of K-rows t / 16 +
+// 16 i of the 64 x 128 B tile and scatters its 8 values into the [n][k]
+// LDS tile (2-byte stores; this kernel only serves shapes the 256-tile
+// kernel does not take).
+template <int EPI, bool KN>
 __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
     const uint16_t* __restrict__ A, const float* __restrict__ a_scale,
     const uint16_t* __restrict__ B, const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
@@ -187,9 +192,12 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
   for (int i = 0; i < 4; ++i) {
     const int r = ld_row + 32 * i;
     a_src[i] = reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m0 + r) * K) + ld_chunk;
-    b_src[i] = reinterpret_cast<const u32x4*>(B + static_cast<size_t>(n0 + r) * K) + ld_chunk;
+    b_src[i] = KN ? reinterpret_cast<const u32x4*>(B + static_cast<size_t>((tid >> 4) + 16 * i) * N +
+                                                   n0) + (tid & 15)
+                  : reinterpret_cast<const u32x4*>(B + static_cast<size_t>(n0 + r) * K) + ld_chunk;
     scale[i] = kScaleA ? a_scale[m0 + r] : 1.0f;
   }
+  const size_t b_step = KN ? static_cast<size_t>(kBK) * N / 8 : kBK / 8;  // u32x4 per K-step
   u32x4 ra[4], rb[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -213,15 +221,25 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
       const int r = ld_row + 32 * i;
       const u32x4 av = kScaleA ? scale_bf16x8(ra[i], scale[i]) : ra[i];
       *reinterpret_cast<u32x4*>(&As[r * kLdsStride + ld_chunk * 8]) = av;
-      *reinterpret_cast<u32x4*>(&Bs[r * kLdsStride + ld_chunk * 8]) = rb[i];
+      if constexpr (KN) {
+        const int kr = (tid >> 4) + 16 * i, n8 = (tid & 15) * 8;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          Bs[(n8 + 2 * e) * kLdsStride + kr] = static_cast<uint16_t>(rb[i][e] & 0xffffu);
+          Bs[(n8 + 2 * e + 1) * kLdsStride + kr] = static_cast<uint16_t>(rb[i][e] >> 16);
+        }
+      } else {
+        *reinterpret_cast<u32x4*>(&Bs[r * kLdsStride + ld_chunk * 8]) = rb[i];
+      }
     }
     __syncthreads();
     if (ks + 1 < ksteps) {  // prefetch the next K-step into registers
       const int off = (ks + 1) * (kBK / 8);
+      const size_t boff = (ks + 1) * b_step;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         ra[i] = a_src[i][off];
-        rb[i] = b_src[i][off];
+        rb[i] = b_src[i][boff];
       }
     }
 #pragma unroll
@@ -363,11 +381,33 @@ constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+
+// ds_read_b64_tr_b16 at the LDS location of p (a pointer into smem).
+__device__ __forceinline__ bf16x4_t ds_read_tr16(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      reinterpret_cast<lds_bf16x4_t*>((lds_ptr_t)(const_cast<char*>(p))));
+}
 
 // Loads per thread per K-step: 16 (8 of A, 8 of B).  Load q of wave w fills
 // rows 8 b .. 8 b + 7 of operand q >> 3, b = (q & 7) * 4 + w.
+//
+// KN: B is stored [K, N] (N contiguous: the [in, out] weight layout, W1
+// [d, f] and W2 [f, d]) instead of [N, K].  Its stage is then 64 K-rows of
+// 512 bytes (256 columns); load q >= 8 of wave w fills K-rows 8 (q & 7) + 2 w
+// and + 1 (one 1 KiB wave instruction), lane l writing 16-byte chunk l % 32
+// of row 2 w + l / 32.  Chunk c of K-row r sits at position c ^ 4 (r & 3).
+// A B fragment (8 consecutive k of one column per lane) is then gathered by
+// two ds_read_b64_tr_b16: within each 16-lane group, result lane 4 a + b
+// takes 16-bit word b of the 8-byte pieces addressed by group lanes a,
+// a + 4, a + 8, a + 12.  Group lane j addresses K-row k0 + j / 4 and
+// columns c0 + 4 (j % 4) .. + 3, so lane j receives column c0 + j at
+// K-rows k0 .. k0 + 3 -- the MFMA B operand's layout.  The 32 lanes of one
+// half-wave read 4 K-rows x 64 bytes, which the swizzle spreads over all
+// 64 banks.
 
-template <int EPI>
+template <int EPI, bool KN>
 __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     const uint16_t* __restrict__ A, const float* __restrict__ scale,
     const uint16_t* __restrict__ B, const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
@@ -400,9 +440,16 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
   // lane-dependent part of the byte offset is one VGPR; row block (q & 7)
   // * 32 rows and the K step go into the scalar offset.
   const buffer_rsrc_t rsrc_a = make_rsrc(A + static_cast<size_t>(m0) * K, 256u * K * 2u);
-  const buffer_rsrc_t rsrc_b = make_rsrc(B + static_cast<size_t>(n0) * K, 256u * K * 2u);
+  // KN: columns n0 .. n0 + 255 of K rows of pitch N (the host keeps K N 2
+  // within 32 bits).
+  const buffer_rsrc_t rsrc_b =
+      KN ? make_rsrc(B + n0, static_cast<uint32_t>((static_cast<size_t>(K - 1) * N + 256) * 2))
+         : make_rsrc(B + static_cast<size_t>(n0) * K, 256u * K * 2u);
   const int chunk = (lane & 7) ^ (((wave & 1) << 2) + (lane >> 4));
   const uint32_t voff = static_cast<uint32_t>(((wave * 8 + (lane >> 3)) * K + chunk * 8) * 2);
+  const int kn_row = 2 * wave + (lane >> 5);  // K-row of the stage mod 8 (KN loads)
+  const uint32_t voff_kn = static_cast<uint32_t>(
+      (kn_row * N + (((lane & 31) ^ ((kn_row & 3) << 2)) * 8)) * 2);
   // LDS byte address of smem (an address-space cast; C++ casts do not express it).
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
   const uint32_t m0_wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
@@ -414,12 +461,15 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     const int stage_off = q < 8 ? (k & 1) * kBigTile : kBigBBase + (k % kBigBRing) * kBigTile;
     const uint32_t base = static_cast<uint32_t>(
         __builtin_amdgcn_readfirstlane(static_cast<int>(m0_wave + stage_off)));
-    const uint32_t soff = static_cast<uint32_t>(
-        __builtin_amdgcn_readfirstlane(kc * kBigK * 2 + (q & 7) * 64 * K));
+    const uint32_t soff_nk = static_cast<uint32_t>(kc * kBigK * 2 + (q & 7) * 64 * K);
+    const uint32_t soff_kn =
+        (static_cast<uint32_t>(kc * kBigK + (q & 7) * 8) * static_cast<uint32_t>(N)) * 2u;
+    const uint32_t soff = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+        static_cast<int>(KN && q >= 8 ? soff_kn : soff_nk)));
     if constexpr (q < 8)
       load_to_lds<qoff>(rsrc_a, voff, base, soff);
     else
-      load_to_lds<qoff>(rsrc_b, voff, base, soff);
+      load_to_lds<qoff>(rsrc_b, KN ? voff_kn : voff, base, soff);
   };
 
   // Fragment reads: A rows wm*128 + i*32 + (l & 31), B rows wn*128 + j*32 +
@@ -428,12 +478,24 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
   const int fsw = ((lane & 31) >> 1) & 7;
   const int a_frag = (wm * 128 + (lane & 31)) * 128;
   const int b_frag = (wn * 128 + (lane & 31)) * 128;
+  // KN fragment j of sub-step kk: group lane j' = l % 16 of group g = (l / 16)
+  // % 4 addresses K-row 16 kk + 8 (g / 2) + s (s = j' / 4; + 4 for the
+  // second read) and logical chunk 16 wn + 4 j + 2 (g & 1) + (j' / 2) % 2,
+  // byte 8 (j' % 2) of it, which sits at position 16 wn + 4 (j ^ s) + ...
+  const int kn_g = (lane >> 4) & 3, kn_s = (lane & 15) >> 2;
+  const int kn_lane = (8 * (kn_g >> 1) + kn_s) * 512 +
+                      (wn * 16 + 2 * (kn_g & 1) + ((lane >> 1) & 1)) * 16 + 8 * (lane & 1);
   struct Frags { bf16x8_t a[4], b[4]; };
   // step: the K-step whose stages are read (A stage step & 1, B stage step % 3).
   auto frag = [&](int step, int kk, int idx) {
     const int c = ((2 * kk + (lane >> 5)) ^ fsw) << 4;
     const char* abase = smem + (step & 1) * kBigTile;
     const char* bbase = smem + kBigBBase + __builtin_amdgcn_readfirstlane(step % kBigBRing) * kBigTile;
+    if (KN && idx >= 4) {
+      const char* p = bbase + kn_lane + (((idx - 4) ^ kn_s) << 6) + kk * 8192;
+      return __builtin_shufflevector(ds_read_tr16(p), ds_read_tr16(p + 2048), 0, 1, 2, 3, 4, 5,
+                                     6, 7);
+    }
     return idx < 4 ? *reinterpret_cast<const bf16x8_t*>(abase + a_frag + idx * 4096 + c)
                    : *reinterpret_cast<const bf16x8_t*>(bbase + b_frag + (idx - 4) * 4096 + c);
   };
@@ -469,8 +531,13 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
       (mfma.template operator()<Q0, NL, Ms>(cur, nxt, ns, nkk, lk), ...);
     }(std::make_integer_sequence<int, 16>{});
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 4; ++q) {
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {  // a KN B fragment is two reads
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, KN ? 2 : 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
@@ -692,42 +759,45 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 
 // The 256-tile kernels take 160 KiB of dynamic LDS; allow it once per
 // process (the attribute belongs to the kernel, not to a device).
-template <int EPI>
+template <int EPI, bool KN>
 hipError_t allow_big_lds() {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(ffn_gemm256_kernel<EPI>),
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(ffn_gemm256_kernel<EPI, KN>),
                              hipFuncAttributeMaxDynamicSharedMemorySize, kBigLds);
 }
+template <bool KN>
 int enable_big_lds() {
   static int status = [] {
-    for (const hipError_t e : {allow_big_lds<kEpiGelu>(), allow_big_lds<kEpiResidual>(),
-                               allow_big_lds<kEpiUH>(), allow_big_lds<kEpiGeluBwd>(),
-                               allow_big_lds<kEpiStore>(), allow_big_lds<kEpiStoreF32>()})
+    for (const hipError_t e :
+         {allow_big_lds<kEpiGelu, KN>(), allow_big_lds<kEpiResidual, KN>(),
+          allow_big_lds<kEpiUH, KN>(), allow_big_lds<kEpiGeluBwd, KN>(),
+          allow_big_lds<kEpiStore, KN>(), allow_big_lds<kEpiStoreF32, KN>()})
       if (e != hipSuccess) return hip_failure(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
     return static_cast<int>(CREDIT_OK);
   }();
   return status;
 }
 
-// C[M, N] = epi(A[M, K] B[N, K]^T): the 256-tile kernel when M and N are
-// multiples of 256, K a multiple of 128 (an even number of 64-wide K-steps),
-// the tile count a multiple of the 8 XCDs and a 256-row operand tile
-// (256 * K * 2 bytes) and the epilogue's R tile ((255 * N + 256) * 2 bytes)
-// fit a buffer resource; otherwise the 128-tile kernel (M, N multiples of
-// 128, K of 64).
-template <int EPI>
+// C[M, N] = epi(A[M, K] B^T) with B [N, K] (KN false) or [K, N] (KN true):
+// the 256-tile kernel when M and N are multiples of 256, K a multiple of
+// 128 (an even number of 64-wide K-steps), the tile count a multiple of the
+// 8 XCDs and a B tile (256 * K * 2 bytes, KN: (K - 1) * N * 2 + 512), an A
+// tile and the epilogue's R tile ((255 * N + 256) * 2 bytes) fit a buffer
+// resource; otherwise the 128-tile kernel (M, N multiples of 128, K of 64).
+template <int EPI, bool KN = false>
 int launch_gemm(const uint16_t* A, const float* scale, const uint16_t* B, const uint16_t* R,
                 uint16_t* C, uint16_t* C2, float* Cf, int M, int N, int K, hipStream_t stream,
                 const char* name) {
   const bool big = M % kBig == 0 && N % kBig == 0 && K % (2 * kBigK) == 0 &&
-                   ((M / kBig) * (N / kBig)) % 8 == 0 && K <= (1 << 22) && N <= (1 << 22);
+                   ((M / kBig) * (N / kBig)) % 8 == 0 && K <= (1 << 22) && N <= (1 << 22) &&
+                   (!KN || static_cast<uint64_t>(K) * N * 2 < (uint64_t{1} << 32));
   if (big) {
-    CREDIT_TRY(enable_big_lds());
-    ffn_gemm256_kernel<EPI><<<dim3(static_cast<unsigned>((M / kBig) * (N / kBig))),
-                              dim3(kBigThreads), kBigLds, stream>>>(A, scale, B, R, C, C2, Cf,
-                                                                     M, N, K);
+    CREDIT_TRY(enable_big_lds<KN>());
+    ffn_gemm256_kernel<EPI, KN><<<dim3(static_cast<unsigned>((M / kBig) * (N / kBig))),
+                                  dim3(kBigThreads), kBigLds, stream>>>(A, scale, B, R, C, C2,
+                                                                         Cf, M, N, K);
   } else {
-    ffn_gemm_kernel<EPI><<<dim3(static_cast<unsigned>((M / kBM) * (N / kBN))), dim3(kThreads), 0,
-                           stream>>>(A, scale, B, R, C, C2, Cf, M, N, K);
+    ffn_gemm_kernel<EPI, KN><<<dim3(static_cast<unsigned>((M / kBM) * (N / kBN))),
+                               dim3(kThreads), 0, stream>>>(A, scale, B, R, C, C2, Cf, M, N, K);
   }
   return check_launch(name);
 }
@@ -742,10 +812,10 @@ int launch_transpose(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t c
 }
 
 // Backward workspace, in order (each region 256-byte aligned): rstd [M]
-// fp32; u, du [M, f] and h^T, du^T [f, M] bf16; W1^T [d, f] and W2^T [f, d]
-// bf16; dout^T, a^T [d, M] bf16; da [M, d] fp32.
+// fp32; u, du [M, f] and h^T, du^T [f, M] bf16; dout^T, a^T [d, M] bf16;
+// da [M, d] fp32.
 struct BwdLayout {
-  size_t rstd, u, du, ht, dut, w1t, w2t, doutt, at, da, total;
+  size_t rstd, u, du, ht, dut, doutt, at, da, total;
 };
 BwdLayout bwd_layout(int64_t M, int64_t d, int64_t f) {
   BwdLayout l;
@@ -760,8 +830,6 @@ BwdLayout bwd_layout(int64_t M, int64_t d, int64_t f) {
   l.du = take(M * f * 2);
   l.ht = take(M * f * 2);
   l.dut = take(M * f * 2);
-  l.w1t = take(d * f * 2);
-  l.w2t = take(d * f * 2);
   l.doutt = take(M * d * 2);
   l.at = take(M * d * 2);
   l.da = take(M * d * sizeof(float));
@@ -811,10 +879,14 @@ extern "C" int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t
   return launch_transpose(src, dst, rows, cols, nullptr, cfg_stream(cfg));
 }
 
-extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w1,
-                                            const uint16_t* w2, uint16_t* out, int64_t rows,
-                                            int64_t d, int64_t f, float eps,
-                                            const credit_cfg* cfg) {
+namespace credit {
+namespace {
+
+// The forward for either weight layout: KN false takes w1 [f, d], w2 [d, f]
+// (nn.Linear), KN true w1 [d, f], w2 [f, d] ([in, out]).
+template <bool KN>
+int ffn_forward(const uint16_t* x, const uint16_t* w1, const uint16_t* w2, uint16_t* out,
+                int64_t rows, int64_t d, int64_t f, float eps, const credit_cfg* cfg) {
   CREDIT_TRY(check_row_ptr(x, "x", rows));
   CREDIT_TRY(check_ptr(w1, "w1"));
   CREDIT_TRY(check_ptr(w2, "w2"));
@@ -834,10 +906,27 @@ extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w
   const int M = static_cast<int>(rows), D = static_cast<int>(d), F = static_cast<int>(f);
   ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, D, eps);
   CREDIT_TRY(check_launch("ffn_rstd_kernel"));
-  CREDIT_TRY(launch_gemm<kEpiGelu>(x, rstd, w1, nullptr, h, nullptr, nullptr, M, F, D, stream,
-                                   "ffn gemm1 (gelu)"));
-  return launch_gemm<kEpiResidual>(h, nullptr, w2, x, out, nullptr, nullptr, M, D, F, stream,
-                                   "ffn gemm2 (residual)");
+  CREDIT_TRY((launch_gemm<kEpiGelu, KN>(x, rstd, w1, nullptr, h, nullptr, nullptr, M, F, D,
+                                       stream, "ffn gemm1 (gelu)")));
+  return launch_gemm<kEpiResidual, KN>(h, nullptr, w2, x, out, nullptr, nullptr, M, D, F, stream,
+                                       "ffn gemm2 (residual)");
+}
+
+}  // namespace
+}  // namespace credit
+
+extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w1,
+                                            const uint16_t* w2, uint16_t* out, int64_t rows,
+                                            int64_t d, int64_t f, float eps,
+                                            const credit_cfg* cfg) {
+  return ffn_forward<false>(x, w1, w2, out, rows, d, f, eps, cfg);
+}
+
+extern "C" int credit_ffn_rmsnorm_gelu_kn_bf16(const uint16_t* x, const uint16_t* w1,
+                                               const uint16_t* w2, uint16_t* out, int64_t rows,
+                                               int64_t d, int64_t f, float eps,
+                                               const credit_cfg* cfg) {
+  return ffn_forward<true>(x, w1, w2, out, rows, d, f, eps, cfg);
 }
 
 extern "C" int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_t* w1,
@@ -883,34 +972,32 @@ extern "C" int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_
   uint16_t* du = reinterpret_cast<uint16_t*>(b + L.du);
   uint16_t* ht = reinterpret_cast<uint16_t*>(b + L.ht);
   uint16_t* dut = reinterpret_cast<uint16_t*>(b + L.dut);
-  uint16_t* w1t = reinterpret_cast<uint16_t*>(b + L.w1t);
-  uint16_t* w2t = reinterpret_cast<uint16_t*>(b + L.w2t);
   uint16_t* doutt = reinterpret_cast<uint16_t*>(b + L.doutt);
   uint16_t* at = reinterpret_cast<uint16_t*>(b + L.at);
   float* da = reinterpret_cast<float*>(b + L.da);
   const int M = static_cast<int>(rows), D = static_cast<int>(d), F = static_cast<int>(f);
   ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, D, eps);
   CREDIT_TRY(check_launch("ffn_rstd_kernel"));
-  // Operands in the K-contiguous layout the GEMM reads.
-  CREDIT_TRY(launch_transpose(w1, w1t, F, D, nullptr, stream));    // W1^T [d, f]
-  CREDIT_TRY(launch_transpose(w2, w2t, D, F, nullptr, stream));    // W2^T [f, d]
+  // The A operands of the weight gradients in the K-contiguous layout A
+  // takes (the weights themselves are read as [K, N] B operands).
   CREDIT_TRY(launch_transpose(dout, doutt, M, D, nullptr, stream));
   CREDIT_TRY(launch_transpose(x, at, M, D, rstd, stream));         // a^T = bf16(x rstd)^T
   // u = (x W1^T) rstd, h^T = GELU(u)^T.
   CREDIT_TRY(launch_gemm<kEpiUH>(x, rstd, w1, nullptr, u, ht, nullptr, M, F, D, stream,
                                  "ffn bwd gemm u"));
-  // du = (dout W2) * GELU'(u), and du^T.
-  CREDIT_TRY(launch_gemm<kEpiGeluBwd>(dout, nullptr, w2t, u, du, dut, nullptr, M, F, D, stream,
-                                      "ffn bwd gemm du"));
+  // du = (dout W2) * GELU'(u), and du^T; W2 [d, f] is B as [K, N].
+  CREDIT_TRY((launch_gemm<kEpiGeluBwd, true>(dout, nullptr, w2, u, du, dut, nullptr, M, F, D,
+                                            stream, "ffn bwd gemm du")));
   // dW2 [d, f] = dout^T h.
   CREDIT_TRY(launch_gemm<kEpiStore>(doutt, nullptr, ht, nullptr, dw2, nullptr, nullptr, D, F, M,
                                     stream, "ffn bwd gemm dw2"));
   // dW1 [f, d] = du^T a.
   CREDIT_TRY(launch_gemm<kEpiStore>(dut, nullptr, at, nullptr, dw1, nullptr, nullptr, F, D, M,
                                     stream, "ffn bwd gemm dw1"));
-  // da [M, d] = du W1 (fp32), then dx = dout + RMSNorm backward of da.
-  CREDIT_TRY(launch_gemm<kEpiStoreF32>(du, nullptr, w1t, nullptr, nullptr, nullptr, da, M, D, F,
-                                       stream, "ffn bwd gemm da"));
+  // da [M, d] = du W1 (fp32; W1 [f, d] is B as [K, N]), then dx = dout +
+  // RMSNorm backward of da.
+  CREDIT_TRY((launch_gemm<kEpiStoreF32, true>(du, nullptr, w1, nullptr, nullptr, nullptr, da, M, D,
+                                             F, stream, "ffn bwd gemm da")));
   ffn_dx_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, da, dout, dx, D);
   return check_launch("ffn_dx_kernel");
 }

@@ -129,6 +129,7 @@ SIGNATURES: dict[str, list] = {
     "credit_weighted_var_bwd_f32": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_pearson_bwd_f32": [_P, _P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_ffn_rmsnorm_gelu_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
+    "credit_ffn_rmsnorm_gelu_kn_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
     "credit_ffn_rmsnorm_gelu_bwd_bf16": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
     "credit_ffn_bwd_workspace_bytes": [_I64, _I64, _I64],
     "credit_layernorm_bwd_f32": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
@@ -528,19 +529,29 @@ def layernorm_backward(x: torch.Tensor, dy: torch.Tensor, gamma: torch.Tensor,
 
 
 def ffn(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, out: torch.Tensor, eps: float,
-        cfg: CreditCfg) -> None:
-    """out = x + GELU_tanh(RMSNorm(x) @ w1.T) @ w2.T; w1 [f, d], w2 [d, f]."""
+        cfg: CreditCfg, layout: str = "linear") -> None:
+    """out = x + GELU_tanh(RMSNorm(x) W1) W2.  layout "linear": the nn.Linear
+    layout, w1 [f, d] and w2 [d, f] (out = ... @ w1.T ... @ w2.T); layout
+    "in_out": w1 [d, f] and w2 [f, d] as the BASELINE gives them
+    (credit_ffn_rmsnorm_gelu_kn_bf16, no transpose anywhere)."""
     rows, d = _rows_cols(x)
-    f = int(w1.shape[0])
-    if tuple(w1.shape) != (f, d) or tuple(w2.shape) != (d, f):
-        raise ValueError(f"ffn: w1 must be [f, d] and w2 [d, f]; got {tuple(w1.shape)}, "
-                         f"{tuple(w2.shape)} for d={d}")
+    if layout == "linear":
+        f = int(w1.shape[0])
+        want1, want2, fname = (f, d), (d, f), "credit_ffn_rmsnorm_gelu_bf16"
+    elif layout == "in_out":
+        f = int(w1.shape[1])
+        want1, want2, fname = (d, f), (f, d), "credit_ffn_rmsnorm_gelu_kn_bf16"
+    else:
+        raise ValueError(f"ffn: layout must be 'linear' or 'in_out', got {layout!r}")
+    if tuple(w1.shape) != want1 or tuple(w2.shape) != want2:
+        raise ValueError(f"ffn ({layout}): w1 must be {list(want1)} and w2 {list(want2)}; got "
+                         f"{tuple(w1.shape)}, {tuple(w2.shape)} for d={d}")
     check(
-        load_library().credit_ffn_rmsnorm_gelu_bf16(
+        getattr(load_library(), fname)(
             _ptr(x, "x", torch.bfloat16), _ptr(w1, "w1", torch.bfloat16),
             _ptr(w2, "w2", torch.bfloat16), _ptr(out, "out", torch.bfloat16),
             rows, d, f, float(eps), ctypes.byref(cfg)),
-        "credit_ffn_rmsnorm_gelu_bf16",
+        fname,
     )
 
 
@@ -691,6 +702,13 @@ def launch_ffn(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
     ffn(x, w1, w2, out, FFN_EPS, make_cfg(config.variant, config.split))
 
 
+def launch_ffn_baseline_layout(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    """inputs: (x, w1 [d, f], w2 [f, d]) in the BASELINE's [in, out] layout."""
+    x, w1, w2 = inputs
+    (out,) = outputs
+    ffn(x, w1, w2, out, FFN_EPS, make_cfg(config.variant, config.split), layout="in_out")
+
+
 LAYERNORM_EPS = 1.0e-5  # dsmem_eval/workloads.py:55
 
 
@@ -709,6 +727,7 @@ def launch_layernorm_backward(inputs, outputs, config: LaunchConfig = LaunchConf
 
 HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
     "ffn": launch_ffn,
+    "ffn_baseline_layout": launch_ffn_baseline_layout,
     "ffn_backward": launch_ffn_backward,
     "layernorm_backward": launch_layernorm_backward,
     "layernorm_backward_bf16": launch_layernorm_backward,
@@ -832,7 +851,7 @@ def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch
         return torch.empty_like(x), torch.empty_like(x)
     if name == "weighted_var_backward":
         return (torch.empty_like(x),)
-    if name in ("softmax_bwd", "softmax_logits_backward", "ffn", "layernorm_backward",
-                "layernorm_backward_bf16"):
+    if name in ("softmax_bwd", "softmax_logits_backward", "ffn", "ffn_baseline_layout",
+                "layernorm_backward", "layernorm_backward_bf16"):
         return (torch.empty_like(x),)
     raise KeyError(name)

@@ -324,6 +324,19 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         algorithmic_bytes=lambda r, c: 2 * (r * c * 2 + 2 * c * 28672),
         tolerances=(BF16_TOL,),
     ),
+    # C5 again, with the weights in the BASELINE's own [in, out] layout
+    # (W1 [d, f], W2 [f, d]) handed to the library as they are.
+    "ffn_baseline_layout": WorkloadSpec(
+        name="ffn_baseline_layout",
+        label="Norm-fused FFN, [in, out] weights (bf16 MFMA)",
+        category="gemm",
+        rows=4096,
+        cols=8192,
+        input_factory=make_ffn_inputs,
+        output_names=("out",),
+        algorithmic_bytes=lambda r, c: 2 * (r * c * 2 + 2 * c * 28672),
+        tolerances=(BF16_TOL,),
+    ),
     # The "backward of the fused FFN" next row: dx, dW1, dW2 for dout.
     "ffn_backward": WorkloadSpec(
         name="ffn_backward",

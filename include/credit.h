@@ -365,6 +365,15 @@ int credit_pearson_bwd_f32(const float* x, const float* y, const float* grad, fl
 int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w1, const uint16_t* w2,
                                  uint16_t* out, int64_t rows, int64_t d, int64_t f, float eps,
                                  const credit_cfg* cfg);
+/* The same FFN with the weights in the [in_features, out_features] layout
+ * the BASELINE gives them: w1 [d, f], w2 [f, d] (out = x + GELU(RMSNorm(x)
+ * w1) w2), read as they are -- the GEMMs take B as [K, N] tiles and gather
+ * its MFMA fragments with transposing LDS reads, so no transpose runs.
+ * Outputs are bit-identical to credit_ffn_rmsnorm_gelu_bf16 on the
+ * transposed weights.  Same shape, alignment and workspace rules. */
+int credit_ffn_rmsnorm_gelu_kn_bf16(const uint16_t* x, const uint16_t* w1, const uint16_t* w2,
+                                    uint16_t* out, int64_t rows, int64_t d, int64_t f, float eps,
+                                    const credit_cfg* cfg);
 
 /* ----------------------------------- FFN backward (next row of C5) -------
  * The gradients of out = x + GELU_tanh(RMSNorm(x) @ W1^T) @ W2^T (unit
@@ -374,8 +383,9 @@ int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w1, const ui
  *                                                     nn.Linear layouts), bf16;
  * with a = bf16(x rstd), u = bf16(a W1^T) (recomputed), h = bf16(GELU(u)),
  * du = bf16((dout W2) * GELU'(u)); fp32 accumulation on MFMA.  Five GEMMs
- * (one recompute, four gradients) plus transposes of w1, w2, dout and a into
- * the K-contiguous operand layout.  No FFN exists in the reference; this is
+ * (one recompute, four gradients; w1 and w2 are read in place, as [K, N]
+ * operands where the product needs them so) plus transposes of dout and a
+ * into the K-contiguous layout the weight-gradient GEMMs' A operand takes.  No FFN exists in the reference; this is
  * the "backward of the fused FFN" next row.  Same shape and alignment rules
  * as the forward.  Needs credit_ffn_bwd_workspace_bytes(rows, d, f) bytes of
  * workspace (cfg->workspace, or the library's cached buffer). */

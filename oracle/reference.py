@@ -262,15 +262,19 @@ def gelu_tanh(v):
     return v * _sigmoid(2.0 * np.sqrt(2.0 / np.pi) * (v + 0.044715 * v**3))
 
 
-def ffn_rmsnorm_gelu(x, w1, w2, eps: float = 1.0e-6, round_h: bool = True):
+def ffn_rmsnorm_gelu(x, w1, w2, eps: float = 1.0e-6, round_h: bool = True,
+                     round_a: bool = True):
     """out = x + GELU_tanh(RMSNorm(x) @ W1) @ W2 (unit RMSNorm weight).
 
-    The normalised activations and h are rounded to bf16 as the GPU path
-    feeds them to bf16 MFMA; accumulation is float64 here.
+    h is rounded to bf16 as the GPU path feeds it to bf16 MFMA; the
+    normalised activations a = x rstd too with round_a (the 128-tile GEMM
+    scales and rounds the A tile as it stages it), while round_a=False is
+    the 256-tile GEMM's arithmetic: x @ W1 on the bf16 x, the fp32 sum then
+    scaled by rstd, so a is never rounded.  Accumulation is float64 here.
     """
     x = f64(x)
     rstd = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
-    a = round_bf16(x * rstd)
+    a = round_bf16(x * rstd) if round_a else x * rstd
     h = gelu_tanh(a @ f64(w1))
     if round_h:
         h = round_bf16(h)

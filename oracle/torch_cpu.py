@@ -142,5 +142,6 @@ FUNCTIONS = {
     "weighted_var_backward": weighted_var_backward,
     "pearson_backward": pearson_backward,
     "ffn": ffn,
+    "ffn_baseline_layout": ffn,
     "ffn_backward": ffn_backward,
 }

@@ -1,4 +1,5 @@
-"""GPU parity of credit_ffn_rmsnorm_gelu_bf16 (C5) and credit_transpose_bf16.
+"""GPU parity of credit_ffn_rmsnorm_gelu_bf16 (C5), its [in, out]-weight form
+credit_ffn_rmsnorm_gelu_kn_bf16 and credit_transpose_bf16.
 
 out = x + GELU_tanh(RMSNorm(x) @ W1) @ W2 against the float64 oracle
 (oracle.reference.ffn_rmsnorm_gelu, which rounds the normalised activations
@@ -36,9 +37,20 @@ def run_ffn(x, w1, w2, gpu):
     return out.float().cpu().numpy()
 
 
-def oracle(x, w1, w2, rows=None):
+def run_ffn_in_out(x, w1, w2, gpu):
+    """The BASELINE's [in, out] weights (W1 [d, f], W2 [f, d]) passed as they
+    are: credit_ffn_rmsnorm_gelu_kn_bf16."""
+    xs = x.to(gpu)
+    out = torch.full_like(xs, float("nan"))
+    hip_lib.ffn(xs, w1.to(gpu), w2.to(gpu), out, EPS, hip_lib.make_cfg(), layout="in_out")
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def oracle(x, w1, w2, rows=None, round_a=True):
     xs = x.float().numpy() if rows is None else x[rows].float().numpy()
-    return ref.ffn_rmsnorm_gelu(xs, w1.float().numpy(), w2.float().numpy(), EPS)
+    return ref.ffn_rmsnorm_gelu(xs, w1.float().numpy(), w2.float().numpy(), EPS,
+                                round_a=round_a)
 
 
 # (64, 128) and (256, 1024) take the 16-byte tile path, the rest the element path.
@@ -66,6 +78,46 @@ def test_ffn_small_shapes(gpu, rows, d, f):
     print(f"ffn rows={rows} d={d} f={f}", flush=True)
     x, w1, w2 = make(rows, d, f, seed=rows + d + f)
     np.testing.assert_allclose(run_ffn(x, w1, w2, gpu), oracle(x, w1, w2), **BF16)
+
+
+@pytest.mark.parametrize("rows,d,f", [(128, 128, 128), (128, 256, 384), (384, 512, 256),
+                                      (512, 1024, 1024), (1024, 512, 4096), (512, 128, 1024),
+                                      (2048, 384, 256), (4096, 256, 4608)])
+def test_ffn_in_out_layout_is_bit_identical(gpu, rows, d, f):
+    """The [in, out] weight path feeds every MFMA the same operand values in
+    the same lanes as the nn.Linear path (its B fragments come from
+    transposing LDS reads of [K, N] tiles), so the outputs agree bit for
+    bit; the first three shapes take the 128-tile kernels (B staged through
+    registers), the rest the 256-tile ones, (2048, 384, 256) with GEMM2 on
+    the 128-tile kernel (d = 384)."""
+    print(f"ffn in_out rows={rows} d={d} f={f}", flush=True)
+    x, w1, w2 = make(rows, d, f, seed=rows + d + f + 1)
+    got = run_ffn_in_out(x, w1, w2, gpu)
+    assert np.array_equal(got, run_ffn(x, w1, w2, gpu))
+    np.testing.assert_allclose(got, oracle(x, w1, w2), **BF16)
+
+
+@pytest.mark.parametrize("rows,d", [(128, 256), (2048, 256)])
+def test_ffn_in_out_structured_inputs(gpu, rows, d):
+    """Permutation weights on the [in, out] path: out = x + GELU(2 a[:, p])
+    [:, q], so a column or K-row of the [K, N] tile read from the wrong LDS
+    position (swizzle, transposing-read lane order, stage pitch) moves
+    values to the wrong output column.  Each output carries one a value
+    straight through GELU, so the oracle follows the kernel's arithmetic
+    for a: rounded to bf16 on the 128-tile path (rows 128), unrounded on the
+    256-tile path (rows 2048, both GEMMs), where the fp32 sum is scaled by
+    rstd."""
+    g = torch.Generator().manual_seed(5)
+    p = torch.randperm(d, generator=g)
+    q = torch.randperm(d, generator=g)
+    x = (torch.arange(rows * d, dtype=torch.float32).reshape(rows, d) % 11 - 5).to(torch.bfloat16)
+    w1 = torch.zeros(d, d)
+    w1[p, torch.arange(d)] = 2.0   # h[:, j] = GELU(2 a[:, p[j]])
+    w2 = torch.zeros(d, d)
+    w2[torch.arange(d), q] = 1.0   # out[:, q[j]] += h[:, j]
+    w1, w2 = w1.to(torch.bfloat16), w2.to(torch.bfloat16)
+    np.testing.assert_allclose(run_ffn_in_out(x, w1, w2, gpu),
+                               oracle(x, w1, w2, round_a=rows < 2048), **BF16)
 
 
 @pytest.mark.parametrize("rows,d", [(128, 256), (2048, 256)])
@@ -115,6 +167,16 @@ def test_ffn_full_config_sampled_rows(gpu):
     rows (spread over all row tiles) against the float64 oracle."""
     x, w1, w2 = WORKLOADS["ffn"].make_inputs()
     out = run_ffn(x, w1, w2, gpu)
+    rows = np.linspace(0, x.shape[0] - 1, 48).astype(int)
+    np.testing.assert_allclose(out[rows], oracle(x, w1, w2, rows), **BF16)
+    assert np.isfinite(out).all()
+
+
+def test_ffn_in_out_full_config_sampled_rows(gpu):
+    """BASELINE C5 with W1 [8192, 28672] and W2 [28672, 8192] passed as the
+    BASELINE gives them: 48 sampled rows against the float64 oracle."""
+    x, w1, w2 = WORKLOADS["ffn_baseline_layout"].make_inputs()
+    out = run_ffn_in_out(x, w1, w2, gpu)
     rows = np.linspace(0, x.shape[0] - 1, 48).astype(int)
     np.testing.assert_allclose(out[rows], oracle(x, w1, w2, rows), **BF16)
     assert np.isfinite(out).all()

@@ -57,3 +57,16 @@ def test_bound_launcher_matches_golden(gpu, case, variant, split):
     bad = hip_lib.bind(name, gins, outs, hip_lib.LaunchConfig("split", 1 << 20))
     with pytest.raises(hip_lib.CreditError):
         bad()
+
+
+def test_ffn_in_out_layout_matches_golden(gpu):
+    """The ffn fixture (weights in the nn.Linear layout) through the [in, out]
+    weight entry point, its weights transposed on the host."""
+    meta, ins, expected = fixtures.load("ffn_128x128x256")
+    x, w1l, w2l = ins
+    gins = (x.to(gpu), w1l.t().contiguous().to(gpu), w2l.t().contiguous().to(gpu))
+    (out,) = hip_lib.allocate_outputs("ffn_baseline_layout", gins)
+    out.fill_(float("nan"))
+    hip_lib.HIP_LAUNCHERS["ffn_baseline_layout"](gins, (out,))
+    torch.cuda.synchronize()
+    fixtures.check(out.float().cpu().numpy(), expected[0], meta["checks"][0], "ffn in_out")

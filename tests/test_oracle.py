@@ -259,6 +259,11 @@ def test_ffn_matches_torch_composition():
     a = a.float().bfloat16().double()
     expect = tx + F.gelu(a @ t64(w1), approximate="tanh") @ t64(w2)
     np.testing.assert_allclose(out, expect.numpy(), rtol=1e-12, atol=1e-12)
+    # round_a=False: the normalised activations stay unrounded.
+    out = ref.ffn_rmsnorm_gelu(x, w1, w2, 1e-6, round_h=False, round_a=False)
+    a = F.rms_norm(tx, (64,), None, 1e-6)
+    expect = tx + F.gelu(a @ t64(w1), approximate="tanh") @ t64(w2)
+    np.testing.assert_allclose(out, expect.numpy(), rtol=1e-12, atol=1e-12)
 
 
 def test_gelu_tanh_grad_matches_autograd():
