@@ -28,6 +28,8 @@
 // (rstd); backward 4MN (x, dy) + 2N + 4M + 2MN (dx) + 4N (dw).
 #include <initializer_list>
 #include <mutex>
+#include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "api_internal.hpp"
@@ -313,34 +315,47 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
 // [member*chunk, member*chunk + THREADS*VPT) of each.
 //
 // No workgroup barrier in the row loop.  In the step of row i each data
-// wave issues the loads of row i+3, reduces row i+2 (loaded a step
-// earlier) to a wave partial in LDS and counts itself in with an LDS
-// atomic; the wave that arrives last sums the partials in wave order and
-// publishes the member's partial of row i+2.  The communication wave runs
-// ahead on its own: it polls each row's exchange, writes the group total
-// into a 4-entry LDS ring and advances an LDS ready count.  A data wave
-// waits (LDS spin) for row i's total, writes dx of row i and folds row i
-// into its dw accumulators.  Row i is published two steps before it is
-// needed, so the exchange round trip (~2000 cycles) overlaps the data
-// waves' work, and no wave waits for another wave's loads.  The ring,
-// partial and counter slots of row k are reused by row k+4 only: a wave
-// reaches the step that rewrites them after row k+3's total is ready,
-// which orders it after every access to them for row k.  Every wait ends:
-// the poll is bounded (watchdog), and the ready count then still advances.
+// wave issues the loads of row i+DEPTH+AHEAD, reduces row i+DEPTH (loaded
+// AHEAD steps earlier) to a wave partial in LDS and counts itself in with
+// an LDS atomic; the wave that arrives last sums the partials in wave order
+// and publishes the member's partial of row i+DEPTH.  The communication
+// wave runs ahead on its own: it polls each row's exchange, writes the
+// group total into an LDS ring of RING entries and advances an LDS ready
+// count.  A data wave waits (LDS spin) for row i's total, writes dx of row
+// i and folds row i into its dw accumulators.  Row i is published DEPTH
+// steps before it is needed, so the exchange round trip (~2000 cycles idle,
+// ~3 us under this kernel's own load) overlaps the data waves' work, and
+// no wave waits for another wave's loads; AHEAD steps of loads stay in
+// flight.  DEPTH + AHEAD + 1 row buffers rotate through registers.  At C3
+// (16 members of 1024 vectors), against DEPTH 2 / AHEAD 1 on the same box:
+// the backward at DEPTH 3 / AHEAD 2 160.3 -> 157.6 us on one box and
+// unchanged (161.0) on another, the fused forward + backward at 2 / 2
+// 227 -> 217 and 229.5 -> 221.3 us; DEPTH 1 is exchange-bound (225 us), and
+// a build whose communication wave does not wait at all is slower (169.5
+// us), so the exchange is not what bounds the kernel.  The LDS ring, partial and
+// counter slots of row k are reused by row k+RING only (RING >= DEPTH + 2):
+// a wave reaches the step that rewrites them after row k+RING-DEPTH-1's
+// total is ready, which orders it after every access to them for row k.
+// The device slot ring must exceed the 2 DEPTH + 1 stages between the
+// fastest publisher and the slowest poller.  Every wait ends: the poll is
+// bounded (watchdog), and the ready count then still advances.
 //
 // The data loop has no branches around its row traffic: every load and
 // store goes through a buffer resource whose num_records covers the
 // member's slice, or 0 for a row beyond the group, so lanes out of range
 // read zeros and drop their stores; the waitcnt pass then waits for row
-// i+2 while row i+3's loads stay in flight (on gfx9 one vmcnt counts loads
-// and stores in order; a load under a branch makes the count
+// i+DEPTH while the later rows' loads stay in flight (on gfx9 one vmcnt
+// counts loads and stores in order; a load under a branch makes the count
 // path-dependent and the wait after the join a full drain).  dw
 // accumulators: fp64 in LDS, [8*VPT][THREADS], one owner lane each.
 // The group pipeline of the backward and of the fused forward + backward.
 // FUSED: the row's sum of squares travels in the same exchange as
 // sum(dy*w*x) (two values per member), rstd comes from it instead of the
 // forward, and y = x * rstd * w is written beside dx.
-template <int THREADS, int VPT, bool FUSED>
+// Exchange stages in the device slot ring of the group kernels.
+constexpr int kGroupSlotRing = 16;
+
+template <int THREADS, int VPT, bool FUSED, int DEPTH, int AHEAD>
 __device__ __forceinline__ void rmsnorm_group_body(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ dy, const float* __restrict__ rstd, float* __restrict__ rstd_out,
@@ -349,13 +364,17 @@ __device__ __forceinline__ void rmsnorm_group_body(
   constexpr int NW = THREADS / kWave;
   constexpr int K = FUSED ? 2 : 1;  // values per member per row
   constexpr int kSlots = 8 * VPT;
+  constexpr int NB = DEPTH + AHEAD + 1;       // row buffers per lane
+  constexpr int RING = DEPTH + 2 <= 4 ? 4 : 8;  // LDS entries per row slot
+  static_assert(DEPTH >= 1 && AHEAD >= 1 && DEPTH + 2 <= 8, "pipeline depth");
+  static_assert(2 * DEPTH + 1 < kGroupSlotRing, "device slot ring too short for DEPTH");
   extern __shared__ double dw_lds[];  // [kSlots][THREADS]
-  __shared__ double red[4][K][NW];    // wave partials of row k at [(k - r0) & 3]
-  __shared__ double ring[4][K];       // group totals of row k at [(k - r0) & 3]
-  __shared__ uint32_t arrivals[4];
-  __shared__ uint32_t ready;          // rows r0 .. r0 + ready - 1 have totals
+  __shared__ double red[RING][K][NW];  // wave partials of row k at [(k - r0) % RING]
+  __shared__ double ring[RING][K];     // group totals of row k at [(k - r0) % RING]
+  __shared__ uint32_t arrivals[RING];
+  __shared__ uint32_t ready;           // rows r0 .. r0 + ready - 1 have totals
   const int tid = threadIdx.x;
-  if (tid < 4) arrivals[tid] = 0;
+  if (tid < RING) arrivals[tid] = 0;
   if (tid == 0) ready = 0;
   const SplitGroup g = split_join(sa, members, K);  // its barrier covers the stores above
   const int r0 = g.group * rows_per_group;
@@ -373,8 +392,8 @@ __device__ __forceinline__ void rmsnorm_group_body(
       const double dot = split_wave_sum(bits, members, 0);
       const double ssq = FUSED ? split_wave_sum(bits, members, 1) : 0.0;
       if (tid == THREADS) {
-        ring[(k - r0) & 3][0] = dot;
-        if (FUSED) ring[(k - r0) & 3][K - 1] = ssq;
+        ring[(k - r0) % RING][0] = dot;
+        if (FUSED) ring[(k - r0) % RING][K - 1] = ssq;
         __hip_atomic_store(&ready, static_cast<uint32_t>(k - r0 + 1), __ATOMIC_RELEASE,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
       }
@@ -390,7 +409,7 @@ __device__ __forceinline__ void rmsnorm_group_body(
   struct Row {
     u32x4 x[VPT], d[VPT];
   };
-  Row b0, b1, b2, b3;
+  Row b[NB];
   // Row r's slice, or zeros (no traffic) when r is beyond the group.
   auto load_row = [&](Row& b, int r) {
     const bool live = r < r1;
@@ -418,7 +437,7 @@ __device__ __forceinline__ void rmsnorm_group_body(
     }
     const double v = wave_reduce_sum_f64(static_cast<double>(part));
     const double vs = FUSED ? wave_reduce_sum_f64(static_cast<double>(ss)) : 0.0;
-    const int slot = (k - r0) & 3;
+    const int slot = (k - r0) % RING;
     if (lead) {
       red[slot][0][wid] = v;
       if (FUSED) red[slot][K - 1][wid] = vs;
@@ -440,10 +459,20 @@ __device__ __forceinline__ void rmsnorm_group_body(
     const uint32_t need = static_cast<uint32_t>(i - r0 + 1);
     while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < need)
       __builtin_amdgcn_s_sleep(1);
-    return (i - r0) & 3;
+    return (i - r0) % RING;
   };
   const double inv_cols = 1.0 / cols;
-  auto finish_row = [&](const Row& b, int r, int slot) {
+  auto finish_row = [&](Row& b, int r, int slot) {
+    if constexpr (AHEAD > 1) {
+      // The row's unpacked products were formed at its publish, DEPTH steps
+      // earlier; kept live across the steps they take ~50 VGPRs per dwordx4
+      // and the deeper pipeline spills.  Recompute them from the packed row.
+#pragma unroll
+      for (int q = 0; q < VPT; ++q) {
+        __asm__ volatile("" : "+v"(b.x[q]));
+        __asm__ volatile("" : "+v"(b.d[q]));
+      }
+    }
     const double dot = ring[slot][0];
     float rs;
     if (FUSED) {
@@ -480,32 +509,33 @@ __device__ __forceinline__ void rmsnorm_group_body(
       }
     }
   };
-  // Step of row i: cur = row i, r2 = row i+2 (loaded), fut receives row i+3.
-  auto step = [&](Row& cur, Row& r2, Row& fut, int i) {
-    load_row(fut, i + 3);
+  // Step of row i (buffer S = i - r0 mod NB): cur = row i, row i+DEPTH
+  // (loaded) is reduced and published, buffer (S + DEPTH + AHEAD) % NB
+  // receives row i+DEPTH+AHEAD.
+  auto step = [&]<int S>(std::integral_constant<int, S>, int i) {
+    load_row(b[(S + DEPTH + AHEAD) % NB], i + DEPTH + AHEAD);
     __builtin_amdgcn_sched_barrier(0);
-    if (i + 2 < r1) publish_row(r2, i + 2);
-    finish_row(cur, i, wait_total(i));
+    if (i + DEPTH < r1) publish_row(b[(S + DEPTH) % NB], i + DEPTH);
+    finish_row(b[S], i, wait_total(i));
   };
 
 #pragma unroll
   for (int q = 0; q < kSlots; ++q) dw_lds[q * THREADS + tid] = 0.0;
-  load_row(b0, r0);
-  load_row(b1, r0 + 1);
-  load_row(b2, r0 + 2);
-  publish_row(b0, r0);
-  if (r0 + 1 < r1) publish_row(b1, r0 + 1);
-  // Rotate the four buffers through statically named registers.
+  [&]<int... J>(std::integer_sequence<int, J...>) {
+    (load_row(b[J], r0 + J), ...);
+  }(std::make_integer_sequence<int, DEPTH + AHEAD>{});
+  [&]<int... J>(std::integer_sequence<int, J...>) {
+    ((r0 + J < r1 ? publish_row(b[J], r0 + J) : void()), ...);
+  }(std::make_integer_sequence<int, DEPTH>{});
+  // Rotate the NB buffers through statically indexed registers.
   int i = r0;
-  for (; i + 3 < r1; i += 4) {
-    step(b0, b2, b3, i);
-    step(b1, b3, b0, i + 1);
-    step(b2, b0, b1, i + 2);
-    step(b3, b1, b2, i + 3);
-  }
-  if (i < r1) step(b0, b2, b3, i);
-  if (i + 1 < r1) step(b1, b3, b0, i + 1);
-  if (i + 2 < r1) step(b2, b0, b1, i + 2);
+  for (; i + NB - 1 < r1; i += NB)
+    [&]<int... S>(std::integer_sequence<int, S...>) {
+      (step(std::integral_constant<int, S>{}, i + S), ...);
+    }(std::make_integer_sequence<int, NB>{});
+  [&]<int... S>(std::integer_sequence<int, S...>) {
+    ((i + S < r1 ? step(std::integral_constant<int, S>{}, i + S) : void()), ...);
+  }(std::make_integer_sequence<int, NB - 1>{});
   // One fp64 partial row per group member slice (own lanes' accumulators).
   const buffer_rsrc_t prs =
       make_rsrc(dw_part + static_cast<size_t>(g.group) * cols + 8 * static_cast<size_t>(v0),
@@ -519,27 +549,34 @@ __device__ __forceinline__ void rmsnorm_group_body(
                                                    dw_lds[(v * 8 + 2 * q + 1) * THREADS + tid]}));
 }
 
-template <int THREADS, int VPT>
+// Waves per SIMD a group kernel is compiled for: VPT 1 leaves room for two
+// 8-wave workgroups per CU; VPT 2 fills one 9-wave workgroup (512 data
+// lanes plus the communication wave).
+template <int VPT>
+constexpr int kGroupWavesPerEU = VPT == 1 ? 4 : 3;
+
+template <int THREADS, int VPT, int DEPTH = 2, int AHEAD = 1>
 __global__ __launch_bounds__(THREADS + kWave)
-__attribute__((amdgpu_waves_per_eu(VPT == 1 ? 4 : 3, 8))) void rmsnorm_bwd_group_kernel(
+__attribute__((amdgpu_waves_per_eu(kGroupWavesPerEU<VPT>, 8))) void rmsnorm_bwd_group_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ dy, const float* __restrict__ rstd, uint16_t* __restrict__ dx,
     double* __restrict__ dw_part, int rows, int cols, int chunk, int members,
     int rows_per_group, SplitArgs sa) {
-  rmsnorm_group_body<THREADS, VPT, false>(x, w, dy, rstd, nullptr, nullptr, dx, dw_part, rows,
-                                          cols, chunk, members, rows_per_group, 0.0f, sa);
+  rmsnorm_group_body<THREADS, VPT, false, DEPTH, AHEAD>(x, w, dy, rstd, nullptr, nullptr, dx, dw_part,
+                                                 rows, cols, chunk, members, rows_per_group,
+                                                 0.0f, sa);
 }
 
 // Forward and backward in one pass: x, dy, w in; y, rstd, dx, dweight out.
-template <int THREADS, int VPT>
+template <int THREADS, int VPT, int DEPTH = 2, int AHEAD = 1>
 __global__ __launch_bounds__(THREADS + kWave)
-__attribute__((amdgpu_waves_per_eu(VPT == 1 ? 4 : 3, 8))) void rmsnorm_fused_group_kernel(
+__attribute__((amdgpu_waves_per_eu(kGroupWavesPerEU<VPT>, 8))) void rmsnorm_fused_group_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ dy, float* __restrict__ rstd, uint16_t* __restrict__ y,
     uint16_t* __restrict__ dx, double* __restrict__ dw_part, int rows, int cols, int chunk,
     int members, int rows_per_group, float eps, SplitArgs sa) {
-  rmsnorm_group_body<THREADS, VPT, true>(x, w, dy, nullptr, rstd, y, dx, dw_part, rows, cols,
-                                         chunk, members, rows_per_group, eps, sa);
+  rmsnorm_group_body<THREADS, VPT, true, DEPTH, AHEAD>(x, w, dy, nullptr, rstd, y, dx, dw_part, rows,
+                                                cols, chunk, members, rows_per_group, eps, sa);
 }
 
 // READ variant pre-pass: rowdot[r] = sum_j dy*w*x over the row, streamed.
@@ -645,7 +682,7 @@ const BwdGroupPick kBwdGroup[] = {
     {rmsnorm_bwd_group_kernel<192, 1>, 192, 192, 4},
     {rmsnorm_bwd_group_kernel<448, 1>, 448, 448, 2},
     {rmsnorm_bwd_group_kernel<960, 1>, 960, 960, 1},
-    {rmsnorm_bwd_group_kernel<512, 2>, 512, 1024, 1},
+    {rmsnorm_bwd_group_kernel<512, 2, 3, 2>, 512, 1024, 1},
 };
 // Fused forward + backward: the same shapes, the sum of squares riding in
 // the same exchange (two values per member, so at most 32 members).
@@ -664,7 +701,7 @@ const FusedGroupPick kFusedGroup[] = {
     {rmsnorm_fused_group_kernel<192, 1>, 192, 192},
     {rmsnorm_fused_group_kernel<448, 1>, 448, 448},
     {rmsnorm_fused_group_kernel<960, 1>, 960, 960},
-    {rmsnorm_fused_group_kernel<512, 2>, 512, 1024},
+    {rmsnorm_fused_group_kernel<512, 2, 2, 2>, 512, 1024},
 };
 constexpr int kMaxFusedMembers = kMaxExchangeValues / 2;
 constexpr int kFwdMaxCapacity = 8192;
@@ -839,7 +876,7 @@ int resolve_bwd(const credit_cfg* cfg, int64_t rows, int64_t cols, bool vec, int
 // Slot rows per group of the group kernel: a member publishes row k two
 // steps before it needs row k's total, and a member reaches row k + 16 only
 // after every member has polled row k, so 16 rows of slots suffice.
-constexpr int kBwdRing = 16;
+constexpr int kBwdRing = kGroupSlotRing;
 int bwd_ring(const BwdPlan& p) { return p.variant == CREDIT_VARIANT_SPLIT ? kBwdRing : 1; }
 
 size_t bwd_extra_bytes(const BwdPlan& p, int64_t rows, int64_t cols) {
