@@ -164,9 +164,9 @@ __device__ __forceinline__ void merge_maxsum_lanes(bool has, float m, float s, f
   *S_out = static_cast<float>(wave_reduce_sum_f64(term));
 }
 
-// SPLIT variant for rows wider than one workgroup: a co-resident wave of
-// row groups, each group P members that hold 1/P of every row of a block of
-// rows, pipelined four rows deep.  The workgroup is THREADS data lanes (VPT
+// SPLIT variant for rows wider than one workgroup: a co-resident wave of G
+// row groups, each group P members that hold 1/P of every one of its rows
+// (group g: rows g, g + G, g + 2G, ...), pipelined four rows deep.  The workgroup is THREADS data lanes (VPT
 // f32x4 of the member's slice per lane and row) plus one communication wave.
 //
 // In the step of row i each data wave issues the loads of row i+3, reduces
@@ -209,9 +209,18 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
   if (tid < 4) arrivals[tid] = 0;
   if (tid == 0) ready = 0;
   const SplitGroup g = split_join(sa, members, 2);  // its barrier covers the stores above
-  const int r0 = g.group * rows_per_group;
-  if (r0 >= rows) return;  // padding group
-  const int r1 = r0 + rows_per_group < rows ? r0 + rows_per_group : rows;
+  // Rows are dealt to the G groups round-robin (group g's i-th row is
+  // g + i G), so the rows in flight at any moment are adjacent in memory;
+  // i below counts the group's rows and row_of(i) is the tensor row.
+  // G: the groups that take rows (the launch pads the grid to a multiple
+  // of the dispensers; padding groups, and their dweight partial rows where
+  // there are any, stay out).  Each takes at most rows_per_group rows, the
+  // host's bound on its exchange tags.
+  const int G = (rows + rows_per_group - 1) / rows_per_group;
+  if (g.group >= G) return;  // padding group
+  const int r0 = 0;
+  const int r1 = (rows - g.group + G - 1) / G;
+  auto row_of = [&](int i) { return g.group + i * G; };
   const int nvec = cols >> 2;
   const int v0 = g.member * chunk;
   const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
@@ -233,8 +242,8 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
         __hip_atomic_store(&ready, static_cast<uint32_t>(k - r0 + 1), __ATOMIC_RELEASE,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
         if (g.member == 0) {
-          rowmax[k] = M;
-          lse[k] = static_cast<float>(static_cast<double>(M) + ::log(static_cast<double>(S)));
+          rowmax[row_of(k)] = M;
+          lse[row_of(k)] = static_cast<float>(static_cast<double>(M) + ::log(static_cast<double>(S)));
         }
       }
     }
@@ -252,7 +261,8 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
   Row b0, b1, b2, b3;
   auto load_row = [&](Row& b, int r) {
     const bool live = r < r1;
-    const size_t off = static_cast<size_t>(live ? r : r0) * cols + 4 * static_cast<size_t>(v0);
+    const size_t off =
+        static_cast<size_t>(row_of(live ? r : r0)) * cols + 4 * static_cast<size_t>(v0);
     const buffer_rsrc_t xs = make_rsrc(x + off, live ? slice_bytes : 0u);
 #pragma unroll
     for (int q = 0; q < VPT; ++q)
@@ -311,7 +321,7 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
     // e^(m_w - M) / S; 0/0 (NaN) for a row of -inf, as torch.softmax.
     const float mw = wmax[slot][wid];
     const float f = (mw == kNegInf ? 0.0f : exp_accurate(mw - M)) / S;
-    const size_t off = static_cast<size_t>(r) * cols + 4 * static_cast<size_t>(v0);
+    const size_t off = static_cast<size_t>(row_of(r)) * cols + 4 * static_cast<size_t>(v0);
     const buffer_rsrc_t out = make_rsrc(p + off, slice_bytes);
 #pragma unroll
     for (int q = 0; q < VPT; ++q)
@@ -367,9 +377,18 @@ __attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
   if (tid < 4) arrivals[tid] = 0;
   if (tid == 0) ready = 0;
   const SplitGroup g = split_join(sa, members, 1);  // its barrier covers the stores above
-  const int r0 = g.group * rows_per_group;
-  if (r0 >= rows) return;  // padding group
-  const int r1 = r0 + rows_per_group < rows ? r0 + rows_per_group : rows;
+  // Rows are dealt to the G groups round-robin (group g's i-th row is
+  // g + i G), so the rows in flight at any moment are adjacent in memory;
+  // i below counts the group's rows and row_of(i) is the tensor row.
+  // G: the groups that take rows (the launch pads the grid to a multiple
+  // of the dispensers; padding groups, and their dweight partial rows where
+  // there are any, stay out).  Each takes at most rows_per_group rows, the
+  // host's bound on its exchange tags.
+  const int G = (rows + rows_per_group - 1) / rows_per_group;
+  if (g.group >= G) return;  // padding group
+  const int r0 = 0;
+  const int r1 = (rows - g.group + G - 1) / G;
+  auto row_of = [&](int i) { return g.group + i * G; };
   const int nvec = cols >> 2;
   const int v0 = g.member * chunk;
   const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
@@ -400,7 +419,8 @@ __attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
   Row b0, b1, b2, b3;
   auto load_row = [&](Row& b, int r) {
     const bool live = r < r1;
-    const size_t off = static_cast<size_t>(live ? r : r0) * cols + 4 * static_cast<size_t>(v0);
+    const size_t off =
+        static_cast<size_t>(row_of(live ? r : r0)) * cols + 4 * static_cast<size_t>(v0);
     const buffer_rsrc_t ps = make_rsrc(p + off, live ? slice_bytes : 0u);
     const buffer_rsrc_t ds = make_rsrc(dy + off, live ? slice_bytes : 0u);
 #pragma unroll
@@ -436,7 +456,7 @@ __attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
   };
   auto finish_row = [&](const Row& b, int r, double dot) {
     const float c = static_cast<float>(dot);
-    const size_t off = static_cast<size_t>(r) * cols + 4 * static_cast<size_t>(v0);
+    const size_t off = static_cast<size_t>(row_of(r)) * cols + 4 * static_cast<size_t>(v0);
     const buffer_rsrc_t out = make_rsrc(dx + off, slice_bytes);
 #pragma unroll
     for (int q = 0; q < VPT; ++q) slice_store(out, lane_off + q * kStride, grad4(b.p[q], b.d[q], c));
@@ -877,8 +897,8 @@ int resolve_bwd(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
 }
 
 // Rows per group and groups of a group-kernel launch: as many groups as
-// fit the device at once (a multiple of kDispensers), each taking a
-// contiguous block of rows.
+// fit the device at once (a multiple of kDispensers); the kernels deal the
+// rows to them round-robin, at most rows_per_group each.
 int plan_row_groups(const void* fn, int threads, int members, int64_t rows, int* rows_per_group,
                     int64_t* groups, const char* name) {
   int64_t fit = 0;
