@@ -65,9 +65,9 @@ CALL_KERNELS = {
     "row_sum_max": ("rowreduce.hip", ["row_sum_max_read_kernel<256>"]),
     "layernorm_fwd": ("layernorm.hip", ["layernorm_fwd_pipe_kernel<512, 8>"]),
     "rmsnorm_fwd": ("rmsnorm.hip", ["rmsnorm_fwd_slice_kernel<1024, 8>"]),
-    "rmsnorm_bwd": ("rmsnorm.hip", ["rmsnorm_bwd_group_kernel<512, 2>",
+    "rmsnorm_bwd": ("rmsnorm.hip", ["rmsnorm_bwd_group_kernel<512, 2, 3, 2>",
                                     "rmsnorm_dw_reduce_kernel"]),
-    "rmsnorm_fwd_bwd": ("rmsnorm.hip", ["rmsnorm_fused_group_kernel<512, 2>",
+    "rmsnorm_fwd_bwd": ("rmsnorm.hip", ["rmsnorm_fused_group_kernel<512, 2, 2, 2>",
                                         "rmsnorm_dw_reduce_kernel"]),
     "softmax_fwd": ("softmax.hip", ["softmax_fwd_group_kernel<512, 8>"]),
     "softmax_bwd": ("softmax.hip", ["softmax_bwd_group_kernel<512, 4>"]),
