@@ -1,8 +1,15 @@
 // C5: norm-fused FFN on MFMA, bf16 with fp32 accumulation.
 //
-//   a   = bf16(x * rstd),  rstd = 1/sqrt(mean_j x^2 + eps)   (unit RMSNorm weight)
-//   h   = bf16(GELU_tanh(a @ W1^T))
-//   out = bf16(x + h @ W2^T)
+//   rstd = 1/sqrt(mean_j x^2 + eps)                          (unit RMSNorm weight)
+//   h    = bf16(GELU_tanh(rstd * (x @ W1^T)))   256-tile kernel (the C5 path)
+//   h    = bf16(GELU_tanh(bf16(x * rstd) @ W1^T))   128-tile kernel
+//   out  = bf16(x + h @ W2^T)
+//
+// The 256-tile kernel multiplies the fp32 accumulator of x @ W1^T by the
+// row's rstd in its epilogue (the row scale commutes with the GEMM), so the
+// normalised input is never rounded; the 128-tile kernel scales and rounds
+// the A tile to bf16 as it stages it.  Both are the same function up to that
+// rounding (the oracle's round_a switch selects either).
 //
 // No FFN exists in the reference; this is the consumer of the row-norm
 // kernels the BASELINE names.  Weights come in the nn.Linear layout
