@@ -52,8 +52,8 @@ HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 # Workloads whose tensors are bf16 (fp32 accumulation); the rest compute in fp32.
 BF16_WORKLOADS = ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd", "ffn", "ffn_baseline_layout",
-                  "ffn_backward", "layernorm_backward_bf16")
-FFN_WORKLOADS = ("ffn", "ffn_baseline_layout", "ffn_backward")
+                  "ffn_backward", "ffn_backward_saved", "layernorm_backward_bf16")
+FFN_WORKLOADS = ("ffn", "ffn_baseline_layout", "ffn_backward", "ffn_backward_saved")
 
 # Kernels one AUTO call launches at the BASELINE shape (names as rocprofv3
 # reports them) and the source file they are built from; the committed PMC
@@ -214,6 +214,9 @@ def cpu_baseline(name, cpu_inputs, spec, seconds):
     elif name == "softmax_bwd":
         p = torch.softmax(args[0], dim=-1)
         fn, args = torch_cpu.softmax_bwd, (p, args[1])
+    elif name == "ffn_backward_saved":
+        # the forward (with its saved activations) outside the timed calls
+        fn, args = torch_cpu.ffn_backward_saved(*args), ()
     # Row sample: shrink the batch until one call takes <= seconds/4.
     sample_rows = rows
     t0 = time.perf_counter()
@@ -257,7 +260,8 @@ def cpu_baseline(name, cpu_inputs, spec, seconds):
 def spec_ffn_flops(rows, d, name="ffn"):
     from credit_amd.workloads import ffn_backward_flops, ffn_flops
 
-    return ffn_backward_flops(rows, d) if name == "ffn_backward" else ffn_flops(rows, d)
+    return (ffn_backward_flops(rows, d) if name in ("ffn_backward", "ffn_backward_saved")
+            else ffn_flops(rows, d))
 
 
 # ------------------------------------------------------------------ main --

@@ -49,16 +49,19 @@ constexpr int kThreads = 256;
 constexpr int kLdsStride = kBK + 8;  // bf16 per LDS row: 16-byte pad against bank conflicts
 
 // GEMM epilogues.  Forward: kEpiGelu (h = GELU(acc * rstd[m])),
-// kEpiResidual (out = acc + x).  Backward (credit_ffn_rmsnorm_gelu_bwd_bf16):
-// kEpiUH (u = acc * rstd[m] to C, h = GELU(u) transposed to C2),
-// kEpiGeluBwd (du = acc * GELU'(u[m, n]) to C and, transposed, to C2),
-// kEpiStore (bf16(acc)), kEpiStoreF32 (acc as fp32 to Cf).
+// kEpiResidual (out = acc + x); the training forward's kEpiGeluSave (h =
+// GELU(u) to C and u = acc * rstd[m] to C2, both row-major).  Backward
+// (credit_ffn_rmsnorm_gelu_bwd_bf16): kEpiUH (u = acc * rstd[m] to C, h =
+// GELU(u) transposed to C2), kEpiGeluBwd (du = acc * GELU'(u[m, n]) to C
+// and, transposed, to C2), kEpiStore (bf16(acc)), kEpiStoreF32 (acc as fp32
+// to Cf).
 constexpr int kEpiGelu = 0;
 constexpr int kEpiResidual = 1;
 constexpr int kEpiUH = 2;
 constexpr int kEpiGeluBwd = 3;
 constexpr int kEpiStore = 4;
 constexpr int kEpiStoreF32 = 5;
+constexpr int kEpiGeluSave = 6;
 
 // GELU with the tanh approximation, z = sqrt(2/pi) (v + 0.044715 v^3):
 // 0.5 (1 + tanh z) = sigmoid(2z) = s = e r with e = e^(2z) and
@@ -112,6 +115,11 @@ __device__ __forceinline__ void epilogue(float acc, float s, float rv, int m, in
   const size_t tdx = static_cast<size_t>(n) * M + m;
   if (EPI == kEpiGelu) {
     C[idx] = f32_to_bf16(gelu_tanh(acc * s));
+  } else if (EPI == kEpiGeluSave) {
+    // The same h as kEpiGelu, and the u the backward's kEpiUH recomputes.
+    const float u = acc * s;
+    C[idx] = f32_to_bf16(gelu_tanh(u));
+    C2[idx] = f32_to_bf16(u);
   } else if (EPI == kEpiResidual) {
     C[idx] = f32_to_bf16(acc + rv);
   } else if (EPI == kEpiUH) {
@@ -164,6 +172,7 @@ __global__ __launch_bounds__(256) void ffn_rstd_kernel(const uint16_t* __restric
 // bf16 (KN: B [K, N], element (n, k) at B[k * N + n]); M % 128 == 0,
 // N % 128 == 0, K % 64 == 0 (checked on the host).
 //  kEpiGelu:     A rows scaled by a_scale[m] on load; C = bf16(gelu(acc)).
+//  kEpiGeluSave: likewise, and C2 = bf16(acc) (u).
 //  kEpiResidual: C = bf16(acc + R[m, n]).
 // KN: thread t stages 16-byte chunk t % 16 (8 columns) of K-rows t / 16 +
 // 16 i of the 64 x 128 B tile and scatters its 8 values into the [n][k]
@@ -174,7 +183,7 @@ __global__ __launch_bounds__(kThreads) void ffn_gemm_kernel(
     const uint16_t* __restrict__ A, const float* __restrict__ a_scale,
     const uint16_t* __restrict__ B, const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
     uint16_t* __restrict__ C2, float* __restrict__ Cf, int M, int N, int K) {
-  constexpr bool kScaleA = EPI == kEpiGelu || EPI == kEpiUH;
+  constexpr bool kScaleA = EPI == kEpiGelu || EPI == kEpiUH || EPI == kEpiGeluSave;
   __shared__ __attribute__((aligned(16))) uint16_t As[kBM * kLdsStride];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[kBN * kLdsStride];
   const int tid = threadIdx.x;
@@ -653,7 +662,7 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      const float sc = EPI == kEpiGelu ? scale[m] : 1.0f;
+      const float sc = EPI == kEpiGelu || EPI == kEpiGeluSave ? scale[m] : 1.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n = n0 + wn * 128 + j * 32 + (lane & 31);
@@ -775,7 +784,8 @@ template <bool KN>
 int enable_big_lds() {
   static int status = [] {
     for (const hipError_t e :
-         {allow_big_lds<kEpiGelu, KN>(), allow_big_lds<kEpiResidual, KN>(),
+         {allow_big_lds<kEpiGelu, KN>(), allow_big_lds<kEpiGeluSave, KN>(),
+          allow_big_lds<kEpiResidual, KN>(),
           allow_big_lds<kEpiUH, KN>(), allow_big_lds<kEpiGeluBwd, KN>(),
           allow_big_lds<kEpiStore, KN>(), allow_big_lds<kEpiStoreF32, KN>()})
       if (e != hipSuccess) return hip_failure(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
@@ -929,6 +939,38 @@ extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w
   return ffn_forward<false>(x, w1, w2, out, rows, d, f, eps, cfg);
 }
 
+extern "C" int credit_ffn_rmsnorm_gelu_fwd_train_bf16(const uint16_t* x, const uint16_t* w1,
+                                                      const uint16_t* w2, uint16_t* out,
+                                                      float* rstd, uint16_t* u, uint16_t* h,
+                                                      int64_t rows, int64_t d, int64_t f,
+                                                      float eps, const credit_cfg* cfg) {
+  CREDIT_TRY(check_row_ptr(x, "x", rows));
+  CREDIT_TRY(check_ptr(w1, "w1"));
+  CREDIT_TRY(check_ptr(w2, "w2"));
+  CREDIT_TRY(check_row_ptr(out, "out", rows));
+  CREDIT_TRY(check_row_ptr(rstd, "rstd", rows));
+  CREDIT_TRY(check_row_ptr(u, "u", rows));
+  CREDIT_TRY(check_row_ptr(h, "h", rows));
+  CREDIT_TRY(check_cfg(cfg));
+  CREDIT_TRY(check_ffn_shape(rows, d, f));
+  if (!(eps >= 0.0f)) return set_error(CREDIT_ERR_BAD_CONFIG, "eps must be >= 0");
+  for (const void* p : {static_cast<const void*>(x), static_cast<const void*>(w1),
+                        static_cast<const void*>(w2), static_cast<const void*>(out),
+                        static_cast<const void*>(u), static_cast<const void*>(h)})
+    if (p && !aligned16(p))
+      return set_error(CREDIT_ERR_ALIGNMENT,
+                       "ffn training forward: x, w1, w2, out, u and h must be 16-byte aligned");
+  if (rows == 0) return CREDIT_OK;
+  hipStream_t stream = cfg_stream(cfg);
+  const int M = static_cast<int>(rows), D = static_cast<int>(d), F = static_cast<int>(f);
+  ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, D, eps);
+  CREDIT_TRY(check_launch("ffn_rstd_kernel"));
+  CREDIT_TRY(launch_gemm<kEpiGeluSave>(x, rstd, w1, nullptr, h, u, nullptr, M, F, D, stream,
+                                       "ffn gemm1 (gelu, saving u and h)"));
+  return launch_gemm<kEpiResidual>(h, nullptr, w2, x, out, nullptr, nullptr, M, D, F, stream,
+                                   "ffn gemm2 (residual)");
+}
+
 extern "C" int credit_ffn_rmsnorm_gelu_kn_bf16(const uint16_t* x, const uint16_t* w1,
                                                const uint16_t* w2, uint16_t* out, int64_t rows,
                                                int64_t d, int64_t f, float eps,
@@ -936,11 +978,23 @@ extern "C" int credit_ffn_rmsnorm_gelu_kn_bf16(const uint16_t* x, const uint16_t
   return ffn_forward<true>(x, w1, w2, out, rows, d, f, eps, cfg);
 }
 
-extern "C" int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_t* w1,
-                                                const uint16_t* w2, const uint16_t* dout,
-                                                uint16_t* dx, uint16_t* dw1, uint16_t* dw2,
-                                                int64_t rows, int64_t d, int64_t f, float eps,
-                                                const credit_cfg* cfg) {
+namespace credit {
+namespace {
+
+// The backward.  With saved == nullptr it recomputes rstd, u and h^T from x
+// (one extra GEMM); with the training forward's rstd, u and h it skips that
+// GEMM and reads h as the dW2 GEMM's [K, N] B operand.  Both give the same
+// bits: the saved u and h are the recomputed ones.
+struct FfnSaved {
+  const float* rstd;
+  const uint16_t* u;
+  const uint16_t* h;
+};
+
+int ffn_backward(const uint16_t* x, const uint16_t* w1, const uint16_t* w2,
+                 const uint16_t* dout, const FfnSaved* saved, uint16_t* dx, uint16_t* dw1,
+                 uint16_t* dw2, int64_t rows, int64_t d, int64_t f, float eps,
+                 const credit_cfg* cfg) {
   CREDIT_TRY(check_row_ptr(x, "x", rows));
   CREDIT_TRY(check_ptr(w1, "w1"));
   CREDIT_TRY(check_ptr(w2, "w2"));
@@ -951,10 +1005,17 @@ extern "C" int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_
   CREDIT_TRY(check_cfg(cfg));
   CREDIT_TRY(check_ffn_shape(rows, d, f));
   if (!(eps >= 0.0f)) return set_error(CREDIT_ERR_BAD_CONFIG, "eps must be >= 0");
+  if (saved != nullptr) {
+    CREDIT_TRY(check_row_ptr(saved->rstd, "rstd", rows));
+    CREDIT_TRY(check_row_ptr(saved->u, "u", rows));
+    CREDIT_TRY(check_row_ptr(saved->h, "h", rows));
+  }
   for (const void* p : {static_cast<const void*>(x), static_cast<const void*>(w1),
                         static_cast<const void*>(w2), static_cast<const void*>(dout),
                         static_cast<const void*>(dx), static_cast<const void*>(dw1),
-                        static_cast<const void*>(dw2)})
+                        static_cast<const void*>(dw2),
+                        static_cast<const void*>(saved ? saved->u : nullptr),
+                        static_cast<const void*>(saved ? saved->h : nullptr)})
     if (p && !aligned16(p))
       return set_error(CREDIT_ERR_ALIGNMENT, "ffn backward: every buffer must be 16-byte aligned");
   hipStream_t stream = cfg_stream(cfg);
@@ -974,8 +1035,8 @@ extern "C" int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_
   char* ws = nullptr;
   CREDIT_TRY(acquire_workspace(cfg, L.total, &ws));
   char* b = ws_scratch(ws);
-  float* rstd = reinterpret_cast<float*>(b + L.rstd);
-  uint16_t* u = reinterpret_cast<uint16_t*>(b + L.u);
+  const float* rstd = saved ? saved->rstd : reinterpret_cast<float*>(b + L.rstd);
+  const uint16_t* u = saved ? saved->u : reinterpret_cast<uint16_t*>(b + L.u);
   uint16_t* du = reinterpret_cast<uint16_t*>(b + L.du);
   uint16_t* ht = reinterpret_cast<uint16_t*>(b + L.ht);
   uint16_t* dut = reinterpret_cast<uint16_t*>(b + L.dut);
@@ -983,21 +1044,30 @@ extern "C" int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_
   uint16_t* at = reinterpret_cast<uint16_t*>(b + L.at);
   float* da = reinterpret_cast<float*>(b + L.da);
   const int M = static_cast<int>(rows), D = static_cast<int>(d), F = static_cast<int>(f);
-  ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, D, eps);
-  CREDIT_TRY(check_launch("ffn_rstd_kernel"));
+  if (saved == nullptr) {
+    ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, reinterpret_cast<float*>(b + L.rstd), D,
+                                                       eps);
+    CREDIT_TRY(check_launch("ffn_rstd_kernel"));
+  }
   // The A operands of the weight gradients in the K-contiguous layout A
   // takes (the weights themselves are read as [K, N] B operands).
   CREDIT_TRY(launch_transpose(dout, doutt, M, D, nullptr, stream));
   CREDIT_TRY(launch_transpose(x, at, M, D, rstd, stream));         // a^T = bf16(x rstd)^T
-  // u = (x W1^T) rstd, h^T = GELU(u)^T.
-  CREDIT_TRY(launch_gemm<kEpiUH>(x, rstd, w1, nullptr, u, ht, nullptr, M, F, D, stream,
-                                 "ffn bwd gemm u"));
+  // u = (x W1^T) rstd, h^T = GELU(u)^T (recomputed unless saved).
+  if (saved == nullptr)
+    CREDIT_TRY(launch_gemm<kEpiUH>(x, rstd, w1, nullptr, reinterpret_cast<uint16_t*>(b + L.u), ht,
+                                   nullptr, M, F, D, stream, "ffn bwd gemm u"));
   // du = (dout W2) * GELU'(u), and du^T; W2 [d, f] is B as [K, N].
   CREDIT_TRY((launch_gemm<kEpiGeluBwd, true>(dout, nullptr, w2, u, du, dut, nullptr, M, F, D,
                                             stream, "ffn bwd gemm du")));
-  // dW2 [d, f] = dout^T h.
-  CREDIT_TRY(launch_gemm<kEpiStore>(doutt, nullptr, ht, nullptr, dw2, nullptr, nullptr, D, F, M,
-                                    stream, "ffn bwd gemm dw2"));
+  // dW2 [d, f] = dout^T h: h^T [f, M] as the B operand, or the saved h
+  // [M, f] read as [K, N].
+  if (saved == nullptr)
+    CREDIT_TRY(launch_gemm<kEpiStore>(doutt, nullptr, ht, nullptr, dw2, nullptr, nullptr, D, F, M,
+                                      stream, "ffn bwd gemm dw2"));
+  else
+    CREDIT_TRY((launch_gemm<kEpiStore, true>(doutt, nullptr, saved->h, nullptr, dw2, nullptr,
+                                             nullptr, D, F, M, stream, "ffn bwd gemm dw2")));
   // dW1 [f, d] = du^T a.
   CREDIT_TRY(launch_gemm<kEpiStore>(dut, nullptr, at, nullptr, dw1, nullptr, nullptr, F, D, M,
                                     stream, "ffn bwd gemm dw1"));
@@ -1007,4 +1077,23 @@ extern "C" int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_
                                              F, stream, "ffn bwd gemm da")));
   ffn_dx_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, da, dout, dx, D);
   return check_launch("ffn_dx_kernel");
+}
+
+}  // namespace
+}  // namespace credit
+
+extern "C" int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_t* w1,
+                                                const uint16_t* w2, const uint16_t* dout,
+                                                uint16_t* dx, uint16_t* dw1, uint16_t* dw2,
+                                                int64_t rows, int64_t d, int64_t f, float eps,
+                                                const credit_cfg* cfg) {
+  return ffn_backward(x, w1, w2, dout, nullptr, dx, dw1, dw2, rows, d, f, eps, cfg);
+}
+
+extern "C" int credit_ffn_rmsnorm_gelu_bwd_saved_bf16(
+    const uint16_t* x, const uint16_t* w1, const uint16_t* w2, const uint16_t* dout,
+    const float* rstd, const uint16_t* u, const uint16_t* h, uint16_t* dx, uint16_t* dw1,
+    uint16_t* dw2, int64_t rows, int64_t d, int64_t f, const credit_cfg* cfg) {
+  const FfnSaved saved{rstd, u, h};
+  return ffn_backward(x, w1, w2, dout, &saved, dx, dw1, dw2, rows, d, f, 0.0f, cfg);
 }

@@ -131,6 +131,10 @@ SIGNATURES: dict[str, list] = {
     "credit_ffn_rmsnorm_gelu_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
     "credit_ffn_rmsnorm_gelu_kn_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
     "credit_ffn_rmsnorm_gelu_bwd_bf16": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _CFG],
+    "credit_ffn_rmsnorm_gelu_fwd_train_bf16": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F,
+                                               _CFG],
+    "credit_ffn_rmsnorm_gelu_bwd_saved_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                               _I64, _CFG],
     "credit_ffn_bwd_workspace_bytes": [_I64, _I64, _I64],
     "credit_layernorm_bwd_f32": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_layernorm_bwd_bf16": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
@@ -592,6 +596,56 @@ def ffn_backward(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, dout: torc
     )
 
 
+def _ffn_linear_dims(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, who: str):
+    rows, d = _rows_cols(x)
+    f = int(w1.shape[0])
+    if tuple(w1.shape) != (f, d) or tuple(w2.shape) != (d, f):
+        raise ValueError(f"{who}: w1 must be [f, d] and w2 [d, f]; got {tuple(w1.shape)}, "
+                         f"{tuple(w2.shape)} for d={d}")
+    return rows, d, f
+
+
+def ffn_train_forward(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, out: torch.Tensor,
+                      rstd: torch.Tensor, u: torch.Tensor, h: torch.Tensor, eps: float,
+                      cfg: CreditCfg) -> None:
+    """ffn() (nn.Linear weights) that also writes what its backward needs:
+    rstd [rows] fp32, u [rows, f] and h [rows, f] bf16."""
+    rows, d, f = _ffn_linear_dims(x, w1, w2, "ffn_train_forward")
+    for name, t, shape in (("out", out, (rows, d)), ("rstd", rstd, (rows,)),
+                           ("u", u, (rows, f)), ("h", h, (rows, f))):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"ffn_train_forward: {name} must be {shape}, got {tuple(t.shape)}")
+    bf = torch.bfloat16
+    check(
+        load_library().credit_ffn_rmsnorm_gelu_fwd_train_bf16(
+            _ptr(x, "x", bf), _ptr(w1, "w1", bf), _ptr(w2, "w2", bf), _ptr(out, "out", bf),
+            _ptr(rstd, "rstd", torch.float32), _ptr(u, "u", bf), _ptr(h, "h", bf), rows, d, f,
+            float(eps), ctypes.byref(cfg)),
+        "credit_ffn_rmsnorm_gelu_fwd_train_bf16",
+    )
+
+
+def ffn_backward_saved(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, dout: torch.Tensor,
+                       rstd: torch.Tensor, u: torch.Tensor, h: torch.Tensor, dx: torch.Tensor,
+                       dw1: torch.Tensor, dw2: torch.Tensor, cfg: CreditCfg) -> None:
+    """ffn_backward() from the saved rstd, u and h of ffn_train_forward()."""
+    rows, d, f = _ffn_linear_dims(x, w1, w2, "ffn_backward_saved")
+    for name, t, shape in (("dout", dout, (rows, d)), ("rstd", rstd, (rows,)),
+                           ("u", u, (rows, f)), ("h", h, (rows, f)), ("dx", dx, (rows, d)),
+                           ("dw1", dw1, (f, d)), ("dw2", dw2, (d, f))):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"ffn_backward_saved: {name} must be {shape}, got {tuple(t.shape)}")
+    bf = torch.bfloat16
+    check(
+        load_library().credit_ffn_rmsnorm_gelu_bwd_saved_bf16(
+            _ptr(x, "x", bf), _ptr(w1, "w1", bf), _ptr(w2, "w2", bf), _ptr(dout, "dout", bf),
+            _ptr(rstd, "rstd", torch.float32), _ptr(u, "u", bf), _ptr(h, "h", bf),
+            _ptr(dx, "dx", bf), _ptr(dw1, "dw1", bf), _ptr(dw2, "dw2", bf), rows, d, f,
+            ctypes.byref(cfg)),
+        "credit_ffn_rmsnorm_gelu_bwd_saved_bf16",
+    )
+
+
 def linear_layout(w: torch.Tensor) -> torch.Tensor:
     """A [in, out] weight (the BASELINE's W1 [d, f]) in the nn.Linear layout
     [out, in] the FFN takes, transposed on the GPU by this library."""
@@ -719,6 +773,15 @@ def launch_ffn_backward(inputs, outputs, config: LaunchConfig = LaunchConfig()) 
     ffn_backward(x, w1, w2, dout, dx, dw1, dw2, FFN_EPS, make_cfg(config.variant, config.split))
 
 
+def launch_ffn_backward_saved(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
+    """inputs: (x, w1 [f, d], w2 [d, f], dout, rstd, u, h) -- the last three
+    from ffn_train_forward; outputs: (dx, dw1, dw2)."""
+    x, w1, w2, dout, rstd, u, h = inputs
+    dx, dw1, dw2 = outputs
+    ffn_backward_saved(x, w1, w2, dout, rstd, u, h, dx, dw1, dw2,
+                       make_cfg(config.variant, config.split))
+
+
 def launch_layernorm_backward(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
     x, dy, gamma = inputs
     (dx,) = outputs
@@ -729,6 +792,7 @@ HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
     "ffn": launch_ffn,
     "ffn_baseline_layout": launch_ffn_baseline_layout,
     "ffn_backward": launch_ffn_backward,
+    "ffn_backward_saved": launch_ffn_backward_saved,
     "layernorm_backward": launch_layernorm_backward,
     "layernorm_backward_bf16": launch_layernorm_backward,
     "row_sum_max": launch_row_sum_max,
@@ -821,6 +885,15 @@ def prepare_inputs(name: str, cpu_inputs: tuple[torch.Tensor, ...],
     if name == "ffn_backward":
         x, w1, w2, dout = ins
         return x, linear_layout(w1), linear_layout(w2), dout
+    if name == "ffn_backward_saved":
+        x, w1, w2, dout = ins
+        w1, w2 = linear_layout(w1), linear_layout(w2)
+        rows, f = x.shape[0], w1.shape[0]
+        rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
+        u = torch.empty((rows, f), device=x.device, dtype=torch.bfloat16)
+        h = torch.empty_like(u)
+        ffn_train_forward(x, w1, w2, torch.empty_like(x), rstd, u, h, FFN_EPS, make_cfg())
+        return x, w1, w2, dout, rstd, u, h
     return ins
 
 
@@ -844,7 +917,7 @@ def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch
         return torch.empty_like(x), torch.empty(rows, **f32), torch.empty(rows, **f32)
     if name == "rowwise_quant":
         return torch.empty(x.shape, device=x.device, dtype=torch.int8), torch.empty(rows, **f32)
-    if name == "ffn_backward":
+    if name in ("ffn_backward", "ffn_backward_saved"):
         w1 = inputs[1]
         return torch.empty_like(x), torch.empty_like(w1), torch.empty_like(inputs[2])
     if name in ("lars_momentum", "pearson_backward"):

@@ -349,6 +349,19 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         algorithmic_bytes=lambda r, c: 2 * (3 * r * c + 4 * c * 28672),
         tolerances=(BF16_TOL, BF16_TOL, BF16_TOL),
     ),
+    # The same gradients from the training forward's saved rstd, u and h
+    # (no recompute GEMM).
+    "ffn_backward_saved": WorkloadSpec(
+        name="ffn_backward_saved",
+        label="Norm-fused FFN backward from saved activations (bf16 MFMA)",
+        category="gemm",
+        rows=4096,
+        cols=8192,
+        input_factory=make_ffn_backward_inputs,
+        output_names=("dx", "dw1", "dw2"),
+        algorithmic_bytes=lambda r, c: 2 * (3 * r * c + 4 * c * 28672),
+        tolerances=(BF16_TOL, BF16_TOL, BF16_TOL),
+    ),
     # Reference workloads (dsmem_eval/workloads.py:157-212).
     "layernorm_backward": WorkloadSpec(
         name="layernorm_backward",

@@ -354,9 +354,11 @@ int credit_pearson_bwd_f32(const float* x, const float* y, const float* grad, fl
                            const credit_cfg* cfg);
 
 /* ------------------------------------------ C5: norm-fused FFN ----------
- * out = bf16(x + bf16(GELU_tanh(bf16(x * rstd) @ W1^T)) @ W2^T) with
+ * out = bf16(x + h @ W2^T), h = bf16(GELU_tanh(rstd * (x @ W1^T))) with
  * rstd = 1/sqrt(mean_j x^2 + eps) per row (RMSNorm with unit weight), fp32
- * accumulation on bf16 MFMA.  Weights in the nn.Linear layout:
+ * accumulation on bf16 MFMA.  (Shapes that take the 128 x 128 tile GEMM --
+ * d or f not a multiple of 256 -- form h = bf16(GELU_tanh(bf16(x * rstd) @
+ * W1^T)): the normalised input rounded to bf16 before the product.)  Weights in the nn.Linear layout:
  * w1 [f, d] and w2 [d, f] (K contiguous).  x, out [rows, d].  rows, d and
  * f must be multiples of 128; buffers 16-byte aligned.  The hidden
  * activation h [rows, f] lives in the workspace (query with
@@ -374,6 +376,18 @@ int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w1, const ui
 int credit_ffn_rmsnorm_gelu_kn_bf16(const uint16_t* x, const uint16_t* w1, const uint16_t* w2,
                                     uint16_t* out, int64_t rows, int64_t d, int64_t f, float eps,
                                     const credit_cfg* cfg);
+/* The forward of a training step: credit_ffn_rmsnorm_gelu_bf16 (nn.Linear
+ * weights) that also hands back what its backward needs, so that
+ * credit_ffn_rmsnorm_gelu_bwd_saved_bf16 need not recompute it: rstd
+ * [rows] fp32, u [rows, f] = bf16(rstd * (x @ W1^T)) and h [rows, f] =
+ * bf16(GELU_tanh(rstd * (x @ W1^T))), both bf16 row-major (h is the hidden
+ * activation GEMM2 reads).  out is bit-identical to
+ * credit_ffn_rmsnorm_gelu_bf16.  No workspace.  Same shape and alignment
+ * rules (u and h 16-byte aligned too).  No counterpart in the reference. */
+int credit_ffn_rmsnorm_gelu_fwd_train_bf16(const uint16_t* x, const uint16_t* w1,
+                                           const uint16_t* w2, uint16_t* out, float* rstd,
+                                           uint16_t* u, uint16_t* h, int64_t rows, int64_t d,
+                                           int64_t f, float eps, const credit_cfg* cfg);
 
 /* ----------------------------------- FFN backward (next row of C5) -------
  * The gradients of out = x + GELU_tanh(RMSNorm(x) @ W1^T) @ W2^T (unit
@@ -393,8 +407,24 @@ int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_t* w1, cons
                                      const uint16_t* dout, uint16_t* dx, uint16_t* dw1,
                                      uint16_t* dw2, int64_t rows, int64_t d, int64_t f, float eps,
                                      const credit_cfg* cfg);
-/* Workspace bytes the FFN backward needs at (rows, d, f); 0 for an empty
- * shape.  Plumbing of this ABI, no counterpart in the reference. */
+/* The same gradients from the saved rstd, u and h of
+ * credit_ffn_rmsnorm_gelu_fwd_train_bf16 on the same x, w1, w2: four GEMMs
+ * instead of five (no recompute of u; h is read as the dW2 GEMM's [K, N]
+ * operand, so it needs no transpose either).  dx, dw1 and dw2 are
+ * bit-identical to credit_ffn_rmsnorm_gelu_bwd_bf16's.  eps is the
+ * forward's (already in rstd).  Same shape, alignment and workspace rules as
+ * credit_ffn_rmsnorm_gelu_bwd_bf16.  No counterpart in the reference: the
+ * training-step form of the FFN backward, for callers that keep the
+ * forward's activations. */
+int credit_ffn_rmsnorm_gelu_bwd_saved_bf16(const uint16_t* x, const uint16_t* w1,
+                                           const uint16_t* w2, const uint16_t* dout,
+                                           const float* rstd, const uint16_t* u,
+                                           const uint16_t* h, uint16_t* dx, uint16_t* dw1,
+                                           uint16_t* dw2, int64_t rows, int64_t d, int64_t f,
+                                           const credit_cfg* cfg);
+/* Workspace bytes the FFN backward (either form) needs at (rows, d, f); 0
+ * for an empty shape.  Plumbing of this ABI, no counterpart in the
+ * reference. */
 size_t credit_ffn_bwd_workspace_bytes(int64_t rows, int64_t d, int64_t f);
 
 /* dst[c, r] = src[r, c] for a rows x cols bf16 matrix: converts a [d, f]

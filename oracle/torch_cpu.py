@@ -123,6 +123,17 @@ def ffn_backward(x, w1, w2, dout, eps=1.0e-6):
     return x.grad, w1.grad, w2.grad
 
 
+def ffn_backward_saved(x, w1, w2, dout, eps=1.0e-6):
+    """The autograd graph of ffn() built once, its activations kept: returns
+    a function that runs only the backward pass, (dx, dW1, dW2)."""
+    x = x.detach().requires_grad_()
+    w1 = w1.detach().requires_grad_()
+    w2 = w2.detach().requires_grad_()
+    a = F.rms_norm(x.float(), (x.shape[-1],), None, eps).to(x.dtype)
+    out = x + F.gelu(a @ w1, approximate="tanh") @ w2
+    return lambda: torch.autograd.grad(out, (x, w1, w2), dout, retain_graph=True)
+
+
 # name -> (function, which BASELINE inputs it takes)
 FUNCTIONS = {
     "row_sum_max": row_sum_max,
@@ -144,4 +155,7 @@ FUNCTIONS = {
     "ffn": ffn,
     "ffn_baseline_layout": ffn,
     "ffn_backward": ffn_backward,
+    # Builds the graph and returns the backward-only call (bench.py times
+    # that call).
+    "ffn_backward_saved": ffn_backward_saved,
 }

@@ -74,7 +74,8 @@ def test_golden_set_covers_every_launcher():
     covered = {fixtures.load(c)[0]["workload"] for c in fixtures.cases()}
     # ffn_baseline_layout runs the ffn fixture with its weights transposed
     # to [in, out] (tests/test_gpu_golden.py).
-    assert covered == set(HIP_LAUNCHERS) - {"ffn_backward", "ffn_baseline_layout"}
+    assert covered == set(HIP_LAUNCHERS) - {"ffn_backward", "ffn_backward_saved",
+                                             "ffn_baseline_layout"}
 
 
 def test_golden_fixtures_catch_a_planted_mistake():

@@ -10,6 +10,8 @@ layout or transpose scrambles every output by O(1) of that scale.  Shapes
 cover the 128-tile GEMMs, the 256-tile GEMMs and mixtures of both; at the
 full C5 shape sampled rows of dx and sampled columns of dW1 / dW2 are checked
 (each depends only on its own rows / columns of the intermediates)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -119,3 +121,92 @@ def test_ffn_backward_full_shape_samples(gpu):
         du = ref.round_bf16((G @ W2[f0, :]) * ref.gelu_tanh_grad(ref.round_bf16(u)))
         close(dw2[f0], h @ G, f"dW2 row {f0}")
         close(dw1[:, f0], a.T @ du, f"dW1 column {f0}")
+
+
+# ------------------------------------------------ saved-activation form --
+
+
+def run_train_forward(x, w1l, w2l, gpu):
+    """The training forward on device tensors (w1l [f, d], w2l [d, f])."""
+    rows, f = x.shape[0], w1l.shape[0]
+    out = torch.full_like(x, float("nan"))
+    rstd = torch.full((rows,), float("nan"), device=gpu)
+    u = torch.full((rows, f), float("nan"), device=gpu, dtype=torch.bfloat16)
+    h = torch.full_like(u, float("nan"))
+    hip_lib.ffn_train_forward(x, w1l, w2l, out, rstd, u, h, EPS, hip_lib.make_cfg())
+    return out, rstd, u, h
+
+
+@pytest.mark.parametrize("rows,d,f", [(128, 128, 256), (256, 128, 512), (512, 512, 1024),
+                                      (1024, 512, 2048)])
+def test_ffn_train_forward(gpu, rows, d, f):
+    """out bit-identical to the plain forward; rstd, u and h against the
+    float64 oracle (u and h with the arithmetic of the GEMM path the shape
+    takes: bf16(x rstd) on 128 tiles, rstd on the fp32 sum on 256 tiles)."""
+    print(f"ffn train forward rows={rows} d={d} f={f}", flush=True)
+    x, w1, w2, _ = make(rows, d, f, seed=3 * rows + f)
+    xs = x.to(gpu)
+    w1l, w2l = hip_lib.linear_layout(w1.to(gpu)), hip_lib.linear_layout(w2.to(gpu))
+    out, rstd, u, h = run_train_forward(xs, w1l, w2l, gpu)
+    plain = torch.empty_like(xs)
+    hip_lib.ffn(xs, w1l, w2l, plain, EPS, hip_lib.make_cfg())
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), plain.view(torch.int16))
+    X = x.float().numpy().astype(np.float64)
+    ers = 1.0 / np.sqrt((X * X).mean(-1) + EPS)
+    np.testing.assert_allclose(rstd.cpu().numpy(), ers, rtol=1e-5, atol=1e-6)
+    big = d % 256 == 0 and f % 256 == 0
+    a = X * ers[:, None] if big else ref.round_bf16(X * ers[:, None])
+    eu = a @ w1.float().numpy().astype(np.float64)
+    close(u.float().cpu().numpy(), eu, "u")
+    close(h.float().cpu().numpy(), ref.gelu_tanh(eu), "h")
+
+
+@pytest.mark.parametrize("rows,d,f", [(128, 128, 128), (256, 128, 512), (384, 512, 256),
+                                      (512, 512, 1024), (1024, 512, 2048), (4096, 8192, 28672)])
+def test_ffn_backward_saved_is_bit_identical(gpu, rows, d, f):
+    """The backward from the training forward's rstd, u and h gives the
+    recomputing backward's bits: the saved u and h are the recomputed ones,
+    and h read as a [K, N] operand feeds the dW2 GEMM the same values in the
+    same order as h^T.  Includes the full C5 shape."""
+    print(f"ffn_backward_saved rows={rows} d={d} f={f}", flush=True)
+    x, w1, w2, dout = make(rows, d, f, seed=rows + 2 * d + f)
+    xs, ds = x.to(gpu), dout.to(gpu)
+    w1l, w2l = hip_lib.linear_layout(w1.to(gpu)), hip_lib.linear_layout(w2.to(gpu))
+    _, rstd, u, h = run_train_forward(xs, w1l, w2l, gpu)
+    outs = []
+    for saved in (False, True):
+        dx = torch.full_like(xs, float("nan"))
+        dw1 = torch.full_like(w1l, float("nan"))
+        dw2 = torch.full_like(w2l, float("nan"))
+        if saved:
+            hip_lib.ffn_backward_saved(xs, w1l, w2l, ds, rstd, u, h, dx, dw1, dw2,
+                                       hip_lib.make_cfg())
+        else:
+            hip_lib.ffn_backward(xs, w1l, w2l, ds, dx, dw1, dw2, EPS, hip_lib.make_cfg())
+        torch.cuda.synchronize()
+        outs.append((dx, dw1, dw2))
+    for name, a, b in zip(("dx", "dw1", "dw2"), *outs):
+        assert not torch.isnan(b.float()).any(), name
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), name
+    del outs, u, h
+    torch.cuda.empty_cache()
+
+
+def test_ffn_backward_saved_rejects_bad_shapes(gpu):
+    x, w1, w2, dout = make(128, 128, 256, seed=11)
+    xs, ds = x.to(gpu), dout.to(gpu)
+    w1l, w2l = hip_lib.linear_layout(w1.to(gpu)), hip_lib.linear_layout(w2.to(gpu))
+    _, rstd, u, h = run_train_forward(xs, w1l, w2l, gpu)
+    dx, dw1, dw2 = torch.empty_like(xs), torch.empty_like(w1l), torch.empty_like(w2l)
+    with pytest.raises(ValueError):  # u of the wrong width
+        hip_lib.ffn_backward_saved(xs, w1l, w2l, ds, rstd, u[:, :128], h, dx, dw1, dw2,
+                                   hip_lib.make_cfg())
+    with pytest.raises(hip_lib.CreditError):  # misaligned h (checked in the library)
+        hv = h.view(-1)[1:].view(-1)[: h.numel() - 8]
+        lib = hip_lib.load_library()
+        st = lib.credit_ffn_rmsnorm_gelu_bwd_saved_bf16(
+            xs.data_ptr(), w1l.data_ptr(), w2l.data_ptr(), ds.data_ptr(), rstd.data_ptr(),
+            u.data_ptr(), hv.data_ptr(), dx.data_ptr(), dw1.data_ptr(), dw2.data_ptr(), 128, 128,
+            256, ctypes.byref(hip_lib.make_cfg()))
+        hip_lib.check(st, "credit_ffn_rmsnorm_gelu_bwd_saved_bf16")
