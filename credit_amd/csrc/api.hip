@@ -183,14 +183,21 @@ struct HostFlag {
 };
 std::mutex g_host_flag_mu;
 std::vector<HostFlag> g_host_flags;
+thread_local bool g_in_noalloc = false;
 
-int host_watchdog_flag(int device, HostFlag* out) {
+// The device's flag; with allow_alloc false and none allocated yet, a flag
+// with null words (the caller then goes without it).
+int host_watchdog_flag(int device, HostFlag* out, bool allow_alloc = true) {
   std::lock_guard<std::mutex> lock(g_host_flag_mu);
   for (const HostFlag& f : g_host_flags)
     if (f.device == device) {
       *out = f;
       return CREDIT_OK;
     }
+  if (!allow_alloc) {
+    *out = HostFlag{device, nullptr, nullptr};
+    return CREDIT_OK;
+  }
   void* p = nullptr;
   CREDIT_HIP(hipHostMalloc(&p, 64, hipHostMallocMapped));
   *static_cast<volatile uint32_t*>(p) = 0;
@@ -202,13 +209,17 @@ int host_watchdog_flag(int device, HostFlag* out) {
   return CREDIT_OK;
 }
 
+NoAllocScope::NoAllocScope() : prev_(g_in_noalloc) { g_in_noalloc = true; }
+NoAllocScope::~NoAllocScope() { g_in_noalloc = prev_; }
+bool in_noalloc_call() { return g_in_noalloc; }
+
 int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
                             int k_values, int ring, size_t extra_bytes, SplitWorkspace* out) {
   int device = 0;
   CREDIT_HIP(hipGetDevice(&device));
   HostFlag flag;
-  CREDIT_TRY(host_watchdog_flag(device, &flag));
-  if (*flag.host != 0)
+  CREDIT_TRY(host_watchdog_flag(device, &flag, !g_in_noalloc));
+  if (flag.host != nullptr && *flag.host != 0)
     return set_error(CREDIT_ERR_WATCHDOG,
                      "an earlier split launch on device %d gave up waiting for its group (its "
                      "outputs are wrong); credit_check_watchdog() reports and clears this",
@@ -397,6 +408,23 @@ size_t credit_ffn_bwd_workspace_bytes(int64_t rows, int64_t d, int64_t f) {
 
 int credit_check_watchdog(const credit_cfg* cfg) {
   CREDIT_TRY(check_cfg(cfg));
+  // The allocation-free entry points' fixed array has a watchdog word of its
+  // own (they go without the host-mapped one when none exists yet).
+  bool noalloc_flag = false;
+  {
+    int dev = 0;
+    CREDIT_HIP(hipGetDevice(&dev));
+    if (char* na = noalloc_scratch_base(dev)) {
+      uint32_t w = 0;
+      CREDIT_HIP(hipDeviceSynchronize());
+      CREDIT_HIP(hipMemcpy(&w, na, sizeof(w), hipMemcpyDeviceToHost));
+      if (w != 0) {
+        CREDIT_HIP(hipMemset(na, 0, kScratchOffset));
+        CREDIT_HIP(hipDeviceSynchronize());
+        noalloc_flag = true;
+      }
+    }
+  }
   char* base = nullptr;
   if (cfg != nullptr && cfg->workspace != nullptr) {
     CREDIT_TRY(acquire_workspace(cfg, 0, &base));
@@ -408,7 +436,7 @@ int credit_check_watchdog(const credit_cfg* cfg) {
       CREDIT_HIP(hipDeviceSynchronize());
       HostFlag hf;
       CREDIT_TRY(host_watchdog_flag(dev, &hf));
-      if (*hf.host == 0) return CREDIT_OK;
+      if (*hf.host == 0 && !noalloc_flag) return CREDIT_OK;
       *hf.host = 0;
       return set_error(CREDIT_ERR_WATCHDOG, "a split-row barrier exceeded its spin limit");
     }
@@ -429,7 +457,7 @@ int credit_check_watchdog(const credit_cfg* cfg) {
     CREDIT_HIP(hipMemset(base, 0, kScratchOffset));
     CREDIT_HIP(hipDeviceSynchronize());
   }
-  if (flag != 0 || device_flag)
+  if (flag != 0 || device_flag || noalloc_flag)
     return set_error(CREDIT_ERR_WATCHDOG,
                      "a split-row barrier exceeded its spin limit");
   return CREDIT_OK;

@@ -140,6 +140,26 @@ inline size_t split_workspace_bytes(int64_t groups, int members, int k_values, i
 int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
                             int k_values, int ring, size_t extra_bytes, SplitWorkspace* out);
 
+// Marks the calls this thread makes inside an allocation-free entry point
+// (credit_*_noalloc): the split workspace then uses the device's host-mapped
+// watchdog word only if an earlier call already allocated it, and allocates
+// none (the expiry still raises the workspace's own watchdog word, which
+// credit_check_watchdog reads).
+class NoAllocScope {
+ public:
+  NoAllocScope();
+  ~NoAllocScope();
+  NoAllocScope(const NoAllocScope&) = delete;
+  NoAllocScope& operator=(const NoAllocScope&) = delete;
+
+ private:
+  bool prev_;
+};
+bool in_noalloc_call();
+// The allocation-free scratch array of `device` once an allocation-free
+// call has looked its address up on that device (nullptr before).
+char* noalloc_scratch_base(int device);
+
 // Split launches wait inside a group for all of its members, and the
 // dispatcher does not reliably start a pending workgroup on a CU that a
 // finished group freed while resident workgroups spin (measured on MI355X:

@@ -1004,8 +1004,9 @@ constexpr size_t kNoAllocScratchBytes = size_t{40} << 20;
 static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 
 namespace {
+constexpr int kNoAllocMaxDevices = 64;
 std::mutex g_noalloc_mu;
-std::vector<char*> g_noalloc_base;  // per device: scratch's device address
+char* g_noalloc_base[kNoAllocMaxDevices] = {};  // per device: scratch's device address
 
 // The device address of `scratch` on the current device, looked up once
 // per device.  The host-side name is only a handle for the lookup, never an
@@ -1013,8 +1014,10 @@ std::vector<char*> g_noalloc_base;  // per device: scratch's device address
 int noalloc_scratch(char** out) {
   int dev = 0;
   CREDIT_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return set_error(CREDIT_ERR_UNSUPPORTED, "allocation-free calls support devices 0..%d",
+                     kNoAllocMaxDevices - 1);
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
-  if (static_cast<int>(g_noalloc_base.size()) <= dev) g_noalloc_base.resize(dev + 1, nullptr);
   if (g_noalloc_base[dev] == nullptr) {
     void* p = nullptr;
     const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -1027,6 +1030,12 @@ int noalloc_scratch(char** out) {
   return CREDIT_OK;
 }
 }  // namespace
+
+char* noalloc_scratch_base(int device) {
+  if (device < 0 || device >= kNoAllocMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  return g_noalloc_base[device];
+}
 
 }  // namespace credit
 
@@ -1190,6 +1199,7 @@ extern "C" int credit_rmsnorm_bwd_bf16_noalloc(const uint16_t* x, const uint16_t
   credit_cfg c = cfg != nullptr ? *cfg : credit_cfg{nullptr, CREDIT_VARIANT_AUTO, 0, nullptr, 0};
   c.workspace = base;
   c.workspace_bytes = kNoAllocScratchBytes;
+  const NoAllocScope no_alloc;  // no host-mapped watchdog word is allocated for it
   return credit_rmsnorm_bwd_bf16(x, w, dy, rstd, dx, dw, rows, cols, &c);
 }
 

@@ -265,9 +265,12 @@ int credit_rmsnorm_fwd_bwd_bf16(const uint16_t* x, const uint16_t* w, const uint
  * CREDIT_ERR_WORKSPACE, and a cfg->workspace is refused (CREDIT_ERR_BAD_CONFIG).
  * Outputs equal credit_rmsnorm_bwd_bf16's bit for bit.  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (other streams,
- * other threads) race and must not be issued.  A split-barrier timeout is
- * not reported (the array's watchdog word has no host-visible reader that
- * allocates nothing); outputs are then wrong, as with the allocating call. */
+ * other threads) race and must not be issued.  A split-barrier timeout
+ * (outputs then wrong, as with the allocating call) raises the array's own
+ * watchdog word, which credit_check_watchdog reads, reports and clears;
+ * the device's sticky host-mapped word (later split calls refuse) is raised
+ * too only if an allocating split call created it earlier -- this call
+ * creates none. */
 int credit_rmsnorm_bwd_bf16_noalloc(const uint16_t* x, const uint16_t* w, const uint16_t* dy,
                                     const float* rstd, uint16_t* dx, float* dw, int64_t rows,
                                     int64_t cols, const credit_cfg* cfg);

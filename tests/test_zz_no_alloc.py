@@ -44,8 +44,10 @@ def test_noalloc_matches_the_allocating_entry_point(gpu, first, second):
     for shape, seed in ((first, 11), (second, 12)):
         print(f"rmsnorm_bwd noalloc shape={shape}", flush=True)
         ins = _inputs(*shape, seed, gpu)
-        ref = _run(lib.credit_rmsnorm_bwd_bf16, *ins)
+        # The allocation-free call first: in a fresh process no allocating
+        # split call has run yet, so it runs without a host-mapped watchdog word.
         got = _run(lib.credit_rmsnorm_bwd_bf16_noalloc, *ins)
+        ref = _run(lib.credit_rmsnorm_bwd_bf16, *ins)
         assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
     hip_lib.check_watchdog()
 
@@ -75,3 +77,27 @@ def test_noalloc_split_and_rejections(gpu):
     dx2, dw2 = hip_lib.allocate_outputs("rmsnorm_bwd", ins)
     status = lib.credit_rmsnorm_bwd_bf16_noalloc(*_args(x, w2, dy, r, dx2, dw2, cfg))
     assert status == -8
+
+
+def test_noalloc_expired_wait_is_reported(gpu):
+    """A bounded wait forced to expire inside the allocation-free call (spin
+    limit 0, from the host) raises the fixed array's watchdog word:
+    credit_check_watchdog reports it and re-zeroes the array's header and
+    counters, and the next call matches the allocating entry point again."""
+    lib = hip_lib.load_library()
+    ins = _inputs(64, 65536, 21, gpu)
+    ref = _run(lib.credit_rmsnorm_bwd_bf16, *ins, "split", 8)
+    hip_lib.check_watchdog()
+    print("forcing an expired wait in the allocation-free call (spin limit 0)", flush=True)
+    prev = hip_lib.set_spin_limit(0)
+    try:
+        _run(lib.credit_rmsnorm_bwd_bf16_noalloc, *ins, "split", 8)
+    finally:
+        hip_lib.set_spin_limit(prev)
+    with pytest.raises(hip_lib.CreditError) as err:
+        hip_lib.check_watchdog()
+    assert err.value.status == -7  # CREDIT_ERR_WATCHDOG
+    hip_lib.check_watchdog()  # cleared
+    got = _run(lib.credit_rmsnorm_bwd_bf16_noalloc, *ins, "split", 8)
+    assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
+    hip_lib.check_watchdog()
