@@ -164,6 +164,20 @@ uint32_t next_split_epoch(uint32_t stages) {
           for (const WsBuffer& b : workspace_cache().live())
             if (b.ptr != nullptr) (void)hipMemset(b.ptr + kSlotOffset, 0, kSlotAreaBytes);
         (void)hipDeviceSynchronize();
+        // So do the allocation-free entry points' fixed arrays, on every
+        // device that has used one.
+        int cur = 0;
+        if (hipGetDevice(&cur) == hipSuccess) {
+          int count = 0;
+          if (hipGetDeviceCount(&count) != hipSuccess) count = 0;
+          for (int d = 0; d < count; ++d)
+            if (char* na = noalloc_scratch_base(d)) {
+              if (hipSetDevice(d) != hipSuccess) continue;
+              (void)hipMemset(na + kSlotOffset, 0, kSlotAreaBytes);
+              (void)hipDeviceSynchronize();
+            }
+          (void)hipSetDevice(cur);
+        }
       }
       return start;
     }
