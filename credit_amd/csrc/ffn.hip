@@ -523,10 +523,8 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // MFMA M of a sub-step: fragment read M of the next sub-step first (M < 8);
-  // with NL loads numbered Q0.. of step lk, load j follows MFMA
-  // (j + 1) * (16 / NL) - 1.
-  auto mfma = [&]<int Q0, int NL, int Mi>(const Frags& cur, Frags& nxt, int ns, int nkk, int lk) {
+  // MFMA Mi of a sub-step: fragment read Mi of the next sub-step first (Mi < 8).
+  auto mfma = [&]<int Mi>(const Frags& cur, Frags& nxt, int ns, int nkk) {
     if constexpr (Mi < 8) {
       const bf16x8_t v = frag(ns, nkk, Mi);
       if constexpr (Mi < 4)
@@ -536,31 +534,37 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     }
     acc[Mi >> 2][Mi & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
         cur.a[Mi >> 2], cur.b[Mi & 3], acc[Mi >> 2][Mi & 3], 0, 0, 0);
-    if constexpr (NL > 0) {
-      constexpr int stride = 16 / NL;
-      if constexpr ((Mi + 1) % stride == 0 && (Mi + 1) / stride <= NL)
-        load(lk, std::integral_constant<int, Q0 + (Mi + 1) / stride - 1>{});
-    }
   };
-  auto sub_step = [&]<int Q0, int NL>(const Frags& cur, Frags& nxt, int ns, int nkk, int lk) {
-    [&]<int... Ms>(std::integer_sequence<int, Ms...>) {
-      (mfma.template operator()<Q0, NL, Ms>(cur, nxt, ns, nkk, lk), ...);
-    }(std::make_integer_sequence<int, 16>{});
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {  // a KN B fragment is two reads
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, KN ? 2 : 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
-    __builtin_amdgcn_sched_barrier(0);
+  // A sub-step is four quarters of four MFMAs; load Q0 + j (of step lk)
+  // follows quarter j.  Each quarter is a scheduling region of its own (the
+  // MFMAs would otherwise drift past the inline-assembly loads and leave
+  // them in bursts), with its fragment reads pinned one per MFMA.
+  auto sub_step = [&]<int Q0>(const Frags& cur, Frags& nxt, int ns, int nkk, int lk) {
+    [&]<int... Qs>(std::integer_sequence<int, Qs...>) {
+      (
+          [&] {
+            constexpr int Qi = Qs;
+            [&]<int... Js>(std::integer_sequence<int, Js...>) {
+              (mfma.template operator()<4 * Qi + Js>(cur, nxt, ns, nkk), ...);
+            }(std::make_integer_sequence<int, 4>{});
+            load(lk, std::integral_constant<int, Q0 + Qi>{});
+            [&]<int... Js>(std::integer_sequence<int, Js...>) {
+              (
+                  [&] {
+                    constexpr int Mi = 4 * Qi + Js;
+                    if constexpr (Mi < 8)  // a KN B fragment is two reads
+                      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, KN && Mi >= 4 ? 2 : 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                  }(),
+                  ...);
+            }(std::make_integer_sequence<int, 4>{});
+            __builtin_amdgcn_sched_barrier(0);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, 4>{});
   };
 
-  // Prologue: steps 0 and 1 whole (B before A in each step's issue order).
+  // Prologue: step 0 whole, then B of step 1 and the first half of its A.
   [&]<int... Qs>(std::integer_sequence<int, Qs...>) {
     (load(0, std::integral_constant<int, Qs>{}), ...);
   }(std::make_integer_sequence<int, 16>{});
@@ -569,8 +573,8 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
   }(std::make_integer_sequence<int, 8>{});
   [&]<int... Qs>(std::integer_sequence<int, Qs...>) {
     (load(1, std::integral_constant<int, Qs>{}), ...);
-  }(std::make_integer_sequence<int, 8>{});
-  wait_vmcnt<16>();  // own loads of step 0 landed
+  }(std::make_integer_sequence<int, 4>{});
+  wait_vmcnt<12>();  // own loads of step 0 landed
   lds_barrier();
   Frags f0, f1;
 #pragma unroll
@@ -581,18 +585,20 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     else
       f0.b[m - 4] = v;
   }
-  // Iteration it computes step it.  Sub-steps 0-2 issue B of step it+2 (its
-  // stage (it+2) % 3 was last read in step it-1, before the previous
-  // barrier); after this iteration's barrier, sub-step 3 issues A of step
-  // it+2 into A stage it & 1, whose reads all precede the barrier.  The wait
-  // before the barrier leaves B of step it+2 (8 loads) in flight.
+  // Iteration it computes step it, four loads per sub-step.  Sub-step 0
+  // issues the second half of A of step it+1 (its stage (it+1) & 1 was last
+  // read in step it-1, before the previous barrier), sub-steps 1-2 B of step
+  // it+2 (stage (it+2) % 3, last read in step it-1), and after this
+  // iteration's barrier sub-step 3 the first half of A of step it+2 into A
+  // stage it & 1, whose reads all precede the barrier.  The wait before the
+  // barrier leaves B of step it+2 (8 loads) in flight.
   auto iteration = [&](int it) {
-    sub_step.template operator()<8, 3>(f0, f1, it, 1, it + 2);
-    sub_step.template operator()<11, 3>(f1, f0, it, 2, it + 2);
-    sub_step.template operator()<14, 2>(f0, f1, it, 3, it + 2);
+    sub_step.template operator()<4>(f0, f1, it, 1, it + 1);
+    sub_step.template operator()<8>(f1, f0, it, 2, it + 2);
+    sub_step.template operator()<12>(f0, f1, it, 3, it + 2);
     wait_vmcnt<8>();  // own loads of step it+1 landed
     lds_barrier();
-    sub_step.template operator()<0, 8>(f1, f0, it + 1, 0, it + 2);
+    sub_step.template operator()<0>(f1, f0, it + 1, 0, it + 2);
   };
   for (int it = 0; it < iters; ++it) iteration(it);
   wait_vmcnt<0>();  // the tail re-loads

@@ -200,11 +200,13 @@ def profile_as_dict(profile: DeviceProfile) -> dict[str, Any]:
     return asdict(profile)
 
 
-def run_ffn_reference(rows: int = 4096, d: int = 8192, f: int = 28672) -> None:
+def run_ffn_reference(rows: int = 4096, d: int = 8192, f: int = 28672, reps: int = 2,
+                      gemm2: bool = False) -> None:
     """The FFN forward (this library's two GEMMs) and the vendor library's GEMM
-    of GEMM1's shape (torch.matmul -> hipBLASLt), twice each, on random bf16
-    operands in the nn.Linear layouts: a workload for per-kernel counter
-    collection (rocprofv3 --pmc), not a benchmark."""
+    of GEMM1's shape (torch.matmul -> hipBLASLt), `reps` times each, on random
+    bf16 operands in the nn.Linear layouts; with `gemm2` also the vendor GEMM of
+    GEMM2's shape (h @ W2^T).  A workload for per-kernel counter collection
+    (rocprofv3 --pmc), not a benchmark."""
     import torch
 
     dev = torch.device("cuda:0")
@@ -215,12 +217,17 @@ def run_ffn_reference(rows: int = 4096, d: int = 8192, f: int = 28672) -> None:
     w2 = (torch.randn(d, f, device=dev, generator=g) / f ** 0.5).bfloat16()
     out = torch.empty_like(x)
     cfg = hip_lib.make_cfg("auto")
-    for _ in range(2):
+    for _ in range(reps):
         hip_lib.ffn(x, w1, w2, out, hip_lib.FFN_EPS, cfg)
     torch.cuda.synchronize()
-    for _ in range(2):
+    for _ in range(reps):
         torch.matmul(x, w1.t())
     torch.cuda.synchronize()
+    if gemm2:
+        h = torch.randn(rows, f, device=dev, generator=g).bfloat16()
+        for _ in range(reps):
+            torch.matmul(h, w2.t())
+        torch.cuda.synchronize()
     print("ffn reference workload done", flush=True)
 
 
@@ -239,11 +246,14 @@ def main(argv=None) -> int:
     ap.add_argument("--ffn-reference", action="store_true",
                     help="run the C5 FFN forward twice, then hipBLASLt (torch.matmul) on GEMM1's "
                          "shape twice: the workload of the FFN-against-library counter runs")
+    ap.add_argument("--reps", type=int, default=2, help="calls of each in --ffn-reference")
+    ap.add_argument("--gemm2", action="store_true",
+                    help="--ffn-reference also runs hipBLASLt on GEMM2's shape")
     args = ap.parse_args(argv)
     import torch  # noqa: F401  (loads the HIP runtime torch uses before the library)
 
     if args.ffn_reference:
-        run_ffn_reference()
+        run_ffn_reference(reps=args.reps, gemm2=args.gemm2)
         return 0
     if args.ceilings:
         sys.stdout.write(ceiling_table([int(b) for b in args.ceilings.split(",") if b.strip()]))
