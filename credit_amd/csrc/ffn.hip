@@ -64,21 +64,26 @@ constexpr int kEpiStoreF32 = 5;
 constexpr int kEpiGeluSave = 6;
 
 // GELU with the tanh approximation, z = sqrt(2/pi) (v + 0.044715 v^3):
-// 0.5 (1 + tanh z) = sigmoid(2z) = s = e r with e = e^(2z) and
-// r = 1 / (e + 1) = 1 - s, so GELU(v) = v s.  e = 2^(2z log2 e) is one
-// hardware exp2 and r one hardware reciprocal (about 1 ulp each); s = e r
-// has no cancellation on either side (1 - r would cancel on the negative
-// tail, where r is within an ulp of 1 below v of about -4), so GELU and
-// GELU' keep a relative error of a few ulp everywhere, far below the bf16
-// rounding of h and du (4e-3) that follows every use.  The exponent is
-// capped at 64 (v above about 6.6): e stays finite, s rounds to 1 and r
-// to 2^-64, so GELU = v and GELU' = 1 up to rounding, and +inf gives +inf.
-// Against the correctly rounded division and double-float exp it replaces:
-// GEMM1's epilogue is ~4x cheaper.
+// 0.5 (1 + tanh z) = sigmoid(2z), so GELU(v) = v / (1 + e') with
+// e' = e^(-2z) = 2^(v t), t = -2 sqrt(2/pi) log2(e) (1 + 0.044715 v^2): one
+// hardware exp2 and one hardware reciprocal (about 1 ulp each), no
+// cancellation on either side.  On the negative tail e' is large and 1/(1 +
+// e') keeps its relative accuracy until e' overflows (v below about -10.5,
+// GELU below 4e-38 in magnitude), where rcp(inf) = 0 gives -0; on the
+// positive side e' -> 0 and GELU -> v, +inf giving +inf.
 constexpr float kGeluC = 0.7978845608028654f;   // sqrt(2/pi)
 constexpr float kGeluC2 = 2.302208198144325f;   // 2 sqrt(2/pi) log2(e)
 constexpr float kGeluA = 0.044715f;
 
+__device__ __forceinline__ float gelu_tanh(float v) {
+  const float t = __builtin_fmaf(-kGeluC2 * kGeluA, v * v, -kGeluC2);
+  return v * __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(v * t) + 1.0f);
+}
+
+// GELU' needs both s = sigmoid(2z) and r = 1 - s = sigmoid(-2z): with e =
+// e^(2z) = 2^(arg), r = 1 / (e + 1) and s = e r, neither cancelling.  The
+// exponent is capped at 64 (v above about 6.6), so e stays finite, s rounds
+// to 1 and r to 2^-64.
 struct GeluParts {
   float r;  // 1 / (e + 1) = 1 - s
   float s;  // sigmoid(2z) = 0.5 (1 + tanh z)
@@ -92,8 +97,6 @@ __device__ __forceinline__ GeluParts gelu_parts(float v, float v2) {
   g.s = e * g.r;
   return g;
 }
-
-__device__ __forceinline__ float gelu_tanh(float v) { return v * gelu_parts(v, v * v).s; }
 
 // d/dv GELU = s + 2 v r s dz/dv, dz/dv = sqrt(2/pi) (1 + 3 * 0.044715 v^2).
 __device__ __forceinline__ float gelu_tanh_grad(float v) {
@@ -625,11 +628,21 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     wait_vmcnt<0>();
     lds_barrier();
   }
-  auto r_at = [&](int m, int n) { return bf16_to_f32(r_tile[(m - m0) * kBig + (n - n0)]); };
+  // R at rows mb .. mb + 3 (mb = the row of accumulator register 4q of tile
+  // (i, j)) and the lane's column, by one ds_read_b64_tr_b16: group lane k
+  // of each 16-lane group addresses tile row mb + k / 4, columns c0 + 4 (k %
+  // 4) .. + 3, so result lane k receives column c0 + k of the four rows --
+  // the layout of accumulator registers 4q .. 4q + 3.
+  auto r_quad = [&](int i, int j, int q) {
+    const int g = lane >> 4, k = lane & 15;
+    const int row = wm * 128 + i * 32 + 8 * q + 4 * (g >> 1) + (k >> 2);
+    const int col = wn * 128 + j * 32 + 16 * (g & 1) + 4 * (k & 3);
+    return ds_read_tr16(reinterpret_cast<const char*>(r_tile) + row * (kBig * 2) + col * 2);
+  };
 
   // Epilogue.  Accumulator register r of lane l holds row
   // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of its 32 x 32 tile.
-  if (EPI == kEpiUH || EPI == kEpiGeluBwd) {
+  if constexpr (EPI == kEpiUH || EPI == kEpiGeluBwd) {
     // Also stored transposed: registers 4q..4q+3 are four consecutive rows
     // of one column, so each lane writes them as one 8-byte run of C2.
 #pragma unroll
@@ -641,6 +654,8 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
           const int mb = m0 + wm * 128 + i * 32 + 8 * q + 4 * (lane >> 5);
           const int n = n0 + wn * 128 + j * 32 + (lane & 31);
           uint32_t t[2];
+          bf16x4_t rq;
+          if constexpr (EPI == kEpiGeluBwd) rq = r_quad(i, j, q);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int m = mb + e;
@@ -650,7 +665,7 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
               c = acc[i][j][4 * q + e] * scale[m];
               ct = gelu_tanh(c);
             } else {
-              c = ct = acc[i][j][4 * q + e] * gelu_tanh_grad(r_at(m, n));
+              c = ct = acc[i][j][4 * q + e] * gelu_tanh_grad(static_cast<float>(rq[e]));
             }
             C[idx] = f32_to_bf16(c);
             const uint32_t b = f32_to_bf16(ct);
@@ -662,19 +677,58 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
           *reinterpret_cast<uint2*>(C2 + static_cast<size_t>(n) * M + mb) = uint2{t[0], t[1]};
         }
     return;
-  }
+  } else {
+  // Registers r and r + 1 (r even) are rows m and m + 1 of one column: both
+  // are converted by one packed bf16 conversion and stored as its two halves.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    bf16x4_t rq[4][4];  // [j][q]: R of registers 4q .. 4q + 3 of tile (i, j)
+    if constexpr (EPI == kEpiResidual) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) rq[j][q] = r_quad(i, j, q);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
       const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      const float sc = EPI == kEpiGelu || EPI == kEpiGeluSave ? scale[m] : 1.0f;
+      constexpr bool kScaled = EPI == kEpiGelu || EPI == kEpiGeluSave;
+      const float sc0 = kScaled ? scale[m] : 1.0f;
+      const float sc1 = kScaled ? scale[m + 1] : 1.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n = n0 + wn * 128 + j * 32 + (lane & 31);
-        epilogue<EPI>(acc[i][j][r], sc, kEpiReadsR<EPI> ? r_at(m, n) : 0.0f, m, n, M, N, C, C2, Cf);
+        const float a0 = acc[i][j][r], a1 = acc[i][j][r + 1];
+        const size_t idx = static_cast<size_t>(m) * N + n;
+        if constexpr (EPI == kEpiStoreF32) {
+          Cf[idx] = a0;
+          Cf[idx + N] = a1;
+        } else {
+          uint32_t p, p2 = 0;
+          if constexpr (EPI == kEpiGelu) {
+            p = pack_bf16x2(gelu_tanh(a0 * sc0), gelu_tanh(a1 * sc1));
+          } else if constexpr (EPI == kEpiGeluSave) {
+            // The same h as kEpiGelu, and the u the backward's kEpiUH recomputes.
+            const float u0 = a0 * sc0, u1 = a1 * sc1;
+            p = pack_bf16x2(gelu_tanh(u0), gelu_tanh(u1));
+            p2 = pack_bf16x2(u0, u1);
+          } else if constexpr (EPI == kEpiResidual) {
+            p = pack_bf16x2(a0 + static_cast<float>(rq[j][r >> 2][r & 3]),
+                            a1 + static_cast<float>(rq[j][r >> 2][(r & 3) + 1]));
+          } else {
+            static_assert(EPI == kEpiStore, "row-major epilogues only");
+            p = pack_bf16x2(a0, a1);
+          }
+          C[idx] = static_cast<uint16_t>(p);
+          C[idx + N] = static_cast<uint16_t>(p >> 16);
+          if constexpr (EPI == kEpiGeluSave) {
+            C2[idx] = static_cast<uint16_t>(p2);
+            C2[idx + N] = static_cast<uint16_t>(p2 >> 16);
+          }
+        }
       }
     }
+  }
   }
 }
 
