@@ -231,6 +231,57 @@ def run_ffn_reference(rows: int = 4096, d: int = 8192, f: int = 28672, reps: int
     print("ffn reference workload done", flush=True)
 
 
+def ffn_vs_library(rows: int = 4096, d: int = 8192, f: int = 28672, rounds: int = 2,
+                   calls: int = 20) -> list[dict[str, Any]]:
+    """Same-process timing of this library's C5 FFN forward against the vendor
+    path on the same operands: hipBLASLt (torch.matmul) on GEMM1's and
+    GEMM2's shapes, and the unfused torch FFN (rms_norm, matmul, gelu tanh,
+    matmul, residual add).  Each line: `calls` calls after 5 warmup calls,
+    bracketed by events on torch's current stream, `rounds` times in turn."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x = torch.randn(rows, d, device=dev, generator=g).bfloat16()
+    w1 = (torch.randn(f, d, device=dev, generator=g) / d ** 0.5).bfloat16()
+    w2 = (torch.randn(d, f, device=dev, generator=g) / f ** 0.5).bfloat16()
+    h = torch.randn(rows, f, device=dev, generator=g).bfloat16()
+    out = torch.empty_like(x)
+    cfg = hip_lib.make_cfg("auto")
+    gemm = 2.0 * rows * d * f
+
+    def torch_ffn():
+        a = torch.nn.functional.rms_norm(x, (d,), eps=hip_lib.FFN_EPS)
+        hh = torch.nn.functional.gelu(a @ w1.t(), approximate="tanh")
+        return x + hh @ w2.t()
+
+    cases = [("this library's fused FFN", lambda: hip_lib.ffn(x, w1, w2, out, hip_lib.FFN_EPS, cfg),
+              2 * gemm),
+             ("hipBLASLt, GEMM1 shape (x @ W1^T)", lambda: torch.matmul(x, w1.t()), gemm),
+             ("hipBLASLt, GEMM2 shape (h @ W2^T)", lambda: torch.matmul(h, w2.t()), gemm),
+             ("torch FFN over hipBLASLt", torch_ffn, 2 * gemm)]
+    rows_out = []
+    for rnd in range(rounds):
+        for name, fn, flop in cases:
+            for _ in range(5):
+                fn()
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(calls):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) / calls * 1e3
+            rows_out.append({"round": rnd + 1, "case": name, "us": us,
+                             "tflops": flop / us / 1e6})
+            print(f"round {rnd + 1}  {name:36s} {us:8.1f} us  {flop / us / 1e6:7.1f} TFLOP/s",
+                  flush=True)
+    return rows_out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="gfx950 calibration microbenchmarks")
     ap.add_argument("--hbm-bytes", type=int, default=1 << 30)
@@ -246,12 +297,18 @@ def main(argv=None) -> int:
     ap.add_argument("--ffn-reference", action="store_true",
                     help="run the C5 FFN forward twice, then hipBLASLt (torch.matmul) on GEMM1's "
                          "shape twice: the workload of the FFN-against-library counter runs")
+    ap.add_argument("--ffn-vs-library", action="store_true",
+                    help="time the C5 FFN forward against hipBLASLt's GEMMs of its shapes and "
+                         "the unfused torch FFN in one process")
     ap.add_argument("--reps", type=int, default=2, help="calls of each in --ffn-reference")
     ap.add_argument("--gemm2", action="store_true",
                     help="--ffn-reference also runs hipBLASLt on GEMM2's shape")
     args = ap.parse_args(argv)
     import torch  # noqa: F401  (loads the HIP runtime torch uses before the library)
 
+    if args.ffn_vs_library:
+        ffn_vs_library()
+        return 0
     if args.ffn_reference:
         run_ffn_reference(reps=args.reps, gemm2=args.gemm2)
         return 0
