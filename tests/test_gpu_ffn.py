@@ -7,7 +7,9 @@ and h to bf16 as the MFMA path feeds them).  Tolerance: bf16 output within
 rtol 1e-2 / atol 1e-2.  The small shapes also pin the
 MFMA operand/accumulator lane layout: a wrong row/column mapping scrambles
 every output.  At the full C5 shape the oracle checks a sample of rows
-(each row of out depends only on the same row of x)."""
+(each row of out depends only on the same row of x), and every element is
+checked against a float32 restatement on the GPU (torch_fp32_ffn), itself
+held to the oracle on sampled rows."""
 import numpy as np
 import pytest
 import torch
@@ -170,6 +172,44 @@ def test_ffn_full_config_sampled_rows(gpu):
     rows = np.linspace(0, x.shape[0] - 1, 48).astype(int)
     np.testing.assert_allclose(out[rows], oracle(x, w1, w2, rows), **BF16)
     assert np.isfinite(out).all()
+
+
+def torch_fp32_ffn(x, w1, w2, gpu):
+    """The 256-tile path's arithmetic in float32 on the GPU (W1 [d, f], W2 [f,
+    d]): the fp32 product x @ W1 scaled by rstd (the normalised input is never
+    rounded), h = bf16(GELU_tanh(u)), out = x + h @ W2, as a float32 tensor on
+    the device.  Full-precision float32 products (no reduced-precision modes)."""
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        X = x.to(gpu).float()
+        rstd = torch.rsqrt((X * X).mean(dim=1, keepdim=True) + EPS)
+        u = (X @ w1.to(gpu).float()) * rstd
+        h = torch.nn.functional.gelu(u, approximate="tanh").to(torch.bfloat16).float()
+        del u
+        return X + h @ w2.to(gpu).float()
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+
+
+@pytest.mark.parametrize("layout", ["linear", "in_out"])
+def test_ffn_full_config_every_element(gpu, layout):
+    """BASELINE C5, every element of out against torch_fp32_ffn, itself
+    checked against the float64 oracle on 8 sampled rows (to a tenth of the
+    tolerance): 33.5M outputs, all within rtol 1e-2 / atol 1e-2."""
+    x, w1, w2 = WORKLOADS["ffn" if layout == "linear" else "ffn_baseline_layout"].make_inputs()
+    print(f"ffn C5 every element, {layout} weights", flush=True)
+    out = run_ffn(x, w1, w2, gpu) if layout == "linear" else run_ffn_in_out(x, w1, w2, gpu)
+    expect = torch_fp32_ffn(x, w1, w2, gpu)
+    rows = np.array([0, 1, 1000, 2047, 2048, 3333, 4094, 4095])
+    np.testing.assert_allclose(expect[rows].cpu().numpy(),
+                               oracle(x, w1, w2, rows, round_a=False), rtol=1e-3, atol=1e-3)
+    got = torch.from_numpy(out).to(gpu)
+    excess = (got - expect).abs() - (1e-2 * expect.abs() + 1e-2)
+    worst = int(excess.argmax())
+    assert float(excess.max()) <= 0, (
+        f"max excess {float(excess.max()):.3e} at {np.unravel_index(worst, out.shape)}")
+    assert bool(torch.isfinite(got).all())
 
 
 def test_ffn_in_out_full_config_sampled_rows(gpu):
