@@ -68,7 +68,8 @@ SWEEP: Schema = (
     ("predicted_hbm_bytes", float), ("predicted_block_hbm_bytes", float),
     ("predicted_l2_requests", float), ("predicted_lds_bytes", float),
     ("measured_hbm_bytes", float), ("measured_block_hbm_bytes", float),
-    ("measured_l2_requests", float), ("counter_source", str),
+    ("measured_l2_requests", float), ("measured_lds_instructions", float),
+    ("counter_source", str),
 )
 
 TABLES: dict[str, Schema] = {

@@ -7,7 +7,7 @@ rocprofv3 -- one counter per run, as the hardware allows:
     python -m credit_amd.counters pass --plan P.json [sweep options]      # under rocprofv3 --pmc C
     python -m credit_amd.counters merge BUNDLE --plan P.json \\
         --fetch F.csv --write W.csv --copy-fetch CF.csv --copy-write CW.csv \\
-        --copy-bytes B [--l2-requests T.csv]
+        --copy-bytes B [--l2-requests T.csv] [--lds-instructions L.csv]
 
 ``pass`` issues, for every plan entry, a marker dispatch -- a bf16 transpose
 of a 64 x 64 (i + 2) tile, whose grid of i + 2 workgroups names entry i --
@@ -20,7 +20,10 @@ WRITE_SIZE by what they read for a copy kernel of known size
 (credit_amd.traffic.copy_scale), and writes the results into the bundle's
 cluster_sweep.csv beside cost_model.predict_traffic's columns:
 measured_hbm_bytes (split variant), measured_block_hbm_bytes (the point's
-best no-split variant) and measured_l2_requests (TCC_REQ_sum, split).  It
+best no-split variant), measured_l2_requests (TCC_REQ_sum, split) and
+measured_lds_instructions (SQ_INSTS_LDS, split: wave-level LDS instructions
+of the call, beside predicted_lds_bytes, which prices only the exchange
+copies; the kernels' block reductions and LDS rings are the rest).  It
 also writes counters.csv, one row per plan entry, and TRAFFIC.md, the
 measured / predicted ratios per workload.  The plan is a pure
 function of the sweep options, so it names the same rows as the timed sweep.
@@ -135,7 +138,8 @@ def entry_sums(counter_csv: str | Path) -> dict[int, dict[str, float]]:
 
 
 def merge(bundle_dir: Path, plan_path: Path, fetch: str, write: str, copy_fetch: str,
-          copy_write: str, copy_bytes: int, l2_requests: str | None = None) -> dict[str, Any]:
+          copy_write: str, copy_bytes: int, l2_requests: str | None = None,
+          lds_instructions: str | None = None) -> dict[str, Any]:
     from . import bundle as bundle_mod
 
     plan = json.loads(Path(plan_path).read_text())
@@ -143,6 +147,7 @@ def merge(bundle_dir: Path, plan_path: Path, fetch: str, write: str, copy_fetch:
     fs, ws = copy_scale(copy_fetch, copy_bytes), copy_scale(copy_write, copy_bytes)
     f, w = entry_sums(fetch), entry_sums(write)
     t = entry_sums(l2_requests) if l2_requests else {}
+    ld = entry_sums(lds_instructions) if lds_instructions else {}
     rows_out = []
     measured: dict[tuple[str, int, int, str, int], dict[str, float]] = {}
     for e in entries:
@@ -150,11 +155,13 @@ def merge(bundle_dir: Path, plan_path: Path, fetch: str, write: str, copy_fetch:
         hbm = (f.get(i, {}).get("FETCH_SIZE", math.nan) * fs +
                w.get(i, {}).get("WRITE_SIZE", math.nan) * ws)
         req = t.get(i, {}).get("TCC_REQ_sum", math.nan) if t else math.nan
+        lds = ld.get(i, {}).get("SQ_INSTS_LDS", math.nan) if ld else math.nan
         key = (e["workload"], e["rows"], e["cols"], e["variant"], e["split"])
-        measured[key] = {"hbm": hbm, "l2": req}
+        measured[key] = {"hbm": hbm, "l2": req, "lds": lds}
         rows_out.append({**{k: e[k] for k in ("index", "workload", "rows", "cols", "variant",
                                               "split")},
-                         "status": e.get("status", ""), "hbm_bytes": hbm, "l2_requests": req})
+                         "status": e.get("status", ""), "hbm_bytes": hbm, "l2_requests": req,
+                         "lds_instructions": lds})
     b = bundle_mod.Bundle.load(bundle_dir)
     block_of = {(r["workload"], r["rows"], r["cols"]): r["block_variant"] for r in b.summary}
     source = f"counter pass {Path(plan_path).name}"
@@ -166,7 +173,8 @@ def merge(bundle_dir: Path, plan_path: Path, fetch: str, write: str, copy_fetch:
             continue
         blk = measured.get((*pt, block_of.get(pt, "read"), 0), {"hbm": math.nan})
         r.update(measured_hbm_bytes=m["hbm"], measured_block_hbm_bytes=blk["hbm"],
-                 measured_l2_requests=m["l2"], counter_source=source)
+                 measured_l2_requests=m["l2"], measured_lds_instructions=m["lds"],
+                 counter_source=source)
         filled += 1
     b.save_tables()
     with (Path(bundle_dir) / "counters.csv").open("w", newline="") as fh:
@@ -192,6 +200,12 @@ def agreement(bundle_dir: Path) -> list[dict[str, Any]]:
                                 if r.get("measured_block_hbm_bytes") else math.nan),
             "l2_ratio": (r["measured_l2_requests"] / r["predicted_l2_requests"]
                          if r.get("measured_l2_requests") else math.nan),
+            # per row and member: the LDS instructions counted, the exchange
+            # bytes the model prices into LDS
+            "lds_insts_per_row_member": (r["measured_lds_instructions"] / (r["rows"] * r["split"])
+                                         if r.get("measured_lds_instructions") else math.nan),
+            "lds_bytes_per_row_member": (r["predicted_lds_bytes"] / (r["rows"] * r["split"])
+                                         if r.get("predicted_lds_bytes") is not None else math.nan),
         })
     return out
 
@@ -207,22 +221,28 @@ def traffic_report(bundle_dir: Path) -> str:
     for r in rows:
         by[r["workload"]].append(r)
 
-    def span(vals):
+    def span(vals, fmt=".3f"):
         v = [x for x in vals if math.isfinite(x)]
         if not v:
             return "-"
-        return f"{statistics.median(v):.3f} [{min(v):.3f}, {max(v):.3f}]"
+        return f"{statistics.median(v):{fmt}} [{min(v):{fmt}}, {max(v):{fmt}}]"
 
     lines = ["# Counters against the cost model's traffic", "",
              "measured / predicted per sweep row (median [min, max]); HBM = scaled FETCH_SIZE +"
-             " WRITE_SIZE of one call, L2 = TCC_REQ_sum.", "",
-             "| workload | rows | split HBM | no-split HBM | split L2 requests |",
-             "|---|---:|---|---|---|"]
+             " WRITE_SIZE of one call, L2 = TCC_REQ_sum. LDS: SQ_INSTS_LDS (wave instructions) per"
+             " row and member, beside the exchange bytes per row and member the model copies into"
+             " LDS (not a ratio: the counted instructions include the block reductions and LDS"
+             " rings the model does not price).", "",
+             "| workload | rows | split HBM | no-split HBM | split L2 requests |"
+             " split LDS instr. / row / member | predicted LDS B / row / member |",
+             "|---|---:|---|---|---|---|---|"]
     for name in sorted(by):
         rs = by[name]
         lines.append(f"| {name} | {len(rs)} | {span([r['hbm_ratio'] for r in rs])} | "
                      f"{span([r['block_hbm_ratio'] for r in rs])} | "
-                     f"{span([r['l2_ratio'] for r in rs])} |")
+                     f"{span([r['l2_ratio'] for r in rs])} | "
+                     f"{span([r['lds_insts_per_row_member'] for r in rs], '.0f')} | "
+                     f"{span([r['lds_bytes_per_row_member'] for r in rs], '.0f')} |")
     within = sum(1 for r in rows if abs(r["hbm_ratio"] - 1.0) < 0.05)
     within_b = sum(1 for r in rows
                    if math.isfinite(r["block_hbm_ratio"]) and abs(r["block_hbm_ratio"] - 1.0) < 0.05)
@@ -256,6 +276,7 @@ def main(argv=None) -> int:
     m.add_argument("--copy-write", required=True)
     m.add_argument("--copy-bytes", type=int, required=True)
     m.add_argument("--l2-requests")
+    m.add_argument("--lds-instructions", help="SQ_INSTS_LDS counter CSV of a pass")
     args = ap.parse_args(argv)
     if args.cmd == "pass":
         workloads = SWEEP_WORKLOADS if args.workloads == "all" else tuple(
@@ -267,7 +288,7 @@ def main(argv=None) -> int:
         print(f"counter pass: {len(done)} entries -> {args.plan}", flush=True)
         return 0
     res = merge(args.bundle, args.plan, args.fetch, args.write, args.copy_fetch, args.copy_write,
-                args.copy_bytes, args.l2_requests)
+                args.copy_bytes, args.l2_requests, args.lds_instructions)
     print(json.dumps(res))
     print(traffic_report(args.bundle))
     return 0
