@@ -61,9 +61,11 @@ def oracle(x, w1, w2, dout):
 
 # (128, 128, 128) .. (384, 512, 256): 128-tile GEMMs throughout;
 # (512, 512, 1024): the f-wide GEMMs on 256 tiles, da on 128 tiles;
-# (1024, 512, 2048): every GEMM on 256 tiles.
+# (1024, 512, 2048): every GEMM on 256 tiles; (128, 12288, 256) and
+# (128, 20480, 128): rows wider than C5's for the dx row kernel.
 @pytest.mark.parametrize("rows,d,f", [(128, 128, 128), (128, 256, 384), (256, 128, 512),
-                                      (384, 512, 256), (512, 512, 1024), (1024, 512, 2048)])
+                                      (384, 512, 256), (512, 512, 1024), (1024, 512, 2048),
+                                      (128, 12288, 256), (128, 20480, 128)])
 def test_ffn_backward_small_shapes(gpu, rows, d, f):
     print(f"ffn_backward rows={rows} d={d} f={f}", flush=True)
     x, w1, w2, dout = make(rows, d, f, seed=rows + d + f)
