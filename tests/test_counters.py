@@ -113,12 +113,21 @@ def test_merge_fills_the_sweep_beside_predictions(tmp_path):
                                             (MARK, 768, 0), (KERN, 4096, 60.0)])
     _csv(tmp_path / "t.csv", "TCC_REQ_sum", [(MARK, 512, 0), (KERN, 4096, 1800.0),
                                              (MARK, 768, 0), (KERN, 4096, 2100.0)])
+    # Two kernels in the split call: the LDS instruction count is their sum.
+    _csv(tmp_path / "l.csv", "SQ_INSTS_LDS", [(MARK, 512, 0), (KERN, 4096, 70.0),
+                                              (MARK, 768, 0), (KERN, 4096, 300.0),
+                                              (KERN, 4096, 20.0)])
     res = counters.merge(b, tmp_path / "plan.json", tmp_path / "f.csv", tmp_path / "w.csv",
-                         tmp_path / "cf.csv", tmp_path / "cw.csv", 1 << 20, tmp_path / "t.csv")
+                         tmp_path / "cf.csv", tmp_path / "cw.csv", 1 << 20, tmp_path / "t.csv",
+                         tmp_path / "l.csv")
     assert res["sweep_rows_filled"] == 1
     row = bundle.read_table(b / "cluster_sweep.csv", bundle.SWEEP)[0]
     assert row["measured_hbm_bytes"] == pytest.approx(110.0 * 2048 + 60.0 * 1024)
     assert row["measured_block_hbm_bytes"] == pytest.approx(100.0 * 2048 + 50.0 * 1024)
     assert row["measured_l2_requests"] == 2100.0
+    assert row["measured_lds_instructions"] == 320.0
     ratios = counters.agreement(b)
     assert len(ratios) == 1 and math.isfinite(ratios[0]["hbm_ratio"])
+    # per row (8) and member (2)
+    assert ratios[0]["lds_insts_per_row_member"] == pytest.approx(320.0 / 16)
+    assert "SQ_INSTS_LDS" in counters.traffic_report(b)
