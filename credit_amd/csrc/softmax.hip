@@ -192,21 +192,38 @@ __device__ __forceinline__ void merge_maxsum_lanes(bool has, float m, float s, f
 // member's slice (0 for a row beyond the group): out-of-range lanes read
 // zeros, masked to -inf / 0, and drop their stores; no branch surrounds a
 // load or store, so the waitcnt pass keeps rows i+1..i+3 in flight.
-template <int THREADS, int VPT>
+// Buffer J of four statically named row buffers (J a constant, so the
+// rotation stays in registers).
+template <int J, typename T>
+__device__ __forceinline__ T& pick4(T& a, T& b, T& c, T& d) {
+  if constexpr (J == 0) return a;
+  else if constexpr (J == 1) return b;
+  else if constexpr (J == 2) return c;
+  else return d;
+}
+
+template <int THREADS, int VPT, bool PARK = false>
 __global__ __launch_bounds__(THREADS + kWave)
 __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void softmax_fwd_group_kernel(
     const float* __restrict__ x, float* __restrict__ p, float* __restrict__ rowmax,
     float* __restrict__ lse, int rows, int cols, int chunk, int members, int rows_per_group,
     SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
-  __shared__ float wmax[4][NW];       // wave partials of row k at [(k - r0) & 3]
-  __shared__ double wsum[4][NW];
-  __shared__ float ring_m[4];         // group (M, S) of row k at [(k - r0) & 3]
-  __shared__ float ring_s[4];
-  __shared__ uint32_t arrivals[4];
+  // Rows between their publish and their finish: 2, or 4 with PARK (two of
+  // them parked in LDS).  The per-row LDS rings hold every row from the
+  // slowest wave's finish to the comm wave's newest total: RING entries.
+  constexpr int RING = PARK ? 8 : 4;
+  __shared__ float wmax[RING][NW];    // wave partials of row k at [(k - r0) % RING]
+  __shared__ double wsum[RING][NW];
+  __shared__ float ring_m[RING];      // group (M, S) of row k at [(k - r0) % RING]
+  __shared__ float ring_s[RING];
+  __shared__ uint32_t arrivals[RING];
   __shared__ uint32_t ready;          // rows r0 .. r0 + ready - 1 have (M, S)
+  // PARK: two published rows of e^(x - m_w), lane-private ([slot][q][lane]):
+  // each lane reads back only what it wrote, so no barrier guards a slot.
+  __shared__ f32x4 parked[PARK ? 2 * VPT * THREADS : 1];
   const int tid = threadIdx.x;
-  if (tid < 4) arrivals[tid] = 0;
+  if (tid < RING) arrivals[tid] = 0;
   if (tid == 0) ready = 0;
   const SplitGroup g = split_join(sa, members, 2);  // its barrier covers the stores above
   // Rows are dealt to the G groups round-robin (group g's i-th row is
@@ -237,8 +254,8 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
       merge_maxsum_lanes(lane < members, __builtin_bit_cast(float, bits),
                          __builtin_bit_cast(float, sbits), &M, &S);
       if (tid == THREADS) {
-        ring_m[(k - r0) & 3] = M;
-        ring_s[(k - r0) & 3] = S;
+        ring_m[(k - r0) & (RING - 1)] = M;
+        ring_s[(k - r0) & (RING - 1)] = S;
         __hip_atomic_store(&ready, static_cast<uint32_t>(k - r0 + 1), __ATOMIC_RELEASE,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
         if (g.member == 0) {
@@ -289,7 +306,7 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
       for (int q = 0; q < VPT; ++q) b.v[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     const double ws = wave_reduce_sum_f64(static_cast<double>(ls));
-    const int slot = (k - r0) & 3;
+    const int slot = (k - r0) & (RING - 1);
     uint32_t t = 0;
     if (lead) {
       wmax[slot][wid] = wm;
@@ -311,8 +328,9 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
       }
     }
   };
-  auto finish_row = [&](const Row& b, int r) {
-    const int slot = (r - r0) & 3;
+  // Waits for row r's (M, S); returns the wave's output scale for it.
+  auto row_scale = [&](int r) {
+    const int slot = (r - r0) & (RING - 1);
     const uint32_t need = static_cast<uint32_t>(r - r0 + 1);
     while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < need)
       __builtin_amdgcn_s_sleep(1);
@@ -320,13 +338,65 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
     const float S = ring_s[slot];
     // e^(m_w - M) / S; 0/0 (NaN) for a row of -inf, as torch.softmax.
     const float mw = wmax[slot][wid];
-    const float f = (mw == kNegInf ? 0.0f : exp_accurate(mw - M)) / S;
+    return (mw == kNegInf ? 0.0f : exp_accurate(mw - M)) / S;
+  };
+  auto out_rsrc = [&](int r) {
     const size_t off = static_cast<size_t>(row_of(r)) * cols + 4 * static_cast<size_t>(v0);
-    const buffer_rsrc_t out = make_rsrc(p + off, slice_bytes);
+    return make_rsrc(p + off, slice_bytes);
+  };
+  auto finish_row = [&](const Row& b, int r) {
+    const float f = row_scale(r);
+    const buffer_rsrc_t out = out_rsrc(r);
 #pragma unroll
     for (int q = 0; q < VPT; ++q)
       buffer_store_nt(out, lane_off + q * kStride, __builtin_bit_cast(u32x4, b.v[q] * f));
   };
+  if constexpr (PARK) {
+    // Row k lives in buffer k % 4 from its load to its park.  Step i: load
+    // row i+5, publish row i+4, finish row i from LDS slot i % 2, park row
+    // i+2 there: a row is published four steps before its total is needed.
+    auto park = [&](const Row& b, int slot) {
+#pragma unroll
+      for (int q = 0; q < VPT; ++q) parked[(slot * VPT + q) * THREADS + tid] = b.v[q];
+    };
+    auto finish_parked = [&](int r, int slot) {
+      const float f = row_scale(r);
+      const buffer_rsrc_t out = out_rsrc(r);
+#pragma unroll
+      for (int q = 0; q < VPT; ++q)
+        buffer_store_nt(out, lane_off + q * kStride,
+                        __builtin_bit_cast(u32x4, parked[(slot * VPT + q) * THREADS + tid] * f));
+    };
+    auto step = [&]<int S>(std::integral_constant<int, S>, int i) {
+      load_row(pick4<(S + 1) & 3>(b0, b1, b2, b3), i + 5);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + 4 < r1) publish_row(pick4<S>(b0, b1, b2, b3), i + 4);
+      finish_parked(i, S & 1);
+      park(pick4<(S + 2) & 3>(b0, b1, b2, b3), S & 1);
+    };
+    load_row(b0, r0);
+    load_row(b1, r0 + 1);
+    load_row(b2, r0 + 2);
+    load_row(b3, r0 + 3);
+    publish_row(b0, r0);
+    park(b0, 0);
+    load_row(b0, r0 + 4);
+    if (r0 + 1 < r1) publish_row(b1, r0 + 1);
+    park(b1, 1);
+    if (r0 + 2 < r1) publish_row(b2, r0 + 2);
+    if (r0 + 3 < r1) publish_row(b3, r0 + 3);
+    int i = r0;
+    for (; i + 3 < r1; i += 4) {
+      step(std::integral_constant<int, 0>{}, i);
+      step(std::integral_constant<int, 1>{}, i + 1);
+      step(std::integral_constant<int, 2>{}, i + 2);
+      step(std::integral_constant<int, 3>{}, i + 3);
+    }
+    if (i < r1) step(std::integral_constant<int, 0>{}, i);
+    if (i + 1 < r1) step(std::integral_constant<int, 1>{}, i + 1);
+    if (i + 2 < r1) step(std::integral_constant<int, 2>{}, i + 2);
+    return;
+  }
   auto step = [&](Row& cur, Row& r2, Row& fut, int i) {
     load_row(fut, i + 3);
     __builtin_amdgcn_sched_barrier(0);
@@ -836,7 +906,7 @@ const Pick<FwdGroupFn> kFwdGroup[] = {
     {softmax_fwd_group_kernel<448, 4>, 448, 1792},
     {softmax_fwd_group_kernel<512, 4>, 512, 2048},
     {softmax_fwd_group_kernel<960, 4>, 960, 3840},
-    {softmax_fwd_group_kernel<512, 8>, 512, 4096},
+    {softmax_fwd_group_kernel<512, 8, true>, 512, 4096},
 };
 constexpr int64_t kFwdGroupCapacity = 4096;
 // Slot rows per group: a member publishes row k two steps before it needs
