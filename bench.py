@@ -70,7 +70,7 @@ CALL_KERNELS = {
     "rmsnorm_fwd_bwd": ("rmsnorm.hip", ["rmsnorm_fused_group_kernel<512, 2, 2, 2>",
                                         "rmsnorm_dw_reduce_kernel"]),
     "softmax_fwd": ("softmax.hip", ["softmax_fwd_group_kernel<512, 8, true>"]),
-    "softmax_bwd": ("softmax.hip", ["softmax_bwd_group_kernel<512, 4>"]),
+    "softmax_bwd": ("softmax.hip", ["softmax_bwd_group_kernel<512, 4, true>"]),
     "softmax_logits_backward": ("softmax.hip", ["softmax_logits_bwd_slice_kernel<1024, 8>"]),
     "ffn": ("ffn.hip", ["ffn_rstd_kernel", "ffn_gemm256_kernel<0, false>",
                         "ffn_gemm256_kernel<1, false>"]),

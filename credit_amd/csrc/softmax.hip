@@ -432,19 +432,26 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
 // waits for row i's group total and writes dx = p * (dy - c): the exchange
 // round trip has two steps to complete and no workgroup barrier sits in the
 // loop.  Buffer resources cover the member's slice (0 for a row beyond the
-// group), so no load or store is under a branch.
-template <int THREADS, int VPT>
+// group), so no load or store is under a branch.  PARK moves two published
+// rows into LDS, so each row is published four steps before its total is
+// needed, with the same four register buffers (the forward's scheme).
+template <int THREADS, int VPT, bool PARK = false>
 __global__ __launch_bounds__(THREADS + kWave)
 __attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
     const float* __restrict__ p, const float* __restrict__ dy, float* __restrict__ dx, int rows,
     int cols, int chunk, int members, int rows_per_group, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
-  __shared__ double red[4][NW];  // wave partials of row k at [(k - r0) & 3]
-  __shared__ double ring[4];     // group totals of row k at [(k - r0) & 3]
-  __shared__ uint32_t arrivals[4];
+  // Rows between publish and finish: 2, or 4 with PARK (two parked in LDS);
+  // the per-row LDS rings hold RING entries.
+  constexpr int RING = PARK ? 8 : 4;
+  __shared__ double red[RING][NW];  // wave partials of row k at [(k - r0) % RING]
+  __shared__ double ring[RING];     // group totals of row k at [(k - r0) % RING]
+  __shared__ uint32_t arrivals[RING];
+  // PARK: p and dy of two published rows, lane-private ([slot][p/dy][q][lane]).
+  __shared__ f32x4 parked[PARK ? 2 * 2 * VPT * THREADS : 1];
   __shared__ uint32_t ready;     // rows r0 .. r0 + ready - 1 have totals
   const int tid = threadIdx.x;
-  if (tid < 4) arrivals[tid] = 0;
+  if (tid < RING) arrivals[tid] = 0;
   if (tid == 0) ready = 0;
   const SplitGroup g = split_join(sa, members, 1);  // its barrier covers the stores above
   // Rows are dealt to the G groups round-robin (group g's i-th row is
@@ -470,7 +477,7 @@ __attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
       const uint32_t bits = split_poll(g, k - r0, 1);
       const double dot = split_wave_sum(bits, members, 0);
       if (tid == THREADS) {
-        ring[(k - r0) & 3] = dot;
+        ring[(k - r0) & (RING - 1)] = dot;
         __hip_atomic_store(&ready, static_cast<uint32_t>(k - r0 + 1), __ATOMIC_RELEASE,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
       }
@@ -504,7 +511,7 @@ __attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
 #pragma unroll
     for (int q = 0; q < VPT; ++q) part += dot4(b.p[q], b.d[q]);
     const double v = wave_reduce_sum_f64(static_cast<double>(part));
-    const int slot = (k - r0) & 3;
+    const int slot = (k - r0) & (RING - 1);
     if (lead) {
       red[slot][wid] = v;
       const uint32_t t = __hip_atomic_fetch_add(&arrivals[slot], 1u, __ATOMIC_ACQ_REL,
@@ -522,7 +529,7 @@ __attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
     const uint32_t need = static_cast<uint32_t>(i - r0 + 1);
     while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < need)
       __builtin_amdgcn_s_sleep(1);
-    return ring[(i - r0) & 3];
+    return ring[(i - r0) & (RING - 1)];
   };
   auto finish_row = [&](const Row& b, int r, double dot) {
     const float c = static_cast<float>(dot);
@@ -531,6 +538,54 @@ __attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
 #pragma unroll
     for (int q = 0; q < VPT; ++q) slice_store(out, lane_off + q * kStride, grad4(b.p[q], b.d[q], c));
   };
+  if constexpr (PARK) {
+    // Row k lives in buffer k % 4 from its load to its park.  Step i: load
+    // row i+5, publish row i+4, finish row i from LDS slot i % 2, park row
+    // i+2 there: a row is published four steps before its total is needed.
+    auto park = [&](const Row& b, int slot) {
+#pragma unroll
+      for (int q = 0; q < VPT; ++q) {
+        parked[((slot * 2 + 0) * VPT + q) * THREADS + tid] = b.p[q];
+        parked[((slot * 2 + 1) * VPT + q) * THREADS + tid] = b.d[q];
+      }
+    };
+    auto step = [&]<int S>(std::integral_constant<int, S>, int i) {
+      load_row(pick4<(S + 1) & 3>(b0, b1, b2, b3), i + 5);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + 4 < r1) publish_row(pick4<S>(b0, b1, b2, b3), i + 4);
+      const float c = static_cast<float>(wait_total(i));
+      const size_t off = static_cast<size_t>(row_of(i)) * cols + 4 * static_cast<size_t>(v0);
+      const buffer_rsrc_t out = make_rsrc(dx + off, slice_bytes);
+#pragma unroll
+      for (int q = 0; q < VPT; ++q)
+        slice_store(out, lane_off + q * kStride,
+                    grad4(parked[(((S & 1) * 2 + 0) * VPT + q) * THREADS + tid],
+                          parked[(((S & 1) * 2 + 1) * VPT + q) * THREADS + tid], c));
+      park(pick4<(S + 2) & 3>(b0, b1, b2, b3), S & 1);
+    };
+    load_row(b0, r0);
+    load_row(b1, r0 + 1);
+    load_row(b2, r0 + 2);
+    load_row(b3, r0 + 3);
+    publish_row(b0, r0);
+    park(b0, 0);
+    load_row(b0, r0 + 4);
+    if (r0 + 1 < r1) publish_row(b1, r0 + 1);
+    park(b1, 1);
+    if (r0 + 2 < r1) publish_row(b2, r0 + 2);
+    if (r0 + 3 < r1) publish_row(b3, r0 + 3);
+    int i = r0;
+    for (; i + 3 < r1; i += 4) {
+      step(std::integral_constant<int, 0>{}, i);
+      step(std::integral_constant<int, 1>{}, i + 1);
+      step(std::integral_constant<int, 2>{}, i + 2);
+      step(std::integral_constant<int, 3>{}, i + 3);
+    }
+    if (i < r1) step(std::integral_constant<int, 0>{}, i);
+    if (i + 1 < r1) step(std::integral_constant<int, 1>{}, i + 1);
+    if (i + 2 < r1) step(std::integral_constant<int, 2>{}, i + 2);
+    return;
+  }
   // Step of row i: cur = row i, r2 = row i+2 (loaded), fut receives row i+3.
   auto step = [&](Row& cur, Row& r2, Row& fut, int i) {
     load_row(fut, i + 3);
@@ -883,7 +938,7 @@ const Pick<BwdGroupFn> kBwdGroup[] = {
     {softmax_bwd_group_kernel<64, 4>, 64, 256},
     {softmax_bwd_group_kernel<128, 4>, 128, 512},
     {softmax_bwd_group_kernel<256, 4>, 256, 1024},
-    {softmax_bwd_group_kernel<512, 4>, 512, 2048},
+    {softmax_bwd_group_kernel<512, 4, true>, 512, 2048},
 };
 constexpr int64_t kBwdGroupCapacity = 2048;
 
