@@ -41,10 +41,12 @@ Schema = tuple[tuple[str, type], ...]
 RAW: Schema = (
     ("workload", str), ("rows", int), ("cols", int), ("variant", str), ("split", int),
     ("correct", bool), ("ms", float), ("p20_ms", float), ("p80_ms", float), ("samples", int),
-    ("error", str),
+    ("error", str), ("threads", int), ("lds_bytes", int), ("per_cu", int), ("dispensers", int),
 )
 
-CONTROL: Schema = (("rows", int), ("split", int), ("barriers", int), ("overhead_ms", float))
+CONTROL: Schema = (("workload", str), ("cols", int), ("rows", int), ("split", int),
+                   ("barriers", int), ("threads", int), ("lds_bytes", int), ("per_cu", int),
+                   ("overhead_ms", float))
 
 SUMMARY: Schema = (
     ("workload", str), ("label", str), ("category", str), ("rows", int), ("cols", int),

@@ -101,6 +101,16 @@ int check_cfg(const credit_cfg* cfg) {
   return CREDIT_OK;
 }
 
+// XCDs (XCCs) of a device as the runtime reports them; gfx950 carries 32
+// CUs per XCD, the fallback when the attribute is unavailable.
+int xcd_count_of(int device, int cu_count) {
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, device) == hipSuccess && n > 0)
+    return n;
+  (void)hipGetLastError();
+  return cu_count >= 32 ? cu_count / 32 : 1;
+}
+
 int current_device_props(const DeviceProps** out) {
   int dev = 0;
   CREDIT_HIP(hipGetDevice(&dev));
@@ -116,9 +126,8 @@ int current_device_props(const DeviceProps** out) {
     p.clock_khz = prop.clockRate;
     p.cooperative = prop.cooperativeLaunch;
     p.l2_bytes = prop.l2CacheSize;
-    // gfx950 (MI355X) carries 32 CUs per XCD; the XCD count is what the
-    // blockIdx -> XCD round-robin mapping needs.
-    p.xcd_count = p.cu_count >= 32 ? p.cu_count / 32 : 1;
+    // The XCD count is what the blockIdx -> XCD round-robin mapping needs.
+    p.xcd_count = xcd_count_of(dev, p.cu_count);
     p.device = dev;
   }
   *out = &p;
@@ -143,45 +152,6 @@ int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base) {
 __global__ void fill_f32_kernel(float* __restrict__ p, float v, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
-}
-
-uint32_t next_split_epoch(uint32_t stages) {
-  // Tag 0 is the zero-filled state, so no reserved range may contain it.
-  static std::atomic<uint32_t> next{1};
-  if (stages == 0) stages = 1;
-  for (;;) {
-    uint32_t base = next.load(std::memory_order_relaxed);
-    const uint32_t end = base + stages;  // may wrap; [base, 2^32) ending at 0 is fine
-    const bool wraps = base == 0 || (end < base && end != 0);
-    const uint32_t start = wraps ? 1u : base;
-    if (next.compare_exchange_weak(base, start + stages, std::memory_order_relaxed)) {
-      if (wraps) {
-        // Tags restart at 1 after 2^32 - 1 stages: slots still holding tags
-        // from the previous cycle could match again, so the library's own
-        // workspaces return their slot areas to zero first.  (Caller
-        // workspaces are the caller's to re-zero; include/credit.h.)
-        if (hipDeviceSynchronize() == hipSuccess)
-          for (const WsBuffer& b : workspace_cache().live())
-            if (b.ptr != nullptr) (void)hipMemset(b.ptr + kSlotOffset, 0, kSlotAreaBytes);
-        (void)hipDeviceSynchronize();
-        // So do the allocation-free entry points' fixed arrays, on every
-        // device that has used one.
-        int cur = 0;
-        if (hipGetDevice(&cur) == hipSuccess) {
-          int count = 0;
-          if (hipGetDeviceCount(&count) != hipSuccess) count = 0;
-          for (int d = 0; d < count; ++d)
-            if (char* na = noalloc_scratch_base(d)) {
-              if (hipSetDevice(d) != hipSuccess) continue;
-              (void)hipMemset(na + kSlotOffset, 0, kSlotAreaBytes);
-              (void)hipDeviceSynchronize();
-            }
-          (void)hipSetDevice(cur);
-        }
-      }
-      return start;
-    }
-  }
 }
 
 std::atomic<uint32_t> g_spin_limit{kSpinLimit};
@@ -258,37 +228,63 @@ int acquire_split_workspace(const credit_cfg* cfg, int64_t groups, int members,
   return CREDIT_OK;
 }
 
+// Shape of the last co-resident split launch this thread planned
+// (credit_last_split_shape).
+struct SplitShape {
+  int threads = 0;
+  int lds_bytes = 0;
+  int per_cu = 0;
+  int dispensers = 0;
+  int64_t groups = 0;
+};
+thread_local SplitShape g_last_split;
+
 int coresident_groups(const void* kernel, int threads, size_t dynamic_lds, int members,
-                      int64_t* groups) {
+                      int64_t* groups, int* dispensers) {
   struct Entry {
     int device;
     const void* kernel;
     int threads;
     size_t lds;
     int per_cu;
+    size_t static_lds;
   };
   static std::mutex mu;
   static std::vector<Entry> cache;
   int dev = 0;
   CREDIT_HIP(hipGetDevice(&dev));
   int per_cu = -1;
+  size_t static_lds = 0;
   {
     std::lock_guard<std::mutex> lock(mu);
     for (const Entry& e : cache)
-      if (e.device == dev && e.kernel == kernel && e.threads == threads && e.lds == dynamic_lds)
+      if (e.device == dev && e.kernel == kernel && e.threads == threads && e.lds == dynamic_lds) {
         per_cu = e.per_cu;
+        static_lds = e.static_lds;
+      }
   }
   if (per_cu < 0) {
     CREDIT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads,
                                                             dynamic_lds));
+    hipFuncAttributes attr;
+    CREDIT_HIP(hipFuncGetAttributes(&attr, kernel));
+    static_lds = attr.sharedSizeBytes;
     std::lock_guard<std::mutex> lock(mu);
-    cache.push_back(Entry{dev, kernel, threads, dynamic_lds, per_cu});
+    cache.push_back(Entry{dev, kernel, threads, dynamic_lds, per_cu, static_lds});
   }
   const DeviceProps* props = nullptr;
   CREDIT_TRY(current_device_props(&props));
   const int64_t resident = static_cast<int64_t>(per_cu) * props->cu_count;
-  *groups = resident / (static_cast<int64_t>(kDispensers) * members) * kDispensers;
+  *groups = plan::coresident_group_count(resident, members);
+  const int d = plan::dispensers_for(resident, members);
+  if (dispensers != nullptr) *dispensers = d;
+  g_last_split = SplitShape{threads, static_cast<int>(static_lds + dynamic_lds), per_cu, d,
+                            *groups};
   return CREDIT_OK;
+}
+
+int split_dispensers(int per_cu, int cu_count, int members) {
+  return plan::dispensers_for(static_cast<int64_t>(per_cu) * cu_count, members);
 }
 
 int cu_count_or_default() {
@@ -347,7 +343,7 @@ int credit_query_device(int32_t device, credit_device_info* info) {
   snprintf(info->arch, sizeof(info->arch), "%s", prop.gcnArchName);
   info->device = device;
   info->cu_count = prop.multiProcessorCount;
-  info->xcd_count = prop.multiProcessorCount >= 32 ? prop.multiProcessorCount / 32 : 1;
+  info->xcd_count = xcd_count_of(device, prop.multiProcessorCount);
   info->wave_size = prop.warpSize;
   info->max_threads_per_block = prop.maxThreadsPerBlock;
   info->cooperative_launch = prop.cooperativeLaunch;
@@ -474,6 +470,21 @@ int credit_check_watchdog(const credit_cfg* cfg) {
   if (flag != 0 || device_flag || noalloc_flag)
     return set_error(CREDIT_ERR_WATCHDOG,
                      "a split-row barrier exceeded its spin limit");
+  return CREDIT_OK;
+}
+
+int credit_last_split_shape(int32_t* threads, int32_t* lds_bytes, int32_t* per_cu,
+                            int32_t* dispensers) {
+  CREDIT_TRY(check_ptr(threads, "threads"));
+  CREDIT_TRY(check_ptr(lds_bytes, "lds_bytes"));
+  CREDIT_TRY(check_ptr(per_cu, "per_cu"));
+  CREDIT_TRY(check_ptr(dispensers, "dispensers"));
+  if (g_last_split.threads == 0)
+    return set_error(CREDIT_ERR_UNSUPPORTED, "no co-resident split launch on this thread yet");
+  *threads = g_last_split.threads;
+  *lds_bytes = g_last_split.lds_bytes;
+  *per_cu = g_last_split.per_cu;
+  *dispensers = g_last_split.dispensers;
   return CREDIT_OK;
 }
 

@@ -8,6 +8,7 @@
 #include <stdint.h>
 
 #include "../../include/credit.h"
+#include "split_plan.hpp"
 
 namespace credit {
 
@@ -63,30 +64,40 @@ inline int cfg_variant(const credit_cfg* cfg) {
 inline int cfg_split(const credit_cfg* cfg) { return cfg ? cfg->split : 0; }
 
 // Workspace layout, identical for every operation:
-//   [0, 256)                 header: the watchdog word the split-row
-//                            barrier raises
+//   [0, 256)                 header, one 64-byte line per word: the watchdog
+//                            word the split-row barrier raises (byte 0), the
+//                            exchange-tag sequence of split launches (byte
+//                            64, split_plan.hpp) and the count of dispenser
+//                            subsets whose workgroups have all exited (byte
+//                            128)
 //   [256, 256 + 1 MiB)       counter area: 262144 uint32 slots.  The first
 //                            kDispensers lines are the ticket dispensers of
-//                            split launches; group arrival counters follow
-//                            from slot kGroupCounterBase, one 64-byte line
-//                            each.  Only the arrival protocols write here
-//                            and each returns its counters to zero, so the
-//                            area stays zero between calls whatever shapes
-//                            the calls have.
+//                            split launches (word 0: the next ticket, word 1:
+//                            the subset's exited workgroups); group arrival
+//                            counters follow from slot kGroupCounterBase,
+//                            one 64-byte line each.  Every protocol returns
+//                            its counters to zero, so the area stays zero
+//                            between calls whatever shapes the calls have.
 //   [kSlotOffset, +4 MiB)    exchange slots of the tagged-slot split
 //                            protocol.  Only split launches write here, and
 //                            every slot carries the tag of the launch stage
-//                            that wrote it, so a later launch (new tags)
-//                            never takes an old value for its own.
+//                            that wrote it; tags come from the sequence word,
+//                            which every split launch advances on the device,
+//                            so a later launch (or a graph replay) never
+//                            takes an old value for its own.
 //   [kScratchOffset, ...)    op-specific scratch (dweight partials, FFN h,
 //                            row-sum partials): written before it is read
 //                            within one call, so its contents between calls
 //                            do not matter.
 // The first kScratchOffset bytes must read zero before the workspace's
-// first use; calls keep them that way (counters return to zero, slot tags
-// only grow).  Uses the caller's buffer when cfg->workspace is set, else the
-// library's buffer for (device, stream) (workspace_cache.hpp).
+// first use; calls keep them that way (counters return to zero, the
+// sequence and slot tags only grow, and the launch that takes the sequence
+// past its limit returns the slot area to zero itself).  Uses the caller's
+// buffer when cfg->workspace is set, else the library's buffer for (device,
+// stream) (workspace_cache.hpp).
 constexpr size_t kWorkspaceHeader = 256;
+constexpr int kHeaderSeqWord = 16;   // uint32 index of the sequence word
+constexpr int kHeaderExitWord = 32;  // uint32 index of the exited-subset count
 constexpr int kCounterSlots = 262144;
 constexpr size_t kSlotOffset = kWorkspaceHeader + size_t{4} * kCounterSlots;
 // Tagged slots of one split launch: at most (resident workgroups) x ring x
@@ -94,7 +105,7 @@ constexpr size_t kSlotOffset = kWorkspaceHeader + size_t{4} * kCounterSlots;
 // kernel, ring 16, two values), 4 MiB leaves room for larger devices.
 constexpr size_t kSlotAreaBytes = size_t{4} << 20;
 constexpr size_t kScratchOffset = kSlotOffset + kSlotAreaBytes;
-constexpr int kDispensers = 8;           // ticket dispensers, one per blockIdx % 8
+constexpr int kDispensers = plan::kMaxDispensers;  // ticket dispensers at most (blockIdx % 8)
 constexpr int kDispenserStride = 16;     // one 64-byte line each
 constexpr int kGroupCounterBase = kDispensers * kDispenserStride;  // first group counter
 constexpr int kGroupCounterStride = 16;  // one 64-byte line per group counter
@@ -113,9 +124,6 @@ constexpr int kMaxExchangeValues = 64;
 inline size_t split_slot_bytes(int64_t groups, int members, int k_values, int ring) {
   return static_cast<size_t>(groups) * ring * k_values * members * sizeof(uint64_t);
 }
-// Reserve `stages` consecutive exchange tags for one split launch and
-// return the first (a process-wide counter; the range never contains 0).
-uint32_t next_split_epoch(uint32_t stages);
 int acquire_workspace(const credit_cfg* cfg, size_t bytes, char** base);
 
 // Workspace of a ticketed split launch: the counter area, the partial slots
@@ -165,12 +173,16 @@ char* noalloc_scratch_base(int device);
 // finished group freed while resident workgroups spin (measured on MI355X:
 // pending members started seconds late when launches were queued back to
 // back).  So a split launch is one resident wave: G groups of P members,
-// G a multiple of kDispensers (one dispenser subset per XCD), G*P no more
-// than the workgroups of the kernel resident at once on the device, and
-// each group loops over its rows.  *groups = G (0: not even kDispensers
-// groups fit).
+// G a multiple of kDispensers, G*P no more than the workgroups of the kernel
+// resident at once on the device, and each group loops over its rows.
+// *groups = G (0: not even kDispensers groups fit).  *dispensers: the ticket
+// subsets of the launch (plan::dispensers_for), chosen so that every subset's
+// slots hold at least two groups: no group spans every slot of its subset.
 int coresident_groups(const void* kernel, int threads, size_t dynamic_lds, int members,
-                      int64_t* groups);
+                      int64_t* groups, int* dispensers = nullptr);
+// Dispenser subsets of a launch of `groups` x `members` of a kernel with
+// `per_cu` workgroups resident per CU (plan::dispensers_for).
+int split_dispensers(int per_cu, int cu_count, int members);
 // Upper bound of G for workspace sizing without a device query.
 inline int64_t coresident_groups_bound(int members, int cu_count) {
   const int64_t resident = static_cast<int64_t>(cu_count) * 32;  // >= blocks per CU

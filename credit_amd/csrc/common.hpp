@@ -303,38 +303,38 @@ __device__ __forceinline__ uint32_t counter_read(const uint32_t* counter) {
 // group and exchange partial results to combine them.
 //
 // Membership comes from a ticket, not from blockIdx.  The grid is split into
-// kDispensers subsets by blockIdx % kDispensers, each with its own
-// device-scope ticket dispenser; thread 0 of every workgroup draws the next
-// ticket of its subset as the workgroup starts, and ticket t of subset d
-// makes it member t % P of group d * (subset size / P) + t / P.  The grid
-// is a multiple of kDispensers * P, so every subset holds whole groups.
-// Within a subset a group's members hold consecutive tickets, so every group
-// whose P tickets are drawn has all P members running, and at most one group
-// per subset (the newest) is incomplete; its missing members are later
-// workgroups of the same subset, which the dispatcher can start because
-// complete groups never wait on anything and free their slots.  A plain
-// launch is thus deadlock-free whenever the device holds kDispensers * P
-// workgroups at once: no cooperative launch (which costs ~30 us on gfx950)
-// and no co-residency of the whole grid is needed.  One dispenser per subset
-// keeps the same-address atomics off a single serialisation point, and with
-// workgroups dealt to the 8 XCDs round-robin a subset -- so a group -- sits
-// on one XCD.  The workgroup that draws a subset's last ticket returns that
-// dispenser to zero.
+// D subsets by blockIdx % D (D = SplitArgs::dispensers: 8, one subset per
+// XCD, or fewer when an XCD's slots hold fewer than two groups), each with
+// its own device-scope ticket dispenser; thread 0 of every workgroup draws
+// the next ticket of its subset as the workgroup starts, and ticket t of
+// subset d makes it member t % P of group d * (subset size / P) + t / P
+// (plan::seat_of).  The grid is a multiple of D * P, so every subset holds
+// whole groups.  Within a subset a group's members hold consecutive tickets,
+// so every group whose P tickets are drawn has all P members running, and at
+// most one group per subset (the newest) is incomplete.  Split launches are
+// sized to what the device holds at once (coresident_groups), and every
+// subset's slots hold at least two groups, so no group needs every slot of
+// its subset: a slot withheld from the launch delays a group until another
+// group of the subset exits rather than stranding it.  One dispenser per
+// subset keeps the same-address atomics off a single serialisation point.
+// The workgroup that draws a subset's last ticket returns that dispenser to
+// zero.  tests/cpp/split_protocol_model.cpp runs these rules on host threads.
 //
 // Exchange protocol: tagged slots, no counters.  Every (group, stage, value
 // k, member) has its own 64-bit slot: the partial's fp32 bits in the low
 // word and a tag in the high word, written by ONE device-scope atomic store.
-// The tag of stage s is epoch + s, where the host reserves a fresh range of
-// tags [epoch, epoch + stages) for every split launch (never containing 0,
-// the zero-filled state), so a publisher never waits for anything (no
-// fence, no vmcnt drain of its own loads and stores), and a reader that sees
-// the tag in a slot sees that launch's value of that stage.  Stages use
-// slot rows modulo `ring`: a kernel whose members run many stages reuses a
-// slot row only once every member has polled it (the kernels guarantee
-// that by their step structure).  One wave of each member polls the group's
-// P*K slots of the stage (contiguous: one request per poll) until every tag
-// matches, puts the values in LDS, and after a barrier every thread
-// combines them in member order: all members, and every run, get
+// The tag of stage s is seq + 1 + s, where seq is the workspace header's
+// sequence word as the launch starts; the launch's last workgroup to exit
+// advances it by the launch's stage count (split_leave), so every launch --
+// a replayed graph too -- owns tags no slot holds yet, and a publisher never
+// waits for anything (no fence, no vmcnt drain of its own loads and stores):
+// a reader that sees the tag in a slot sees that launch's value of that
+// stage.  Stages use slot rows modulo `ring`: a kernel whose members run many
+// stages reuses a slot row only once every member has polled it (the kernels
+// guarantee that by their step structure).  One wave of each member polls
+// the group's P*K slots of the stage (contiguous: one request per poll)
+// until every tag matches, puts the values in LDS, and after a barrier every
+// thread combines them in member order: all members, and every run, get
 // bit-identical results.  Partials travel as fp32 (the block reductions
 // before them are fp64); the combination is fp64.  The poll is bounded: on
 // expiry it raises *watchdog (and the device's host-mapped watchdog word)
@@ -344,23 +344,26 @@ constexpr uint32_t kSpinLimit = 1u << 21;  // ~1 s of s_sleep polling
 constexpr int kMaxExchange = kMaxExchangeValues;  // members * values per stage
 static_assert(kMaxExchange <= kWave, "one wave polls a stage's slots");
 
-// Split-launch arguments, passed by value to every split kernel.
+// Split-launch arguments, passed by value to every split kernel.  grid == 0
+// marks a launch without groups (members == 1): no join, no leave.
 struct SplitArgs {
   uint32_t* counters;  // workspace counter area (dispensers)
   uint64_t* slots;     // workspace slots, [group][stage % ring][k][member]
-  uint32_t* watchdog;
-  uint32_t grid;       // gridDim.x, a multiple of kDispensers * members
-  uint32_t epoch;      // tag of stage 0; stage s carries epoch + s
+  uint32_t* header;    // workspace header: watchdog, sequence, exit count
+  uint32_t grid;       // gridDim.x, a multiple of dispensers * members
+  uint32_t stages;     // exchange tags the launch uses (<= plan::kMaxLaunchStages)
   int ring;            // slot rows per group (stages modulo ring)
-  uint32_t spin_limit = kSpinLimit;  // polls before a wait gives up
-  uint32_t* host_flag = nullptr;     // host-mapped word raised with the watchdog
+  uint32_t dispensers = kDispensers;  // ticket subsets (blockIdx % dispensers)
+  uint32_t spin_limit = kSpinLimit;   // polls before a wait gives up
+  uint32_t* host_flag = nullptr;      // host-mapped word raised with the watchdog
 };
 
 // The product launches' arguments: the process-wide spin limit and the
 // device's host-mapped watchdog word (credit_set_spin_limit, api.hip).
-inline SplitArgs make_split_args(const SplitWorkspace& ws, uint32_t grid, uint32_t epoch,
-                                 int ring) {
-  SplitArgs a{ws.counters, ws.slots, ws.watchdog, grid, epoch, ring};
+inline SplitArgs make_split_args(const SplitWorkspace& ws, uint32_t grid, uint32_t stages,
+                                 int ring, int dispensers) {
+  SplitArgs a{ws.counters, ws.slots, ws.watchdog, grid, stages, ring};
+  a.dispensers = static_cast<uint32_t>(dispensers);
   a.spin_limit = split_spin_limit();
   a.host_flag = ws.host_flag;
   return a;
@@ -380,42 +383,120 @@ struct SplitGroup {
   uint32_t* host_flag;
 };
 
-// Draw a ticket and derive (group, member).  Every thread calls it; it
-// contains one __syncthreads.
+// What split_leave needs, stashed in LDS by split_join so that the launch
+// arguments need not stay live in registers across the kernel.
+struct SplitExit {
+  uint32_t* subset_out;  // the subset's exited-workgroup count
+  uint32_t* header;
+  uint64_t* slots;
+  uint32_t per_subset;
+  uint32_t dispensers;
+  uint32_t stages;
+  uint32_t seq;          // the sequence word as the launch started
+  uint32_t waves_out;    // waves of this workgroup that have left
+};
+__device__ __forceinline__ SplitExit* split_exit_lds() {
+  __shared__ SplitExit exit_info;
+  return &exit_info;
+}
+
+// Draw a ticket, read the launch's tag sequence and derive (group, member).
+// Every thread calls it; it contains one __syncthreads.
 __device__ __forceinline__ SplitGroup split_join(const SplitArgs& a, int members, int k_values) {
-  __shared__ uint32_t ticket_s;
-  const uint32_t subset = blockIdx.x % kDispensers;
-  const uint32_t per_subset = a.grid / kDispensers;
+  __shared__ uint32_t join_s[2];  // ticket, sequence
+  const uint32_t subset = blockIdx.x % a.dispensers;
+  const uint32_t per_subset = a.grid / a.dispensers;
   if (threadIdx.x == 0) {
     uint32_t* dispenser = a.counters + subset * kDispenserStride;
     const uint32_t t = __hip_atomic_fetch_add(dispenser, 1u, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
     if (t == per_subset - 1) counter_reset(dispenser);
-    ticket_s = t;
+    const uint32_t seq = __hip_atomic_load(a.header + kHeaderSeqWord, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    join_s[0] = t;
+    join_s[1] = seq;
+    *split_exit_lds() = SplitExit{a.counters + subset * kDispenserStride + 1, a.header, a.slots,
+                                  per_subset, a.dispensers, a.stages, seq, 0u};
   }
   __syncthreads();
   // readfirstlane: the ticket is workgroup-uniform, and saying so keeps the
   // group/member arithmetic (and everything addressed by it) scalar.
-  const uint32_t t = __builtin_amdgcn_readfirstlane(ticket_s);
-  const uint32_t p = static_cast<uint32_t>(members);
+  const uint32_t t = __builtin_amdgcn_readfirstlane(join_s[0]);
+  const plan::Seat seat = plan::seat_of(blockIdx.x, t, a.grid, a.dispensers,
+                                        static_cast<uint32_t>(members));
   SplitGroup g;
-  g.group = static_cast<int>(subset * (per_subset / p) + t / p);
-  g.member = static_cast<int>(t % p);
+  g.group = seat.group;
+  g.member = seat.member;
   g.members = members;
   g.k_values = k_values;
   g.stage = 0;
   g.ring = a.ring;
-  g.epoch = a.epoch;
+  g.epoch = plan::launch_epoch(__builtin_amdgcn_readfirstlane(join_s[1]));
   g.slots = a.slots + static_cast<size_t>(g.group) * a.ring * k_values * members;
-  g.watchdog = a.watchdog;
+  g.watchdog = a.header;
   g.spin_limit = a.spin_limit;
   g.host_flag = a.host_flag;
   return g;
 }
 
+// Every thread of a workgroup that joined (split_join), once, at the end of
+// the kernel, with each wave's threads converged.  Each wave counts itself
+// out in LDS; the last wave of the workgroup counts the workgroup out of its
+// dispenser subset, the last workgroup of a subset counts the subset out of
+// the launch, and the last subset's wave stores the advanced tag sequence
+// (every workgroup read the old value in split_join, before it counted
+// out).  When the advance takes the sequence past plan::kSeqLimit, every
+// wave first waits for its own stores (slot stores included) and the last
+// one returns the whole slot area to zero before the sequence restarts: every
+// other workgroup has exited by then, and the next launch starts after this
+// one ends.  The counters return to zero.  Only the launch's last workgroup
+// waits on anything here: two device-scope atomics.
+__device__ __forceinline__ void split_leave(const SplitArgs& a) {
+  if (a.grid == 0) return;
+  SplitExit* ex = split_exit_lds();
+  bool clear = false;
+  const uint32_t next = plan::advance_seq(ex->seq, ex->stages, &clear);
+  if (clear) publish_wait();  // this wave's slot stores land before the area is cleared
+  const uint64_t exec = __builtin_amdgcn_read_exec();
+  const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(exec >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo(
+                                                      static_cast<uint32_t>(exec), 0u));
+  const uint32_t nwaves = (blockDim.x + kWave - 1) / kWave;
+  uint32_t last = 0;
+  if (rank == 0)
+    last = __hip_atomic_fetch_add(&ex->waves_out, 1u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_WORKGROUP) == nwaves - 1;
+  if (__builtin_amdgcn_readfirstlane(last) == 0) return;
+  uint32_t* header = ex->header;
+  uint32_t done = 0;
+  if (rank == 0) {
+    uint32_t* out = ex->subset_out;
+    if (__hip_atomic_fetch_add(out, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        ex->per_subset - 1) {
+      counter_reset(out);
+      uint32_t* launch_out = header + kHeaderExitWord;
+      if (__hip_atomic_fetch_add(launch_out, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+          ex->dispensers - 1) {
+        counter_reset(launch_out);
+        done = 1;
+      }
+    }
+  }
+  if (__builtin_amdgcn_readfirstlane(done) == 0) return;
+  if (clear) {
+    const uint32_t lanes = static_cast<uint32_t>(__builtin_popcountll(exec));
+    u32x4* area = reinterpret_cast<u32x4*>(ex->slots);
+    for (size_t i = rank; i < kSlotAreaBytes / sizeof(u32x4); i += lanes)
+      area[i] = u32x4{0, 0, 0, 0};
+    publish_wait();
+  }
+  if (rank == 0)
+    __hip_atomic_store(header + kHeaderSeqWord, next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // One thread: publish this member's k-th partial of exchange stage `stage`.
 __device__ __forceinline__ void split_publish_at(const SplitGroup& g, int stage, int k, double v) {
-  const uint64_t word = (static_cast<uint64_t>(g.epoch + static_cast<uint32_t>(stage)) << 32) |
+  const uint64_t word = (static_cast<uint64_t>(plan::stage_tag(g.epoch, stage)) << 32) |
                         __builtin_bit_cast(uint32_t, static_cast<float>(v));
   const int row = stage % g.ring;
   uint64_t* slot = g.slots + (static_cast<size_t>(row) * g.k_values + k) * g.members + g.member;
@@ -435,7 +516,7 @@ __device__ __forceinline__ uint32_t split_poll(const SplitGroup& g, int stage, i
   const int lane = threadIdx.x & (kWave - 1);
   const int n = g.members * values;
   const uint64_t* base = g.slots + static_cast<size_t>(stage % g.ring) * g.k_values * g.members;
-  const uint32_t tag = g.epoch + static_cast<uint32_t>(stage);
+  const uint32_t tag = plan::stage_tag(g.epoch, stage);
   uint64_t word = 0;
   uint32_t spins = 0;
   for (;;) {

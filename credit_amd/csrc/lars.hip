@@ -51,7 +51,7 @@ __device__ __forceinline__ float lars_step(double ww, double uu) {
 }
 
 template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void lars_slice_kernel(
+__device__ __forceinline__ void lars_slice_kernel_body(
     const float* __restrict__ w, const float* __restrict__ grad, const float* __restrict__ mom,
     float* __restrict__ w_out, float* __restrict__ u_out, int cols, int chunk, int members,
     int rows, SplitArgs sa) {
@@ -101,6 +101,15 @@ __global__ __launch_bounds__(THREADS) void lars_slice_kernel(
       slice_store(uo, lane_off + k * kStride, uv[k]);
     }
   }
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void lars_slice_kernel(
+    const float* __restrict__ w, const float* __restrict__ grad, const float* __restrict__ mom,
+    float* __restrict__ w_out, float* __restrict__ u_out, int cols, int chunk, int members,
+    int rows, SplitArgs sa) {
+  lars_slice_kernel_body<THREADS, VPT>(w, grad, mom, w_out, u_out, cols, chunk, members, rows, sa);
+  split_leave(sa);
 }
 
 // Two passes over the row; VEC: f32x4 accesses.

@@ -244,7 +244,7 @@ __global__ __launch_bounds__(THREADS) void layernorm_fwd_pipe_kernel(
 // deviations about the mean.  Partials travel as fp32 (the block sums before
 // them are fp64).  One HBM read of x, one write of y.
 template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void layernorm_fwd_slice_kernel(
+__device__ __forceinline__ void layernorm_fwd_slice_kernel_body(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
     const uint16_t* __restrict__ beta, uint16_t* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out, int cols, int chunk,
@@ -328,6 +328,16 @@ __global__ __launch_bounds__(THREADS) void layernorm_fwd_slice_kernel(
       rstd_out[row] = rs;
     }
   }
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void layernorm_fwd_slice_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
+    const uint16_t* __restrict__ beta, uint16_t* __restrict__ y,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int cols, int chunk,
+    int members, int rows, float eps, SplitArgs sa) {
+  layernorm_fwd_slice_kernel_body<THREADS, VPT>(x, gamma, beta, y, mean_out, rstd_out, cols, chunk, members, rows, eps, sa);
+  split_leave(sa);
 }
 
 // ------------------------------------------------------------------ READ --
@@ -574,20 +584,24 @@ extern "C" int credit_layernorm_fwd_bf16(const uint16_t* x, const uint16_t* gamm
   if (plan.variant == CREDIT_VARIANT_SPLIT) {
     const SlicePick* sp = slice_for(plan.chunk);
     int64_t groups = 0;
+    int dispensers = 0;
     CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(sp->fn), sp->threads, 0,
-                                 plan.members, &groups));
+                                 plan.members, &groups, &dispensers));
     if (groups == 0)
       return set_error(CREDIT_ERR_UNSUPPORTED,
                        "layernorm_fwd: %d groups of %d members do not fit the device",
                        kDispensers, plan.members);
     if (groups > padded_groups(rows)) groups = padded_groups(rows);
     const int64_t per_group = (rows + groups - 1) / groups;
+    if (2 * per_group > int64_t{credit::plan::kMaxLaunchStages})
+      return set_error(CREDIT_ERR_BAD_SHAPE, "layernorm_fwd: %lld rows per group",
+                       static_cast<long long>(per_group));
     SplitWorkspace ws;
     CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 2, kSplitRing, 0, &ws));
     const uint32_t total = static_cast<uint32_t>(groups * plan.members);
     // Two stages per row at most (the second only for offset rows).
-    const SplitArgs sa = make_split_args(
-        ws, total, next_split_epoch(static_cast<uint32_t>(2 * per_group)), kSplitRing);
+    const SplitArgs sa = make_split_args(ws, total, static_cast<uint32_t>(2 * per_group),
+                                         kSplitRing, dispensers);
     hipLaunchKernelGGL(sp->fn, dim3(total), dim3(sp->threads), 0, stream, x, gamma, beta, y,
                        mean, rstd, c, static_cast<int>(plan.chunk), plan.members,
                        static_cast<int>(rows), eps, sa);

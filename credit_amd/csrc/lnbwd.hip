@@ -74,7 +74,7 @@ __device__ __forceinline__ RowStats stats_from(double s1, double s2, float x0, i
 }
 
 template <class T, int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
+__device__ __forceinline__ void layernorm_bwd_slice_kernel_body(
     const T* __restrict__ x, const T* __restrict__ dy, const T* __restrict__ gamma,
     T* __restrict__ dx, int cols, int chunk, int members, int rows, float eps, SplitArgs sa) {
   using V = Vec<T>;
@@ -188,6 +188,14 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
       buffer_store_nt(ors, lane_off + k * kStride, __builtin_bit_cast(u32x4, V::pack(o)));
     }
   }
+}
+
+template <class T, int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
+    const T* __restrict__ x, const T* __restrict__ dy, const T* __restrict__ gamma,
+    T* __restrict__ dx, int cols, int chunk, int members, int rows, float eps, SplitArgs sa) {
+  layernorm_bwd_slice_kernel_body<T, THREADS, VPT>(x, dy, gamma, dx, cols, chunk, members, rows, eps, sa);
+  split_leave(sa);
 }
 
 // Three streaming passes over the row (any width and alignment).
@@ -352,22 +360,25 @@ int layernorm_bwd(const T* x, const T* dy, const T* gamma, T* dx, int64_t rows, 
     return check_launch("layernorm_bwd_slice_kernel");
   }
   int64_t groups = 0;
+  int dispensers = 0;
   CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(pk->fn), pk->threads, 0,
-                               plan.members, &groups));
+                               plan.members, &groups, &dispensers));
   if (groups == 0)
     return set_error(CREDIT_ERR_UNSUPPORTED,
                      "layernorm_bwd: %d groups of %d members do not fit the device", kDispensers,
                      plan.members);
   if (groups > padded_groups(rows)) groups = padded_groups(rows);
   const int64_t per_group = (rows + groups - 1) / groups;
+  if (2 * per_group > int64_t{credit::plan::kMaxLaunchStages})
+    return set_error(CREDIT_ERR_BAD_SHAPE, "layernorm_bwd: %lld rows per group",
+                     static_cast<long long>(per_group));
   SplitWorkspace ws;
   CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 2, kSplitRing, 0, &ws));
   const uint32_t total = static_cast<uint32_t>(groups * plan.members);
   hipLaunchKernelGGL(pk->fn, dim3(total), dim3(pk->threads), 0, stream, x, dy, gamma, dx, c,
                      static_cast<int>(plan.chunk), plan.members, static_cast<int>(rows), eps,
-                     make_split_args(ws, total,
-                                     next_split_epoch(static_cast<uint32_t>(per_group * 2)),
-                                     kSplitRing));
+                     make_split_args(ws, total, static_cast<uint32_t>(per_group * 2), kSplitRing,
+                                     dispensers));
   return check_launch("layernorm_bwd_slice_kernel(split)");
 }
 

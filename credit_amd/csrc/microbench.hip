@@ -207,9 +207,15 @@ __global__ void mb_pingpong_kernel(uint32_t* flag, int peer, int rounds, uint64_
 // like the split kernels' launches: each group takes rows group, group + G,
 // ... of `rows` and meets `barriers` times per row (publish, poll, read the
 // partials): the un-overlapped cost of the exchange the split kernels use.
-__global__ __launch_bounds__(256) void mb_barrier_kernel(SplitArgs sa, int members,
-                                                         int barriers, int rows,
-                                                         double* sink) {
+// The workgroup has the block size and the dynamic LDS of the split launch
+// it prices (src/cluster_control.cu:76-88 sizes its cluster kernel's shared
+// memory the same way), so it holds the same workgroups per CU; thread 0
+// touches the LDS, as there.
+__global__ __launch_bounds__(1024) void mb_barrier_kernel(SplitArgs sa, int members,
+                                                          int barriers, int rows,
+                                                          double* sink, int lds_bytes) {
+  extern __shared__ unsigned char mb_lds[];
+  if (threadIdx.x == 0 && lds_bytes > 0) mb_lds[0] = 1;
   SplitGroup g = split_join(sa, members, 1);
   const int step = static_cast<int>(sa.grid) / members;
   double acc = 0.0;
@@ -220,7 +226,9 @@ __global__ __launch_bounds__(256) void mb_barrier_kernel(SplitArgs sa, int membe
       acc += split_sum(g, 0);
     }
   }
+  if (lds_bytes > 0 && threadIdx.x == 0) acc += mb_lds[0];
   if (acc == -1.0 && threadIdx.x == 0) sink[0] = acc;  // keeps the reads alive
+  split_leave(sa);
 }
 
 __global__ __launch_bounds__(256) void mb_plain_kernel(int* sink) {
@@ -496,6 +504,28 @@ int bench_stream(int which, int64_t bytes, int iters, double* results, int n) {
   return CREDIT_OK;
 }
 
+// XCC of every workgroup of a grid (hardware register XCC_ID, read with
+// s_getreg): the dispatch order the split launches' dispenser subsets rely
+// on (workgroup b on XCC b % 8).
+__global__ __launch_bounds__(64) void mb_xcc_kernel(uint32_t* out) {
+  // hwreg(HW_REG_XCC_ID = 20, offset 0, size 4): size-1 in [15:11], id in [5:0].
+  const uint32_t xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xfu;
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc;
+}
+
+// results[b] = XCC of workgroup b of a grid of n workgroups (n <= 65536).
+int bench_xcc_map(double* results, int n) {
+  if (n < 1 || n > 65536) return set_error(CREDIT_ERR_BAD_CONFIG, "n_results %d (1..65536)", n);
+  DevBuf out;
+  CREDIT_TRY(out.alloc(static_cast<size_t>(n) * 4));
+  mb_xcc_kernel<<<static_cast<unsigned>(n), 64>>>(static_cast<uint32_t*>(out.p));
+  CREDIT_TRY(check_launch("mb_xcc_kernel"));
+  std::vector<uint32_t> h(static_cast<size_t>(n));
+  CREDIT_HIP(hipMemcpy(h.data(), out.p, h.size() * 4, hipMemcpyDeviceToHost));
+  for (int i = 0; i < n; ++i) results[i] = static_cast<double>(h[static_cast<size_t>(i)]);
+  return CREDIT_OK;
+}
+
 int bench_clock(double* results, int n) {
   DevBuf out;
   CREDIT_TRY(out.alloc(64));
@@ -729,18 +759,31 @@ int bench_pingpong(int rounds, double* results, int n) {
 
 }  // namespace
 
-int control_overhead(int64_t rows, int split, int barriers, int warmup, int iters,
-                     double* plain_ms, double* split_ms, int cooperative) {
+int control_overhead(int64_t rows, int split, int barriers, int lds_bytes, int threads,
+                     int warmup, int iters, double* plain_ms, double* split_ms, int cooperative) {
   const DeviceProps* props = nullptr;
   CREDIT_TRY(current_device_props(&props));
   if (split < 1 || split > 64) return set_error(CREDIT_ERR_BAD_CONFIG, "split %d", split);
   if (rows < 1) return set_error(CREDIT_ERR_BAD_CONFIG, "rows must be >= 1");
+  if (threads == 0) threads = 256;
+  if (threads < kWave || threads > 1024 || threads % kWave != 0)
+    return set_error(CREDIT_ERR_BAD_CONFIG, "threads %d (a multiple of 64 up to 1024)", threads);
+  if (lds_bytes < 0 || lds_bytes > props->max_lds_per_block)
+    return set_error(CREDIT_ERR_BAD_CONFIG, "lds_bytes %d (at most %d)", lds_bytes,
+                     props->max_lds_per_block);
+  const void* fn = reinterpret_cast<const void*>(mb_barrier_kernel);
+  const size_t lds = static_cast<size_t>(lds_bytes);
+  if (lds > 65536) CREDIT_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  static_cast<int>(lds)));
   int64_t groups = 0;
-  CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(mb_barrier_kernel), 256, 0, split,
-                               &groups));
+  int dispensers = 0;
+  CREDIT_TRY(coresident_groups(fn, threads, lds, split, &groups, &dispensers));
   if (groups < 1) return set_error(CREDIT_ERR_UNSUPPORTED, "split %d does not fit", split);
   if (groups > padded_groups(rows)) groups = padded_groups(rows);
   const int64_t per_group = (rows + groups - 1) / groups;
+  const int64_t stages64 = per_group * (barriers > 0 ? barriers : 1);
+  if (stages64 > int64_t{credit::plan::kMaxLaunchStages})
+    return set_error(CREDIT_ERR_BAD_CONFIG, "%lld barriers per group", static_cast<long long>(stages64));
   DevBuf ws, sink;
   if (split_slot_bytes(groups, split, 1, kSplitRing) > kSlotAreaBytes)
     return set_error(CREDIT_ERR_UNSUPPORTED, "barrier benchmark slots exceed the slot area");
@@ -757,21 +800,21 @@ int control_overhead(int64_t rows, int split, int barriers, int warmup, int iter
   const unsigned plain_grid = static_cast<unsigned>(rows * split);
   const uint32_t total = grid;
   int valid = static_cast<int>(rows);
-  const uint32_t stages = static_cast<uint32_t>(per_group * (barriers > 0 ? barriers : 1));
+  int lds_arg = lds_bytes;
+  SplitArgs sa{counters, slots, watchdog, total, static_cast<uint32_t>(stages64), kSplitRing};
+  sa.dispensers = static_cast<uint32_t>(dispensers);
   auto plain = [&](int) -> int {
     mb_plain_kernel<<<plain_grid, 256>>>(static_cast<int*>(sink.p));
     return check_launch("mb_plain_kernel");
   };
   int members = split;
   auto timed = [&](int) -> int {
-    SplitArgs sa{counters, slots, watchdog, total, next_split_epoch(stages), kSplitRing};
     if (cooperative) {
-      void* args[] = {&sa, &members, &barriers, &valid, &sinkp};
-      CREDIT_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mb_barrier_kernel),
-                                            dim3(grid), dim3(256), args, 0, nullptr));
+      void* args[] = {&sa, &members, &barriers, &valid, &sinkp, &lds_arg};
+      CREDIT_HIP(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(threads), args, lds, nullptr));
       return CREDIT_OK;
     }
-    mb_barrier_kernel<<<grid, 256>>>(sa, members, barriers, valid, sinkp);
+    mb_barrier_kernel<<<grid, threads, lds>>>(sa, members, barriers, valid, sinkp, lds_arg);
     return check_launch("mb_barrier_kernel");
   };
   CREDIT_TRY(time_ms(plain, warmup, iters, plain_ms));
@@ -813,6 +856,8 @@ extern "C" int credit_microbench(int32_t which, int64_t bytes, int32_t iters, do
       return bench_exchange_throughput(iters, results, n_results);
     case CREDIT_MB_MFMA_BF16:
       return bench_mfma(iters, results, n_results);
+    case CREDIT_MB_XCC_MAP:
+      return bench_xcc_map(results, n_results);
     default:
       return set_error(CREDIT_ERR_BAD_CONFIG, "unknown microbenchmark %d", which);
   }
@@ -830,11 +875,13 @@ extern "C" int credit_stream_ceiling(int32_t reads, int32_t writes, int64_t call
 }
 
 extern "C" int credit_control_overhead(int64_t rows, int32_t split, int32_t barriers,
-                                       int32_t warmup, int32_t iters, int32_t cooperative,
-                                       double* plain_ms, double* split_ms) {
+                                       int32_t lds_bytes, int32_t threads, int32_t warmup,
+                                       int32_t iters, int32_t cooperative, double* plain_ms,
+                                       double* split_ms) {
   CREDIT_TRY(check_ptr(plain_ms, "plain_ms"));
   CREDIT_TRY(check_ptr(split_ms, "split_ms"));
   if (rows < 1 || barriers < 0 || warmup < 0 || iters < 1)
     return set_error(CREDIT_ERR_BAD_CONFIG, "rows >= 1, barriers >= 0, iters >= 1 required");
-  return control_overhead(rows, split, barriers, warmup, iters, plain_ms, split_ms, cooperative);
+  return control_overhead(rows, split, barriers, lds_bytes, threads, warmup, iters, plain_ms,
+                          split_ms, cooperative);
 }

@@ -89,7 +89,7 @@ __device__ __forceinline__ Pair4 grads4(f32x4 x, f32x4 y, const Coef& k) {
 }
 
 template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void pearson_bwd_slice_kernel(
+__device__ __forceinline__ void pearson_bwd_slice_kernel_body(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ grad,
     float* __restrict__ dx, float* __restrict__ dy, int cols, int chunk, int members, int rows,
     float eps, SplitArgs sa) {
@@ -144,6 +144,15 @@ __global__ __launch_bounds__(THREADS) void pearson_bwd_slice_kernel(
       slice_store(dyo, lane_off + q * kStride, r.dy);
     }
   }
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void pearson_bwd_slice_kernel(
+    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ grad,
+    float* __restrict__ dx, float* __restrict__ dy, int cols, int chunk, int members, int rows,
+    float eps, SplitArgs sa) {
+  pearson_bwd_slice_kernel_body<THREADS, VPT>(x, y, grad, dx, dy, cols, chunk, members, rows, eps, sa);
+  split_leave(sa);
 }
 
 // Two passes over the row; VEC: f32x4 accesses.

@@ -52,7 +52,7 @@ __device__ __forceinline__ float inv_scale(float max_abs) {
 }
 
 template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void rowwise_quant_slice_kernel(
+__device__ __forceinline__ void rowwise_quant_slice_kernel_body(
     const float* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scale, int cols,
     int chunk, int members, int rows, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
@@ -86,6 +86,14 @@ __global__ __launch_bounds__(THREADS) void rowwise_quant_slice_kernel(
         __builtin_nontemporal_store(quant4(v[k], inv), &(qr + k * THREADS)[tid]);
     if (sl.member == 0 && threadIdx.x == 0) scale[row] = m / 127.0f;
   }
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void rowwise_quant_slice_kernel(
+    const float* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scale, int cols,
+    int chunk, int members, int rows, SplitArgs sa) {
+  rowwise_quant_slice_kernel_body<THREADS, VPT>(x, q, scale, cols, chunk, members, rows, sa);
+  split_leave(sa);
 }
 
 // Two passes over the row; VEC: f32x4 loads and 4-byte q stores.

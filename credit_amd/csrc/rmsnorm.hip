@@ -82,7 +82,7 @@ __device__ __forceinline__ u32x4 dx8(u32x4 x, u32x4 dy, u32x4 w, float rs, float
 // The member's slice is vectors [v0, v0 + vlen) of the row, held in VPT
 // dwordx4 registers per lane.
 template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
+__device__ __forceinline__ void rmsnorm_fwd_slice_kernel_body(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     uint16_t* __restrict__ y, float* __restrict__ rstd_out, int cols, int chunk,
     int members, int rows, float eps, SplitArgs sa) {
@@ -132,6 +132,15 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
                       scale8(v[k], buffer_load(wrs, lane_off + k * kStride), rs));
     if (member == 0 && threadIdx.x == 0) rstd_out[row] = rs;
   }
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void rmsnorm_fwd_slice_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    uint16_t* __restrict__ y, float* __restrict__ rstd_out, int cols, int chunk,
+    int members, int rows, float eps, SplitArgs sa) {
+  rmsnorm_fwd_slice_kernel_body<THREADS, VPT>(x, w, y, rstd_out, cols, chunk, members, rows, eps, sa);
+  split_leave(sa);
 }
 
 // Streaming forward: pass 1 sum of squares, pass 2 output.  VEC: rows are
@@ -203,7 +212,7 @@ constexpr int kBwdGiven = 2;     // c precomputed in rowdot[] (READ variant)
 // touches consecutive banks; that keeps VGPRs low enough for two
 // workgroups per CU.
 template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
+__device__ __forceinline__ void rmsnorm_bwd_slice_kernel_body(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ dy, const float* __restrict__ rstd,
     const float* __restrict__ rowdot, uint16_t* __restrict__ dx,
@@ -307,6 +316,17 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
       q[3] = f64x2{a[6 * THREADS], a[7 * THREADS]};
     }
   }
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ dy, const float* __restrict__ rstd,
+    const float* __restrict__ rowdot, uint16_t* __restrict__ dx,
+    double* __restrict__ dw_part, int rows, int cols, int chunk, int members,
+    int rows_per_group, int mode, SplitArgs sa) {
+  rmsnorm_bwd_slice_kernel_body<THREADS, VPT>(x, w, dy, rstd, rowdot, dx, dw_part, rows, cols, chunk, members, rows_per_group, mode, sa);
+  split_leave(sa);
 }
 
 // SPLIT variant.  The workgroup is THREADS data lanes (VPT dwordx4 of x
@@ -578,6 +598,7 @@ __attribute__((amdgpu_waves_per_eu(kGroupWavesPerEU<VPT>, 8))) void rmsnorm_bwd_
   rmsnorm_group_body<THREADS, VPT, false, DEPTH, AHEAD>(x, w, dy, rstd, nullptr, nullptr, dx, dw_part,
                                                  rows, cols, chunk, members, rows_per_group,
                                                  0.0f, sa);
+  split_leave(sa);
 }
 
 // Forward and backward in one pass: x, dy, w in; y, rstd, dx, dweight out.
@@ -590,6 +611,7 @@ __attribute__((amdgpu_waves_per_eu(kGroupWavesPerEU<VPT>, 8))) void rmsnorm_fuse
     int members, int rows_per_group, float eps, SplitArgs sa) {
   rmsnorm_group_body<THREADS, VPT, true, DEPTH, AHEAD>(x, w, dy, nullptr, rstd, y, dx, dw_part, rows,
                                                 cols, chunk, members, rows_per_group, eps, sa);
+  split_leave(sa);
 }
 
 // READ variant pre-pass: rowdot[r] = sum_j dy*w*x over the row, streamed.
@@ -947,6 +969,7 @@ struct FusedPlan {
   int rows_per_group;
   int64_t groups;       // groups with rows
   int64_t grid_groups;  // padded to a multiple of kDispensers
+  int dispensers;       // ticket subsets of the launch
 };
 
 int resolve_fused(const credit_cfg* cfg, int64_t rows, int64_t cols, int cu_count,
@@ -971,7 +994,7 @@ int resolve_fused(const credit_cfg* cfg, int64_t rows, int64_t cols, int cu_coun
   int64_t fit = 0;
   CREDIT_TRY(credit::coresident_groups(reinterpret_cast<const void*>((*pick)->fn),
                                        (*pick)->threads + kWave, (*pick)->lds_bytes(),
-                                       sp.members, &fit));
+                                       sp.members, &fit, &plan->dispensers));
   (void)cu_count;
   if (fit == 0)
     return set_error(CREDIT_ERR_UNSUPPORTED,
@@ -1075,19 +1098,23 @@ extern "C" int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uin
     return check_launch("rmsnorm_fwd_slice_kernel");
   }
   int64_t groups = 0;
+  int dispensers = 0;
   CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(pick->fn), pick->threads, 0,
-                               plan.members, &groups));
+                               plan.members, &groups, &dispensers));
   if (groups == 0)
     return set_error(CREDIT_ERR_UNSUPPORTED,
                      "rmsnorm_fwd: %d groups of %d members do not fit the device", kDispensers,
                      plan.members);
   if (groups > padded_groups(rows)) groups = padded_groups(rows);
   const int64_t per_group = (rows + groups - 1) / groups;
+  if (per_group > int64_t{credit::plan::kMaxLaunchStages})
+    return set_error(CREDIT_ERR_BAD_SHAPE, "rmsnorm_fwd: %lld rows per group",
+                     static_cast<long long>(per_group));
   SplitWorkspace ws;
   CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 1, kSplitRing, 0, &ws));
   const uint32_t total = static_cast<uint32_t>(groups * plan.members);
   const SplitArgs sa =
-      make_split_args(ws, total, next_split_epoch(static_cast<uint32_t>(per_group)), kSplitRing);
+      make_split_args(ws, total, static_cast<uint32_t>(per_group), kSplitRing, dispensers);
   hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads), 0, stream, x, w, y, rstd, c,
                      static_cast<int>(plan.chunk), plan.members, static_cast<int>(rows), eps,
                      sa);
@@ -1145,8 +1172,9 @@ extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
   if (mode == kBwdExchange) {
     const BwdGroupPick* pick = pick_for(kBwdGroup, plan.chunk);
     int64_t fit = 0;
+    int dispensers = 0;
     CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(pick->fn), pick->threads + kWave,
-                                 pick->lds_bytes(), plan.members, &fit));
+                                 pick->lds_bytes(), plan.members, &fit, &dispensers));
     if (padded_groups(plan.groups) > fit)
       return set_error(CREDIT_ERR_UNSUPPORTED,
                        "rmsnorm_bwd: %lld groups of %d members exceed the %lld resident at once",
@@ -1156,9 +1184,8 @@ extern "C" int credit_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* w,
                        pick->lds_bytes(), stream, x, w, dy, rstd, dx, dw_part,
                        static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members,
                        plan.rows_per_group,
-                       make_split_args(ws, total,
-                                       next_split_epoch(static_cast<uint32_t>(plan.rows_per_group)),
-                                       kBwdRing));
+                       make_split_args(ws, total, static_cast<uint32_t>(plan.rows_per_group),
+                                       kBwdRing, dispensers));
     CREDIT_TRY(check_launch("rmsnorm_bwd_group_kernel"));
   } else {
     const BwdPick* pick = pick_for(kBwd, plan.chunk);
@@ -1256,9 +1283,8 @@ extern "C" int credit_rmsnorm_fwd_bwd_bf16(const uint16_t* x, const uint16_t* w,
   hipLaunchKernelGGL(pick->fn, dim3(total), dim3(pick->threads + kWave), pick->lds_bytes(),
                      stream, x, w, dy, rstd, y, dx, dw_part, static_cast<int>(rows), c,
                      static_cast<int>(plan.chunk), plan.members, plan.rows_per_group, eps,
-                     make_split_args(ws, total,
-                                     next_split_epoch(static_cast<uint32_t>(plan.rows_per_group)),
-                                     kBwdRing));
+                     make_split_args(ws, total, static_cast<uint32_t>(plan.rows_per_group),
+                                     kBwdRing, plan.dispensers));
   CREDIT_TRY(check_launch("rmsnorm_fused_group_kernel"));
   const unsigned reduce_blocks = static_cast<unsigned>((cols / 2 + 255) / 256);
   rmsnorm_dw_reduce_kernel<<<dim3(reduce_blocks), dim3(256), 0, stream>>>(

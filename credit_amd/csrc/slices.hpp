@@ -128,19 +128,22 @@ int launch_slices(const credit_cfg* cfg, int64_t rows, const Plan& plan, const P
     return check_launch(name);
   }
   int64_t groups = 0;
+  int dispensers = 0;
   CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(pk->fn), pk->threads, 0,
-                               plan.members, &groups));
+                               plan.members, &groups, &dispensers));
   if (groups == 0)
     return set_error(CREDIT_ERR_UNSUPPORTED, "%s: %d groups of %d members do not fit the device",
                      name, kDispensers, plan.members);
   if (groups > padded_groups(rows)) groups = padded_groups(rows);
   const int64_t per_group = (rows + groups - 1) / groups;
+  if (per_group * stages > int64_t{credit::plan::kMaxLaunchStages})
+    return set_error(CREDIT_ERR_BAD_SHAPE, "%s: %lld rows per group exceed the exchange tags of "
+                     "one launch", name, static_cast<long long>(per_group));
   SplitWorkspace ws;
   CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, k_values, kSplitRing, 0, &ws));
   const uint32_t total = static_cast<uint32_t>(groups * plan.members);
-  launch(total, make_split_args(ws, total,
-                                next_split_epoch(static_cast<uint32_t>(per_group * stages)),
-                                kSplitRing));
+  launch(total, make_split_args(ws, total, static_cast<uint32_t>(per_group * stages), kSplitRing,
+                                dispensers));
   return check_launch(name);
 }
 

@@ -101,7 +101,7 @@ __device__ __forceinline__ void split_merge_maxsum(const SplitGroup& g, float* m
 
 // --------------------------------------------------------- forward (C4) --
 template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void softmax_fwd_slice_kernel(
+__device__ __forceinline__ void softmax_fwd_slice_kernel_body(
     const float* __restrict__ x, float* __restrict__ p, float* __restrict__ rowmax,
     float* __restrict__ lse, int cols, int chunk, int members, int rows, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
@@ -149,6 +149,14 @@ __global__ __launch_bounds__(THREADS) void softmax_fwd_slice_kernel(
     lse[row] = static_cast<float>(static_cast<double>(m) + ::log(s));
   }
   }
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void softmax_fwd_slice_kernel(
+    const float* __restrict__ x, float* __restrict__ p, float* __restrict__ rowmax,
+    float* __restrict__ lse, int cols, int chunk, int members, int rows, SplitArgs sa) {
+  softmax_fwd_slice_kernel_body<THREADS, VPT>(x, p, rowmax, lse, cols, chunk, members, rows, sa);
+  split_leave(sa);
 }
 
 // One wave merges up to 64 (max, sum) partials, one per lane (`has`
@@ -203,8 +211,7 @@ __device__ __forceinline__ T& pick4(T& a, T& b, T& c, T& d) {
 }
 
 template <int THREADS, int VPT, bool PARK = false>
-__global__ __launch_bounds__(THREADS + kWave)
-__attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void softmax_fwd_group_kernel(
+__device__ __forceinline__ void softmax_fwd_group_kernel_body(
     const float* __restrict__ x, float* __restrict__ p, float* __restrict__ rowmax,
     float* __restrict__ lse, int rows, int cols, int chunk, int members, int rows_per_group,
     SplitArgs sa) {
@@ -422,6 +429,16 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
   if (i + 2 < r1) step(b2, b0, b1, i + 2);
 }
 
+template <int THREADS, int VPT, bool PARK = false>
+__global__ __launch_bounds__(THREADS + kWave)
+__attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void softmax_fwd_group_kernel(
+    const float* __restrict__ x, float* __restrict__ p, float* __restrict__ rowmax,
+    float* __restrict__ lse, int rows, int cols, int chunk, int members, int rows_per_group,
+    SplitArgs sa) {
+  softmax_fwd_group_kernel_body<THREADS, VPT, PARK>(x, p, rowmax, lse, rows, cols, chunk, members, rows_per_group, sa);
+  split_leave(sa);
+}
+
 // Backward group kernel (SPLIT on rows wider than one workgroup): the row
 // pipeline of softmax_fwd_group_kernel with one exchanged value per row,
 // c = sum_j p*dy.  THREADS data lanes hold VPT f32x4 of p and of dy per row
@@ -436,8 +453,7 @@ __attribute__((amdgpu_waves_per_eu(THREADS <= 512 && VPT <= 4 ? 4 : 3, 8))) void
 // rows into LDS, so each row is published four steps before its total is
 // needed, with the same four register buffers (the forward's scheme).
 template <int THREADS, int VPT, bool PARK = false>
-__global__ __launch_bounds__(THREADS + kWave)
-__attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
+__device__ __forceinline__ void softmax_bwd_group_kernel_body(
     const float* __restrict__ p, const float* __restrict__ dy, float* __restrict__ dx, int rows,
     int cols, int chunk, int members, int rows_per_group, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
@@ -612,6 +628,15 @@ __attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
   if (i + 2 < r1) step(b2, b0, b1, i + 2);
 }
 
+template <int THREADS, int VPT, bool PARK = false>
+__global__ __launch_bounds__(THREADS + kWave)
+__attribute__((amdgpu_waves_per_eu(3, 8))) void softmax_bwd_group_kernel(
+    const float* __restrict__ p, const float* __restrict__ dy, float* __restrict__ dx, int rows,
+    int cols, int chunk, int members, int rows_per_group, SplitArgs sa) {
+  softmax_bwd_group_kernel_body<THREADS, VPT, PARK>(p, dy, dx, rows, cols, chunk, members, rows_per_group, sa);
+  split_leave(sa);
+}
+
 // Streaming forward: online (max, sum) pass, then the output pass.  VEC:
 // f32x4 loads (cols % 4 == 0, 16-byte aligned rows); else element loads.
 template <int THREADS, bool VEC>
@@ -679,7 +704,7 @@ __global__ __launch_bounds__(THREADS) void softmax_fwd_read_kernel(
 
 // -------------------------------------------------------- backward (C4) --
 template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void softmax_bwd_slice_kernel(
+__device__ __forceinline__ void softmax_bwd_slice_kernel_body(
     const float* __restrict__ p, const float* __restrict__ dy, float* __restrict__ dx, int cols,
     int chunk, int members, int rows, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
@@ -713,6 +738,14 @@ __global__ __launch_bounds__(THREADS) void softmax_bwd_slice_kernel(
 #pragma unroll
     for (int k = 0; k < VPT; ++k) slice_store(xr, lane_off + k * kStride, grad4(pv[k], dv[k], d));
   }
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void softmax_bwd_slice_kernel(
+    const float* __restrict__ p, const float* __restrict__ dy, float* __restrict__ dx, int cols,
+    int chunk, int members, int rows, SplitArgs sa) {
+  softmax_bwd_slice_kernel_body<THREADS, VPT>(p, dy, dx, cols, chunk, members, rows, sa);
+  split_leave(sa);
 }
 
 template <int THREADS, bool VEC>
@@ -761,7 +794,7 @@ __global__ __launch_bounds__(THREADS) void softmax_bwd_read_kernel(
 // registers (src/workloads/softmax_logits_backward.cu:410-476 runs the same
 // math as three cluster reductions).
 template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void softmax_logits_bwd_slice_kernel(
+__device__ __forceinline__ void softmax_logits_bwd_slice_kernel_body(
     const float* __restrict__ logits, const float* __restrict__ dy, float* __restrict__ dx,
     int cols, int chunk, int members, int rows, SplitArgs sa) {
   constexpr int NW = THREADS / kWave;
@@ -841,6 +874,14 @@ __global__ __launch_bounds__(THREADS) void softmax_logits_bwd_slice_kernel(
 #pragma unroll
     for (int k = 0; k < VPT; ++k) slice_store(xr, lane_off + k * kStride, grad4(v[k], dv[k], d));
   }
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void softmax_logits_bwd_slice_kernel(
+    const float* __restrict__ logits, const float* __restrict__ dy, float* __restrict__ dx,
+    int cols, int chunk, int members, int rows, SplitArgs sa) {
+  softmax_logits_bwd_slice_kernel_body<THREADS, VPT>(logits, dy, dx, cols, chunk, members, rows, sa);
+  split_leave(sa);
 }
 
 // Streaming logits backward: online (max, sum) over the logits; sum p*dy
@@ -994,9 +1035,14 @@ int resolve_fwd(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
   return resolve(cfg, cols, vec, kFwdCapacity, "softmax_fwd", plan);
 }
 
-// At most 32 members, as the forward: a 64-member launch of the 256-lane
-// kernel (two workgroups per CU, G*P equal to the resident count) ran into
-// the exchange watchdog at 9 x 262144; wider groups take the slice kernel.
+// At most 32 members, as the forward; wider groups take the slice kernel.
+// A 64-member launch of the 256-lane kernel ran into the exchange watchdog
+// at 9 x 262144 when the launch sizing still put one group across every
+// slot of each 8-way ticket subset (two workgroups per CU, G*P equal to the
+// resident count): one slot withheld from such a launch strands that group
+// (tests/cpp/split_protocol_model.cpp, withheld_old).  The sizing now keeps
+// two groups per subset (split_plan.hpp, dispensers_for); the 64-member
+// group kernel is not needed by any shape AUTO picks and stays off.
 constexpr int kMaxBwdGroupMembers = 32;
 
 bool bwd_group_ok(const Plan& plan) {
@@ -1025,15 +1071,15 @@ int resolve_bwd(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
 // fit the device at once (a multiple of kDispensers); the kernels deal the
 // rows to them round-robin, at most rows_per_group each.
 int plan_row_groups(const void* fn, int threads, int members, int64_t rows, int* rows_per_group,
-                    int64_t* groups, const char* name) {
+                    int64_t* groups, int* dispensers, const char* name) {
   int64_t fit = 0;
-  CREDIT_TRY(coresident_groups(fn, threads, 0, members, &fit));
+  CREDIT_TRY(coresident_groups(fn, threads, 0, members, &fit, dispensers));
   if (fit == 0)
     return set_error(CREDIT_ERR_UNSUPPORTED, "%s: %d groups of %d members do not fit the device",
                      name, kDispensers, members);
   const int64_t g = fit < padded_groups(rows) ? fit : padded_groups(rows);
   const int64_t r = (rows + g - 1) / g;
-  if (r > (int64_t{1} << 30))
+  if (r > int64_t{credit::plan::kMaxLaunchStages})
     return set_error(CREDIT_ERR_BAD_SHAPE, "%s: %lld rows per group", name,
                      static_cast<long long>(r));
   *rows_per_group = static_cast<int>(r);
@@ -1094,15 +1140,16 @@ extern "C" int credit_softmax_fwd_f32(const float* x, float* p, float* rowmax, f
     const int threads = gk->threads + kWave;
     int rpg = 0;
     int64_t groups = 0;
+    int dispensers = 0;
     CREDIT_TRY(plan_row_groups(reinterpret_cast<const void*>(gk->fn), threads, plan.members, rows,
-                               &rpg, &groups, "softmax_fwd_group_kernel"));
+                               &rpg, &groups, &dispensers, "softmax_fwd_group_kernel"));
     SplitWorkspace ws;
     CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 2, kGroupRing, 0, &ws));
     const uint32_t total = static_cast<uint32_t>(groups * plan.members);
     hipLaunchKernelGGL(gk->fn, dim3(total), dim3(threads), 0, stream, x, p, rowmax, lse,
                        static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members, rpg,
-                       make_split_args(ws, total, next_split_epoch(static_cast<uint32_t>(rpg)),
-                                       kGroupRing));
+                       make_split_args(ws, total, static_cast<uint32_t>(rpg), kGroupRing,
+                                       dispensers));
     return check_launch("softmax_fwd_group_kernel");
   }
   const Pick<FwdFn>* pk = pick_for(kFwd, plan.chunk);
@@ -1144,15 +1191,16 @@ extern "C" int credit_softmax_bwd_f32(const float* p, const float* dy, float* dx
     const int threads = gk->threads + kWave;
     int rpg = 0;
     int64_t groups = 0;
+    int dispensers = 0;
     CREDIT_TRY(plan_row_groups(reinterpret_cast<const void*>(gk->fn), threads, plan.members, rows,
-                               &rpg, &groups, "softmax_bwd_group_kernel"));
+                               &rpg, &groups, &dispensers, "softmax_bwd_group_kernel"));
     SplitWorkspace ws;
     CREDIT_TRY(acquire_split_workspace(cfg, groups, plan.members, 1, kGroupRing, 0, &ws));
     const uint32_t total = static_cast<uint32_t>(groups * plan.members);
     hipLaunchKernelGGL(gk->fn, dim3(total), dim3(threads), 0, stream, p, dy, dx,
                        static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members, rpg,
-                       make_split_args(ws, total, next_split_epoch(static_cast<uint32_t>(rpg)),
-                                       kGroupRing));
+                       make_split_args(ws, total, static_cast<uint32_t>(rpg), kGroupRing,
+                                       dispensers));
     return check_launch("softmax_bwd_group_kernel");
   }
   const Pick<BwdFn>* pk = pick_for(kBwd, plan.chunk);

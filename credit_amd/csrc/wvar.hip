@@ -87,7 +87,7 @@ __device__ __forceinline__ f32x4 dx4(f32x4 x, f32x4 w, f32x4 dy, const Coef& k) 
 }
 
 template <int THREADS, int VPT>
-__global__ __launch_bounds__(THREADS) void wvar_bwd_slice_kernel(
+__device__ __forceinline__ void wvar_bwd_slice_kernel_body(
     const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ dy,
     float* __restrict__ dx, int cols, int chunk, int members, int rows, float eps,
     SplitArgs sa) {
@@ -130,6 +130,15 @@ __global__ __launch_bounds__(THREADS) void wvar_bwd_slice_kernel(
     for (int q = 0; q < VPT; ++q)
       slice_store(out, lane_off + q * kStride, dx4(xv[q], wv[q], dv[q], k));
   }
+}
+
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void wvar_bwd_slice_kernel(
+    const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ dy,
+    float* __restrict__ dx, int cols, int chunk, int members, int rows, float eps,
+    SplitArgs sa) {
+  wvar_bwd_slice_kernel_body<THREADS, VPT>(x, w, dy, dx, cols, chunk, members, rows, eps, sa);
+  split_leave(sa);
 }
 
 // Two passes over the row; VEC: f32x4 accesses.

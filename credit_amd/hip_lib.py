@@ -144,8 +144,9 @@ SIGNATURES: dict[str, list] = {
     "credit_stream_ceiling": [ctypes.c_int32, ctypes.c_int32, _I64, ctypes.c_int32, ctypes.c_int32,
                               ctypes.c_double, ctypes.POINTER(ctypes.c_double), ctypes.c_int32],
     "credit_control_overhead": [_I64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
-                                ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
-                                ctypes.POINTER(ctypes.c_double)],
+                                ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],
+    "credit_last_split_shape": [ctypes.POINTER(ctypes.c_int32)] * 4,
 }
 _RESTYPES = {
     "credit_version": ctypes.c_char_p,
@@ -277,6 +278,7 @@ MICROBENCH = {
     "cache_read": 9,
     "exchange_throughput": 10,
     "mfma_bf16": 11,
+    "xcc_map": 12,
 }
 
 
@@ -314,18 +316,47 @@ def stream_ceiling(reads: int, writes: int, call_bytes: int, trials: int = 5, it
 
 
 def control_overhead(rows: int, split: int, barriers: int, warmup: int = 3, iters: int = 20,
-                     cooperative: bool = False) -> tuple[float, float]:
+                     cooperative: bool = False, lds_bytes: int = 0,
+                     threads: int = 0) -> tuple[float, float]:
     """(plain_ms, split_ms): `rows` rows covered by a co-resident wave of
     ticketed groups of `split` workgroups meeting `barriers` times per row,
     against a plain launch of rows * split workgroups with no exchange
-    (replaces build/cluster_control)."""
+    (replaces build/cluster_control).  The barrier workgroups have `threads`
+    lanes (0: 256) and `lds_bytes` of dynamic LDS, the reference's
+    --shared-bytes (src/cluster_control.cu:76-88)."""
     plain = ctypes.c_double()
     split_ms = ctypes.c_double()
-    check(load_library().credit_control_overhead(rows, split, barriers, warmup, iters,
-                                                 int(cooperative), ctypes.byref(plain),
-                                                 ctypes.byref(split_ms)),
+    check(load_library().credit_control_overhead(rows, split, barriers, int(lds_bytes),
+                                                 int(threads), warmup, iters, int(cooperative),
+                                                 ctypes.byref(plain), ctypes.byref(split_ms)),
           "credit_control_overhead")
     return plain.value, split_ms.value
+
+
+def last_split_shape() -> dict:
+    """Shape of this thread's last co-resident split launch
+    (credit_last_split_shape): block size, LDS per workgroup, workgroups per
+    CU and ticket subsets."""
+    vals = [ctypes.c_int32() for _ in range(4)]
+    check(load_library().credit_last_split_shape(*[ctypes.byref(v) for v in vals]),
+          "credit_last_split_shape")
+    return dict(zip(("threads", "lds_bytes", "per_cu", "dispensers"), (v.value for v in vals)))
+
+
+def control_lds_bytes(shape: dict, lds_per_cu: int) -> int:
+    """Dynamic LDS for credit_control_overhead that gives the barrier grid
+    the split launch's residency: the launch's own LDS, raised (when the
+    launch's occupancy is set by registers rather than LDS) into the window
+    (lds_per_cu / (per_cu + 1), lds_per_cu / per_cu] that admits exactly
+    per_cu workgroups per CU.  1 KiB of margin on both sides covers the
+    barrier kernel's static LDS and the allocation granularity."""
+    per_cu = max(int(shape["per_cu"]), 1)
+    lds = int(shape["lds_bytes"])
+    lo = lds_per_cu // (per_cu + 1) + 1024
+    hi = lds_per_cu // per_cu - 1024
+    if lo <= hi:
+        lds = min(max(lds, lo), hi)
+    return max(lds, 0)
 
 
 # --------------------------------------------------------------- operators --

@@ -9,8 +9,11 @@ through ``hip_lib.HIP_LAUNCHERS``:
 * the block variants (READ, and STAGED where the row fits one workgroup)
   give ``block_ms`` -- the reference's best non-DSMEM time;
 * SPLIT with P members for P in ``splits`` gives ``cluster_ms[P]``;
-* ``credit_control_overhead`` gives the barrier cost for (rows, P, the
-  workload's barrier count) -- the reference's cluster_control run;
+* ``credit_control_overhead`` gives the barrier cost for each (workload,
+  N, P) -- the reference's cluster_control run -- with the barrier
+  workgroups shaped like that split launch (its block size and LDS,
+  ``credit_last_split_shape``), as the reference passes each point's
+  staged slice as --shared-bytes;
 * every variant's output is checked against the READ variant's (the
   reference never compared its CUDA kernels with anything).
 
@@ -175,6 +178,10 @@ def measure_point(name: str, spec: WorkloadSpec, rows: int, cols: int, cfg: RunC
             torch.cuda.synchronize()
             hip_lib.check_watchdog()
             row["correct"] = all(_close(o, r) for o, r in zip(outs[0], reference))
+            if variant == "split":
+                # The launch's own shape prices its control overhead
+                # (runner.py:714-723 passes the staged slice as --shared-bytes).
+                row.update(hip_lib.last_split_shape())
             # Arguments checked and converted once per buffer set: the timed
             # calls are the library calls alone, not the launcher's Python.
             bound = [hip_lib.bind(name, ins, o, lc) for ins, o in zip(sets, outs)]
@@ -192,11 +199,16 @@ def measure_point(name: str, spec: WorkloadSpec, rows: int, cols: int, cfg: RunC
     return results
 
 
-def measure_control(rows: int, split: int, barriers: int, cfg: RunConfig) -> float:
+def measure_control(rows: int, split: int, barriers: int, cfg: RunConfig, threads: int = 0,
+                    lds_bytes: int = 0) -> float:
+    """Median over trials of the barrier grid's time minus the plain grid's
+    (runner.py:313-347), the barrier workgroups shaped like the split launch
+    they price: `threads` lanes and `lds_bytes` of LDS."""
     samples = []
     for _ in range(cfg.trials):
         plain, coop = hip_lib.control_overhead(rows, split, max(barriers, 1), cfg.warmup,
-                                               cfg.iterations)
+                                               cfg.iterations, lds_bytes=lds_bytes,
+                                               threads=threads)
         samples.append(max(coop - plain, 0.0))
     return statistics.median(samples)
 
@@ -204,7 +216,7 @@ def measure_control(rows: int, split: int, barriers: int, cfg: RunConfig) -> flo
 # -------------------------------------------------------------- summary ----
 
 
-def build_summary(raw: list[dict[str, Any]], control: dict[tuple[int, int, int], float],
+def build_summary(raw: list[dict[str, Any]], control: dict[tuple[str, int, int], float],
                   profile: DeviceProfile, cfg: RunConfig):
     """summary and cluster_sweep rows (dsmem_eval/runner.py:444-620)."""
     by_point: dict[tuple[str, int, int], list[dict]] = defaultdict(list)
@@ -221,7 +233,7 @@ def build_summary(raw: list[dict[str, Any]], control: dict[tuple[int, int, int],
         best_split = min(splits, key=lambda r: r["ms"])
         candidates = []
         for r in splits:
-            ctl = control.get((rows, r["split"], spec.barrier_count), math.nan)
+            ctl = control.get((name, cols, r["split"]), math.nan)
             if not math.isfinite(ctl):
                 continue
             m = estimate(spec, cols, r["split"], ctl, profile, baseline_ms=block["ms"], rows=rows)
@@ -309,21 +321,31 @@ def run_suite(raw_config: dict[str, Any], output_dir: Path,
         return metadata
 
     raw: list[dict[str, Any]] = []
-    control: dict[tuple[int, int, int], float] = {}
+    control: dict[tuple[str, int, int], float] = {}
+    control_rows: list[dict[str, Any]] = []
+    lds_per_cu = int(info["lds_bytes_per_cu"])
     for name in cfg.workloads:
         spec = WORKLOADS[name]
         for cols in cfg.n_values:
             rows = sweep_rows(spec, cols, cfg.tensor_bytes)
             print(f"sweep {name}: rows={rows} cols={cols}", flush=True)
-            raw += measure_point(name, spec, rows, cols, cfg, dev)
-            for p in cfg.splits:
-                key = (rows, p, spec.barrier_count)
-                if key not in control:
-                    control[key] = measure_control(rows, p, spec.barrier_count, cfg)
+            point = measure_point(name, spec, rows, cols, cfg, dev)
+            raw += point
+            # One control run per (workload, N, P), shaped like that split
+            # launch (runner.py:692-723 keys its control samples the same way).
+            for r in point:
+                if r["variant"] != "split" or "threads" not in r:
+                    continue
+                lds = hip_lib.control_lds_bytes(r, lds_per_cu)
+                key = (name, cols, r["split"])
+                control[key] = measure_control(rows, r["split"], spec.barrier_count, cfg,
+                                               threads=r["threads"], lds_bytes=lds)
+                control_rows.append({"workload": name, "cols": cols, "rows": rows,
+                                     "split": r["split"], "barriers": spec.barrier_count,
+                                     "threads": r["threads"], "lds_bytes": lds,
+                                     "per_cu": r["per_cu"], "overhead_ms": control[key]})
             write_table(output_dir / "raw.csv", raw, bundle.RAW)
-    write_table(output_dir / "control.csv",
-                [{"rows": r, "split": p, "barriers": b, "overhead_ms": v}
-                 for (r, p, b), v in sorted(control.items())], bundle.CONTROL)
+    write_table(output_dir / "control.csv", control_rows, bundle.CONTROL)
     summary, sweep = build_summary(raw, control, profile, cfg)
     write_table(output_dir / "summary.csv", summary, bundle.SUMMARY)
     write_table(output_dir / "cluster_sweep.csv", sweep, bundle.SWEEP)

@@ -24,10 +24,10 @@
  *  - Streams: work is enqueued on cfg->stream (a hipStream_t; NULL means the
  *    null stream).  cfg itself may be NULL (= all defaults).
  *  - Workspace: split-row variants exchange partial results through a device
- *    buffer: a 256-byte header (the watchdog word), a 1 MiB counter area
- *    (ticket dispensers, arrival counters), a 4 MiB area of tagged exchange
- *    slots, then per-call scratch (dweight partials, the FFN's hidden
- *    activation, ...).
+ *    buffer: a 256-byte header (the watchdog word, the exchange-tag sequence
+ *    and an exit count), a 1 MiB counter area (ticket dispensers, arrival
+ *    counters), a 4 MiB area of tagged exchange slots, then per-call scratch
+ *    (dweight partials, the FFN's hidden activation, ...).
  *    - cfg->workspace == NULL: the library keeps one buffer per (device,
  *      stream) and grows it on demand.  Calls on one stream run in order,
  *      calls on different streams get different buffers, so concurrent
@@ -38,14 +38,16 @@
  *    - cfg->workspace set: it must hold credit_workspace_bytes(...) bytes,
  *      be 256-byte aligned, and its first 5 MiB + 256 bytes (header,
  *      counters, slots) must read zero before its first use.  Calls keep
- *      those bytes in that state (counters return to zero; slot tags are
- *      fresh per launch), so no clearing is needed between calls; the
- *      scratch part is overwritten freely.  Calls that share one caller
- *      workspace must not run concurrently (on different streams).  Slot
- *      tags are drawn from a 32-bit process-wide counter: after 2^32 - 1
- *      exchange stages it restarts, the library then re-zeroes the slot
- *      areas of its own buffers, and a caller workspace should be re-zeroed
- *      by its owner.
+ *      those bytes in that state, so no clearing is needed between calls;
+ *      the scratch part is overwritten freely.  Calls that share one caller
+ *      workspace must not run concurrently (on different streams).
+ *    - Exchange tags come from the header's sequence word, which each split
+ *      launch reads as it starts and its last workgroup advances on the
+ *      device; the launch that takes it past 3 * 2^30 returns the slot area
+ *      to zero and restarts it.  Nothing about the tags is fixed at enqueue
+ *      time, so a split call captured into a HIP graph (on a stream whose
+ *      workspace exists, a caller workspace, or the allocation-free entry
+ *      point) computes correct results on every replay.
  *  - Split launches and co-residency: the SPLIT kernels (and AUTO when it
  *    splits a row) size their grid to the workgroups the device holds at
  *    once and wait inside a group for all of its members.  They need the
@@ -492,6 +494,12 @@ int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t rows, int6
 #define CREDIT_MB_CACHE_READ 9
 #define CREDIT_MB_EXCHANGE_THROUGHPUT 10
 #define CREDIT_MB_MFMA_BF16 11
+/*  XCC_MAP                the XCC (hardware register XCC_ID) each workgroup
+ *                         of an n_results-workgroup grid ran on, results[b]
+ *                         for workgroup b: the round-robin dispatch the
+ *                         split launches' ticket subsets assume.  No
+ *                         counterpart in the reference (one die per GPU). */
+#define CREDIT_MB_XCC_MAP 12
 int credit_microbench(int32_t which, int64_t bytes, int32_t iters, double* results,
                       int32_t n_results);
 
@@ -517,12 +525,26 @@ int credit_stream_ceiling(int32_t reads, int32_t writes, int64_t call_bytes, int
  * dsmem_eval/runner.py:313-347): time of a grid of `rows` groups of `split`
  * workgroups that meet at `barriers` split-row barriers (the ticketed
  * exchange of the split kernels), against a plain launch of the same grid
- * that does nothing.  cooperative != 0 launches the barrier grid with
- * hipLaunchCooperativeKernel instead (capped at what fits the device), to
- * expose that launch path's fixed cost. */
-int credit_control_overhead(int64_t rows, int32_t split, int32_t barriers, int32_t warmup,
-                            int32_t iters, int32_t cooperative, double* plain_ms,
-                            double* split_ms);
+ * that does nothing.  The barrier workgroups have `threads` lanes (0: 256)
+ * and `lds_bytes` of dynamic LDS, as the reference's cluster kernel has
+ * --shared-bytes of dynamic shared memory (cluster_control.cu:76-88,135,149):
+ * the split launch being priced gives both (credit_last_split_shape), so the
+ * barrier grid holds as many workgroups per CU as that launch.  cooperative
+ * != 0 launches the barrier grid with hipLaunchCooperativeKernel instead
+ * (capped at what fits the device), to expose that launch path's fixed
+ * cost. */
+int credit_control_overhead(int64_t rows, int32_t split, int32_t barriers, int32_t lds_bytes,
+                            int32_t threads, int32_t warmup, int32_t iters, int32_t cooperative,
+                            double* plain_ms, double* split_ms);
+
+/* Shape of the last co-resident split launch this thread made: block size
+ * (data lanes plus any communication wave), LDS per workgroup (static and
+ * dynamic), workgroups resident per CU, and its ticket subsets.  What the
+ * reference's runner passes to cluster_control as --shared-bytes for each
+ * sweep point (dsmem_eval/runner.py:714-723); CREDIT_ERR_UNSUPPORTED before
+ * any split launch on this thread. */
+int credit_last_split_shape(int32_t* threads, int32_t* lds_bytes, int32_t* per_cu,
+                            int32_t* dispensers);
 
 #ifdef __cplusplus
 }

@@ -124,7 +124,13 @@ def test_rmsnorm_fwd_caller_workspace(gpu):
         hip_lib.rmsnorm_fwd(xs, wsb, y, rstd, EPS, hip_lib.make_cfg("split", 4, workspace=ws))
         torch.cuda.synchronize()
         check_fwd(x, w, y.float().cpu().numpy(), rstd.cpu().numpy())
-    assert int(ws[: 256 + 4 * 262144].count_nonzero()) == 0  # header + counters back to zero
+    # Watchdog, exit count and counters back to zero; the tag sequence (header
+    # byte 64) advanced by the three launches' stages.
+    head = ws[: 256 + 4 * 262144].clone()
+    seq = int(head[64:68].cpu().view(torch.int32).item())
+    head[64:68] = 0
+    assert int(head.count_nonzero()) == 0
+    assert seq > 0 and seq % 3 == 0
 
 
 BWD_VARIANTS = [("auto", 0), ("read", 0), ("split", 2), ("split", 4), ("split", 5)]

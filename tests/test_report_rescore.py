@@ -28,8 +28,7 @@ def synthetic_bundle(tmp_path):
                 raw.append(dict(workload=name, rows=rows, cols=cols, variant="split", split=p,
                                 ms=split_ms * (1 + 0.1 * (p == 4)), p20_ms=split_ms,
                                 p80_ms=split_ms, correct=True))
-                for barriers in (1, 2):
-                    control[(rows, p, barriers)] = 0.004
+                control[(name, cols, p)] = 0.004
     summary, sweep = build_summary(raw, control, MI355X_NOMINAL, RunConfig())
     run = tmp_path / "bundle"
     bundle.write_table(run / "summary.csv", summary, bundle.SUMMARY)

@@ -108,7 +108,8 @@ def test_build_summary_scores_model_like_the_reference():
     cfg = RunConfig()
     raw = _raw("softmax_fwd", 256, 262144, 0.30, {2: 0.35, 4: 0.20}) + \
         _raw("row_sum_max", 16384, 4096, 0.05, {2: 0.06, 4: 0.07})
-    control = {(256, 2, 1): 0.004, (256, 4, 1): 0.006, (16384, 2, 1): 0.01, (16384, 4, 1): 0.02}
+    control = {("softmax_fwd", 262144, 2): 0.004, ("softmax_fwd", 262144, 4): 0.006,
+               ("row_sum_max", 4096, 2): 0.01, ("row_sum_max", 4096, 4): 0.02}
     summary, sweep = build_summary(raw, control, prof, cfg)
     by = {r["workload"]: r for r in summary}
     assert by["softmax_fwd"]["measured_profitable"] and by["softmax_fwd"]["measured_split"] == 4
