@@ -34,7 +34,8 @@ measured the same way and reported under "suite".  Per workload:
 
 Each step is one library call whose arguments were checked and converted
 once (hip_lib.bind), so a short kernel is not timed behind its Python
-checks.  Prints ONE JSON line.
+checks.  Prints ONE JSON line (each suite entry in compact form; every
+workload's full record goes to --detail).
 """
 from __future__ import annotations
 
@@ -127,6 +128,9 @@ def parse_args(argv=None):
                     help="skip the per-variant sweep")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bound on the CPU-baseline sample per workload")
+    ap.add_argument("--detail", default="gpurun_out/bench_detail.json",
+                    help="file for every workload's full record (variant sweep, ceilings, "
+                         "trials); '' to skip")
     return ap.parse_args(argv)
 
 
@@ -300,6 +304,11 @@ def measure(name, args, hip_lib, torch, dev, with_cpu):
                              "frac_median": round(flops / (trials.median_ms * 1e-3) / 1e12
                                                   / BF16_PEAK_TFLOPS, 4),
                              "traffic": traffic, "traffic_source": traffic_note})
+        # The shader clock the GEMM tiles ran at, over the same number of
+        # settled calls as one trial block (the clock probe's stamps).
+        i0 = 10 ** 6
+        out["clock_MHz"] = round(hip_lib.gemm_clock_mhz(
+            lambda: [launch(i0 + k) for k in range(max(20, args.steps))]), 1)
         if not args.no_ceiling:
             try:
                 ceiling = hip_lib.mfma_ceiling()
@@ -356,6 +365,28 @@ VARIANT_SWEEP = {
     "weighted_var_backward": [("read", 0), ("split", 4), ("split", 8), ("split", 12)],
     "pearson_backward": [("read", 0), ("split", 2), ("split", 4), ("split", 8)],
 }
+
+
+def compact(entry):
+    """A suite entry as it goes into the printed line: time, rate, roofline
+    fractions, counted traffic over algorithmic bytes and the CPU baseline;
+    the variant sweep and the full ceiling and trial records go to the
+    detail file."""
+    roof = entry["roofline"]
+    ceiling = roof.get("ceiling") or {}
+    out = {"ms": entry["kernel_ms"], "value": entry["value"], "unit": entry["unit"],
+           "frac": roof["frac"], "frac_median": roof["frac_median"],
+           "ceiling_frac": ceiling.get("frac")}
+    if roof["bound"] == "hbm":
+        out["traffic_ratio"] = (round(roof["traffic"] / entry["bytes_per_call"], 3)
+                                if roof.get("traffic") else None)
+    else:
+        out["clock_MHz"] = entry.get("clock_MHz")
+        out["mfma_chain_TFLOPs"] = ceiling.get("TFLOPs")
+    cpu = entry.get("cpu_baseline")
+    if cpu:
+        out["cpu"] = {"value": cpu["value"], "unit": cpu["unit"], "cores": cpu["cores"]}
+    return out
 
 
 def main(argv=None):
@@ -417,10 +448,21 @@ def main(argv=None):
         "watchdog": head["watchdog"],
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
-        "variants_GBps": head.get("variants_GBps"),
-        "suite": suite,
+        "suite": {name: compact(entry) for name, entry in suite.items()},
     }
-    print(json.dumps(line), flush=True)
+    if args.detail:
+        detail = Path(args.detail)
+        if not detail.is_absolute():
+            detail = ROOT / detail
+        try:
+            detail.parent.mkdir(parents=True, exist_ok=True)
+            detail.write_text(json.dumps({"head": {args.workload: head}, "suite": suite},
+                                         indent=1) + "\n")
+            line["detail"] = str(detail.relative_to(ROOT)) if detail.is_relative_to(ROOT) \
+                else str(detail)
+        except OSError as err:
+            line["detail"] = f"not written: {err}"
+    print(json.dumps(line, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":

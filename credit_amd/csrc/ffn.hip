@@ -29,6 +29,7 @@
 // registers one K-step ahead, the A tile scaled by rstd and rounded to bf16
 // while it is staged into LDS).  The backward (credit_ffn_rmsnorm_gelu_bwd_bf16)
 // runs five GEMMs on the same two kernels with its own epilogues.
+#include <atomic>
 #include <initializer_list>
 #include <type_traits>
 #include <utility>
@@ -426,12 +427,29 @@ __device__ __forceinline__ bf16x4_t ds_read_tr16(const char* p) {
 // half-wave read 4 K-rows x 64 bytes, which the swizzle spreads over all
 // 64 banks.
 
+// Clock probe (credit_set_clock_probe): with a non-null `probe`, thread 0 of
+// every workgroup adds the shader cycles (s_memtime) and the 100 MHz
+// constant-clock ticks (s_memrealtime) between the workgroup's start and its
+// end to probe[0] and probe[1] (the start stamps subtracted as it starts, so
+// nothing stays live across the kernel); their ratio is the mean shader clock
+// the tiles ran at.
+__device__ __forceinline__ void clock_probe_add(uint64_t* probe, bool start) {
+  if (probe == nullptr || threadIdx.x != 0) return;
+  const uint64_t c = __builtin_amdgcn_s_memtime();
+  const uint64_t r = __builtin_amdgcn_s_memrealtime();
+  __hip_atomic_fetch_add(probe, start ? 0 - c : c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_add(probe + 1, start ? 0 - r : r, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int EPI, bool KN>
 __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     const uint16_t* __restrict__ A, const float* __restrict__ scale,
     const uint16_t* __restrict__ B, const uint16_t* __restrict__ R, uint16_t* __restrict__ C,
-    uint16_t* __restrict__ C2, float* __restrict__ Cf, int M, int N, int K) {
+    uint16_t* __restrict__ C2, float* __restrict__ Cf, int M, int N, int K,
+    uint64_t* __restrict__ probe) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
+  clock_probe_add(probe, true);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -676,6 +694,7 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
           }
           *reinterpret_cast<uint2*>(C2 + static_cast<size_t>(n) * M + mb) = uint2{t[0], t[1]};
         }
+    clock_probe_add(probe, false);
     return;
   } else {
   // Registers r and r + 1 (r even) are rows m and m + 1 of one column: both
@@ -730,6 +749,7 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
     }
   }
   }
+  clock_probe_add(probe, false);
 }
 
 // dst[c, r] = bf16(src[r, c] * scale[r]) (scale == nullptr: a plain copy
@@ -833,6 +853,9 @@ __global__ __launch_bounds__(256) void ffn_dx_kernel(const uint16_t* __restrict_
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// Sums the 256-tile GEMMs add their clock stamps to (credit_set_clock_probe).
+std::atomic<uint64_t*> g_clock_probe{nullptr};
+
 // The 256-tile kernels take 160 KiB of dynamic LDS; allow it once per
 // process (the attribute belongs to the kernel, not to a device).
 template <int EPI, bool KN>
@@ -870,8 +893,8 @@ int launch_gemm(const uint16_t* A, const float* scale, const uint16_t* B, const 
   if (big) {
     CREDIT_TRY(enable_big_lds<KN>());
     ffn_gemm256_kernel<EPI, KN><<<dim3(static_cast<unsigned>((M / kBig) * (N / kBig))),
-                                  dim3(kBigThreads), kBigLds, stream>>>(A, scale, B, R, C, C2,
-                                                                         Cf, M, N, K);
+                                  dim3(kBigThreads), kBigLds, stream>>>(
+        A, scale, B, R, C, C2, Cf, M, N, K, g_clock_probe.load(std::memory_order_relaxed));
   } else {
     ffn_gemm_kernel<EPI, KN><<<dim3(static_cast<unsigned>((M / kBM) * (N / kBN))),
                                dim3(kThreads), 0, stream>>>(A, scale, B, R, C, C2, Cf, M, N, K);
@@ -943,6 +966,12 @@ size_t ffn_bwd_workspace(int64_t rows, int64_t d, int64_t ffn_dim) {
 }  // namespace credit
 
 using namespace credit;
+
+extern "C" int credit_set_clock_probe(uint64_t* sums) {
+  if (sums != nullptr) CREDIT_TRY(check_aligned(sums, 8, "sums"));
+  g_clock_probe.store(sums, std::memory_order_relaxed);
+  return CREDIT_OK;
+}
 
 extern "C" int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t rows,
                                      int64_t cols, const credit_cfg* cfg) {

@@ -147,6 +147,7 @@ SIGNATURES: dict[str, list] = {
                                 ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                 ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],
     "credit_last_split_shape": [ctypes.POINTER(ctypes.c_int32)] * 4,
+    "credit_set_clock_probe": [_P],
 }
 _RESTYPES = {
     "credit_version": ctypes.c_char_p,
@@ -341,6 +342,22 @@ def last_split_shape() -> dict:
     check(load_library().credit_last_split_shape(*[ctypes.byref(v) for v in vals]),
           "credit_last_split_shape")
     return dict(zip(("threads", "lds_bytes", "per_cu", "dispensers"), (v.value for v in vals)))
+
+
+def gemm_clock_mhz(run, device=None) -> float:
+    """Mean shader clock (MHz) the FFN's 256-tile GEMM workgroups ran at
+    during run() (credit_set_clock_probe: each workgroup's s_memtime cycles
+    over its 100 MHz s_memrealtime ticks, start to end, summed)."""
+    sums = torch.zeros(2, dtype=torch.int64, device=device or "cuda")
+    torch.cuda.synchronize()
+    check(load_library().credit_set_clock_probe(sums.data_ptr()), "credit_set_clock_probe")
+    try:
+        run()
+        torch.cuda.synchronize()
+    finally:
+        check(load_library().credit_set_clock_probe(None), "credit_set_clock_probe")
+    cycles, ticks = (int(v) & 0xFFFFFFFFFFFFFFFF for v in sums.cpu().tolist())
+    return 100.0 * cycles / ticks if ticks else float("nan")
 
 
 def control_lds_bytes(shape: dict, lds_per_cu: int) -> int:

@@ -537,6 +537,15 @@ int credit_control_overhead(int64_t rows, int32_t split, int32_t barriers, int32
                             int32_t threads, int32_t warmup, int32_t iters, int32_t cooperative,
                             double* plain_ms, double* split_ms);
 
+/* Measurement aid, no counterpart in the reference: while `sums` (a device
+ * buffer of two uint64 the caller zeroes) is set, every workgroup of the
+ * FFN's 256-tile GEMM kernels adds its shader cycles (s_memtime) to sums[0]
+ * and its 100 MHz constant-clock ticks (s_memrealtime) to sums[1], start to
+ * end; 100 * sums[0] / sums[1] is the mean shader clock (MHz) the GEMM tiles
+ * ran at.  NULL switches it off (the default).  Process-wide; the GEMMs
+ * launched meanwhile on any stream add to the same sums. */
+int credit_set_clock_probe(uint64_t* sums);
+
 /* Shape of the last co-resident split launch this thread made: block size
  * (data lanes plus any communication wave), LDS per workgroup (static and
  * dynamic), workgroups resident per CU, and its ticket subsets.  What the

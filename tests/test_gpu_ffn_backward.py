@@ -28,8 +28,12 @@ EPS = 1.0e-6
 
 
 def close(got, exp, name):
+    """bf16 parity: rtol 1e-2 and atol 1e-2 for dx (O(1) per element, the
+    flat tolerance of every bf16 output); for the weight gradients, sums over
+    all rows whose magnitude spans orders, atol 1e-2 times the largest
+    expected element."""
     got = np.asarray(got, np.float64)
-    scale = np.abs(exp).max()
+    scale = 1.0 if name.startswith("dx") else np.abs(exp).max()
     excess = np.abs(got - exp) - (1e-2 * np.abs(exp) + 1e-2 * scale)
     assert np.all(excess <= 0), (f"{name}: max excess {excess.max():.3e} (scale {scale:.3e}) "
                                  f"at {np.unravel_index(excess.argmax(), excess.shape)}")
@@ -161,8 +165,9 @@ def torch_fp32_backward(x, w1, w2, dout, gpu):
 
 
 def close_gpu(got, exp, name):
-    """close() on device tensors: |got - exp| <= 1e-2 |exp| + 1e-2 max|exp|."""
-    scale = float(exp.abs().max())
+    """close() on device tensors: |got - exp| <= 1e-2 |exp| + 1e-2 (dx) or
+    + 1e-2 max|exp| (the weight gradients)."""
+    scale = 1.0 if name.startswith("dx") else float(exp.abs().max())
     excess = (got - exp).abs() - (1e-2 * exp.abs() + 1e-2 * scale)
     worst = int(excess.argmax())
     assert float(excess.max()) <= 0, (
