@@ -53,8 +53,10 @@ HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 # Workloads whose tensors are bf16 (fp32 accumulation); the rest compute in fp32.
 BF16_WORKLOADS = ("layernorm_fwd", "rmsnorm_fwd", "rmsnorm_bwd", "ffn", "ffn_baseline_layout",
-                  "ffn_backward", "ffn_backward_saved", "layernorm_backward_bf16")
-FFN_WORKLOADS = ("ffn", "ffn_baseline_layout", "ffn_backward", "ffn_backward_saved")
+                  "ffn_backward", "ffn_backward_saved", "ffn_backward_baseline_layout",
+                  "layernorm_backward_bf16")
+FFN_WORKLOADS = ("ffn", "ffn_baseline_layout", "ffn_backward", "ffn_backward_saved",
+                 "ffn_backward_baseline_layout")
 
 # Kernels one AUTO call launches at the BASELINE shape (names as rocprofv3
 # reports them) and the source file they are built from; the committed PMC
@@ -264,7 +266,7 @@ def cpu_baseline(name, cpu_inputs, spec, seconds):
 def spec_ffn_flops(rows, d, name="ffn"):
     from credit_amd.workloads import ffn_backward_flops, ffn_flops
 
-    return (ffn_backward_flops(rows, d) if name in ("ffn_backward", "ffn_backward_saved")
+    return (ffn_backward_flops(rows, d) if name.startswith("ffn_backward")
             else ffn_flops(rows, d))
 
 

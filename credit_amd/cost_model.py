@@ -31,6 +31,14 @@ L2-resident workspace.  The terms become:
 * ``l2_exchange_ms``   -- replaces dsmem_store_ms (:91-99): per wave of
   resident groups, one device-scope arrival and partial round trip per
   barrier, at the measured same-XCD atomic round trip.
+* ``hidden_sync_ms``   -- new: the part of control + exchange a pipelined
+  split kernel hides.  The group kernels publish a row's partial
+  ``split_pipeline_depth`` row-steps before they need its total, so per row
+  the exchange overlaps that many steps of streaming; the control overhead
+  is measured with the exchanges back to back (credit_control_overhead, at
+  the launch's own block size and LDS), so it is charged only beyond
+  depth x the compulsory stream time.  0 for the barrier-synchronised slice
+  kernels.
 
 ``estimate()`` keeps the reference's signature and result shape so the
 runner's summary logic (dsmem_eval/runner.py:444-620) carries over.
@@ -56,7 +64,7 @@ class WorkloadModelSpec(Protocol):
     barrier_count: int
 
 
-MODEL_VERSION = "cdna4-onchip-fill-exchange-v1"
+MODEL_VERSION = "cdna4-onchip-fill-exchange-v2"
 
 # Register staging budget of one 1024-lane workgroup: 64 VGPRs of data per
 # lane (the rest of the 512-entry file holds addresses and accumulators).
@@ -121,6 +129,7 @@ class ModelEstimate:
     l2_exchange_ms: float
     predicted_delta_ms: float
     predicted_profitable: bool
+    hidden_sync_ms: float = 0.0
 
     @property
     def saved_hbm_ms(self) -> float:
@@ -210,7 +219,10 @@ def estimate(
     lds_replay_ms = (waves * spilled * extra_passes / profile.lds_read_bytes_per_cycle_cu) * cycle_ms
 
     control = max(control_overhead_ms, 0.0)
-    delta = saved_reread_ms + fill_gain_ms - control - lds_replay_ms - l2_exchange_ms
+    depth = getattr(spec, "split_pipeline_depth", 0)
+    hidden_sync_ms = min(control + l2_exchange_ms, depth * remaining_ms)
+    delta = (saved_reread_ms + fill_gain_ms - (control + l2_exchange_ms - hidden_sync_ms)
+             - lds_replay_ms)
     return ModelEstimate(
         effective_bandwidth_gbps=effective_bandwidth_gbps,
         saved_reread_ms=saved_reread_ms,
@@ -220,6 +232,7 @@ def estimate(
         l2_exchange_ms=l2_exchange_ms,
         predicted_delta_ms=delta,
         predicted_profitable=delta > 0.0,
+        hidden_sync_ms=hidden_sync_ms,
     )
 
 

@@ -63,6 +63,7 @@ constexpr int kEpiGeluBwd = 3;
 constexpr int kEpiStore = 4;
 constexpr int kEpiStoreF32 = 5;
 constexpr int kEpiGeluSave = 6;
+constexpr int kEpiStoreT = 7;  // C^T [N, M] = bf16(acc): the output stored transposed
 
 // GELU with the tanh approximation, z = sqrt(2/pi) (v + 0.044715 v^3):
 // 0.5 (1 + tanh z) = sigmoid(2z), so GELU(v) = v / (1 + e') with
@@ -133,7 +134,9 @@ __device__ __forceinline__ void epilogue(float acc, float s, float rv, int m, in
   } else if (EPI == kEpiGeluBwd) {
     const uint16_t v = f32_to_bf16(acc * gelu_tanh_grad(rv));
     C[idx] = v;
-    C2[tdx] = v;
+    if (C2 != nullptr) C2[tdx] = v;
+  } else if (EPI == kEpiStoreT) {
+    C[tdx] = f32_to_bf16(acc);
   } else if (EPI == kEpiStore) {
     C[idx] = f32_to_bf16(acc);
   } else {
@@ -660,9 +663,11 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
 
   // Epilogue.  Accumulator register r of lane l holds row
   // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of its 32 x 32 tile.
-  if constexpr (EPI == kEpiUH || EPI == kEpiGeluBwd) {
-    // Also stored transposed: registers 4q..4q+3 are four consecutive rows
-    // of one column, so each lane writes them as one 8-byte run of C2.
+  if constexpr (EPI == kEpiUH || EPI == kEpiGeluBwd || EPI == kEpiStoreT) {
+    // Also (kEpiStoreT: only) stored transposed: registers 4q..4q+3 are four
+    // consecutive rows of one column, so each lane writes them as one 8-byte
+    // run of C2 (kEpiStoreT: of C).  kEpiGeluBwd with C2 == nullptr skips
+    // the transposed copy.
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -682,17 +687,21 @@ __global__ __launch_bounds__(kBigThreads) void ffn_gemm256_kernel(
             if (EPI == kEpiUH) {
               c = acc[i][j][4 * q + e] * scale[m];
               ct = gelu_tanh(c);
-            } else {
+            } else if (EPI == kEpiGeluBwd) {
               c = ct = acc[i][j][4 * q + e] * gelu_tanh_grad(static_cast<float>(rq[e]));
+            } else {
+              c = ct = acc[i][j][4 * q + e];
             }
-            C[idx] = f32_to_bf16(c);
+            if (EPI != kEpiStoreT) C[idx] = f32_to_bf16(c);
             const uint32_t b = f32_to_bf16(ct);
             if (e & 1)
               t[e >> 1] |= b << 16;
             else
               t[e >> 1] = b;
           }
-          *reinterpret_cast<uint2*>(C2 + static_cast<size_t>(n) * M + mb) = uint2{t[0], t[1]};
+          uint16_t* dst = EPI == kEpiStoreT ? C : C2;
+          if (EPI != kEpiGeluBwd || C2 != nullptr)
+            *reinterpret_cast<uint2*>(dst + static_cast<size_t>(n) * M + mb) = uint2{t[0], t[1]};
         }
     clock_probe_add(probe, false);
     return;
@@ -870,7 +879,8 @@ int enable_big_lds() {
          {allow_big_lds<kEpiGelu, KN>(), allow_big_lds<kEpiGeluSave, KN>(),
           allow_big_lds<kEpiResidual, KN>(),
           allow_big_lds<kEpiUH, KN>(), allow_big_lds<kEpiGeluBwd, KN>(),
-          allow_big_lds<kEpiStore, KN>(), allow_big_lds<kEpiStoreF32, KN>()})
+          allow_big_lds<kEpiStore, KN>(), allow_big_lds<kEpiStoreF32, KN>(),
+          allow_big_lds<kEpiStoreT, KN>()})
       if (e != hipSuccess) return hip_failure(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
     return static_cast<int>(CREDIT_OK);
   }();
@@ -1028,11 +1038,13 @@ extern "C" int credit_ffn_rmsnorm_gelu_bf16(const uint16_t* x, const uint16_t* w
   return ffn_forward<false>(x, w1, w2, out, rows, d, f, eps, cfg);
 }
 
-extern "C" int credit_ffn_rmsnorm_gelu_fwd_train_bf16(const uint16_t* x, const uint16_t* w1,
-                                                      const uint16_t* w2, uint16_t* out,
-                                                      float* rstd, uint16_t* u, uint16_t* h,
-                                                      int64_t rows, int64_t d, int64_t f,
-                                                      float eps, const credit_cfg* cfg) {
+namespace credit {
+namespace {
+
+template <bool KN>
+int ffn_train_forward(const uint16_t* x, const uint16_t* w1, const uint16_t* w2, uint16_t* out,
+                      float* rstd, uint16_t* u, uint16_t* h, int64_t rows, int64_t d, int64_t f,
+                      float eps, const credit_cfg* cfg) {
   CREDIT_TRY(check_row_ptr(x, "x", rows));
   CREDIT_TRY(check_ptr(w1, "w1"));
   CREDIT_TRY(check_ptr(w2, "w2"));
@@ -1054,10 +1066,29 @@ extern "C" int credit_ffn_rmsnorm_gelu_fwd_train_bf16(const uint16_t* x, const u
   const int M = static_cast<int>(rows), D = static_cast<int>(d), F = static_cast<int>(f);
   ffn_rstd_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, D, eps);
   CREDIT_TRY(check_launch("ffn_rstd_kernel"));
-  CREDIT_TRY(launch_gemm<kEpiGeluSave>(x, rstd, w1, nullptr, h, u, nullptr, M, F, D, stream,
-                                       "ffn gemm1 (gelu, saving u and h)"));
-  return launch_gemm<kEpiResidual>(h, nullptr, w2, x, out, nullptr, nullptr, M, D, F, stream,
-                                   "ffn gemm2 (residual)");
+  CREDIT_TRY((launch_gemm<kEpiGeluSave, KN>(x, rstd, w1, nullptr, h, u, nullptr, M, F, D, stream,
+                                            "ffn gemm1 (gelu, saving u and h)")));
+  return launch_gemm<kEpiResidual, KN>(h, nullptr, w2, x, out, nullptr, nullptr, M, D, F, stream,
+                                       "ffn gemm2 (residual)");
+}
+
+}  // namespace
+}  // namespace credit
+
+extern "C" int credit_ffn_rmsnorm_gelu_fwd_train_bf16(const uint16_t* x, const uint16_t* w1,
+                                                      const uint16_t* w2, uint16_t* out,
+                                                      float* rstd, uint16_t* u, uint16_t* h,
+                                                      int64_t rows, int64_t d, int64_t f,
+                                                      float eps, const credit_cfg* cfg) {
+  return ffn_train_forward<false>(x, w1, w2, out, rstd, u, h, rows, d, f, eps, cfg);
+}
+
+extern "C" int credit_ffn_rmsnorm_gelu_fwd_train_kn_bf16(const uint16_t* x, const uint16_t* w1,
+                                                         const uint16_t* w2, uint16_t* out,
+                                                         float* rstd, uint16_t* u, uint16_t* h,
+                                                         int64_t rows, int64_t d, int64_t f,
+                                                         float eps, const credit_cfg* cfg) {
+  return ffn_train_forward<true>(x, w1, w2, out, rstd, u, h, rows, d, f, eps, cfg);
 }
 
 extern "C" int credit_ffn_rmsnorm_gelu_kn_bf16(const uint16_t* x, const uint16_t* w1,
@@ -1072,14 +1103,21 @@ namespace {
 
 // The backward.  With saved == nullptr it recomputes rstd, u and h^T from x
 // (one extra GEMM); with the training forward's rstd, u and h it skips that
-// GEMM and reads h as the dW2 GEMM's [K, N] B operand.  Both give the same
-// bits: the saved u and h are the recomputed ones.
+// GEMM.  Both give the same bits: the saved u and h are the recomputed ones.
+// KN false takes the nn.Linear weights (w1 [f, d], w2 [d, f]) and returns
+// dW1 [f, d], dW2 [d, f]; KN true the [in, out] weights (w1 [d, f], w2
+// [f, d]) and returns dW1 [d, f], dW2 [f, d].  Every GEMM reads the weights,
+// dout and the activations in place, as A (K contiguous) or as B in either
+// layout; the [in, out] form swaps the operands of the weight-gradient GEMMs
+// instead, so it needs neither dout^T nor du^T (only the saved form's dW2,
+// whose h^T no GEMM produced, takes dout^T and a transposed store).
 struct FfnSaved {
   const float* rstd;
   const uint16_t* u;
   const uint16_t* h;
 };
 
+template <bool KN>
 int ffn_backward(const uint16_t* x, const uint16_t* w1, const uint16_t* w2,
                  const uint16_t* dout, const FfnSaved* saved, uint16_t* dx, uint16_t* dw1,
                  uint16_t* dw2, int64_t rows, int64_t d, int64_t f, float eps,
@@ -1139,30 +1177,46 @@ int ffn_backward(const uint16_t* x, const uint16_t* w1, const uint16_t* w2,
     CREDIT_TRY(check_launch("ffn_rstd_kernel"));
   }
   // The A operands of the weight gradients in the K-contiguous layout A
-  // takes (the weights themselves are read as [K, N] B operands).
-  CREDIT_TRY(launch_transpose(dout, doutt, M, D, nullptr, stream));
-  CREDIT_TRY(launch_transpose(x, at, M, D, rstd, stream));         // a^T = bf16(x rstd)^T
-  // u = (x W1^T) rstd, h^T = GELU(u)^T (recomputed unless saved).
+  // takes: a^T = bf16(x rstd)^T always, dout^T where no other form reads it.
+  if (!KN || saved != nullptr) CREDIT_TRY(launch_transpose(dout, doutt, M, D, nullptr, stream));
+  CREDIT_TRY(launch_transpose(x, at, M, D, rstd, stream));
+  // u = (x W1^T) rstd (x W1 for [in, out]), h^T = GELU(u)^T, unless saved.
   if (saved == nullptr)
-    CREDIT_TRY(launch_gemm<kEpiUH>(x, rstd, w1, nullptr, reinterpret_cast<uint16_t*>(b + L.u), ht,
-                                   nullptr, M, F, D, stream, "ffn bwd gemm u"));
-  // du = (dout W2) * GELU'(u), and du^T; W2 [d, f] is B as [K, N].
-  CREDIT_TRY((launch_gemm<kEpiGeluBwd, true>(dout, nullptr, w2, u, du, dut, nullptr, M, F, D,
-                                            stream, "ffn bwd gemm du")));
-  // dW2 [d, f] = dout^T h: h^T [f, M] as the B operand, or the saved h
-  // [M, f] read as [K, N].
-  if (saved == nullptr)
-    CREDIT_TRY(launch_gemm<kEpiStore>(doutt, nullptr, ht, nullptr, dw2, nullptr, nullptr, D, F, M,
-                                      stream, "ffn bwd gemm dw2"));
-  else
-    CREDIT_TRY((launch_gemm<kEpiStore, true>(doutt, nullptr, saved->h, nullptr, dw2, nullptr,
-                                             nullptr, D, F, M, stream, "ffn bwd gemm dw2")));
-  // dW1 [f, d] = du^T a.
-  CREDIT_TRY(launch_gemm<kEpiStore>(dut, nullptr, at, nullptr, dw1, nullptr, nullptr, F, D, M,
-                                    stream, "ffn bwd gemm dw1"));
-  // da [M, d] = du W1 (fp32; W1 [f, d] is B as [K, N]), then dx = dout +
+    CREDIT_TRY((launch_gemm<kEpiUH, KN>(x, rstd, w1, nullptr, reinterpret_cast<uint16_t*>(b + L.u),
+                                        ht, nullptr, M, F, D, stream, "ffn bwd gemm u")));
+  // du = (dout W2) * GELU'(u) (dout W2^T for [in, out]), with du^T for the
+  // nn.Linear dW1 GEMM.
+  CREDIT_TRY((launch_gemm<kEpiGeluBwd, !KN>(dout, nullptr, w2, u, du, KN ? nullptr : dut,
+                                            nullptr, M, F, D, stream, "ffn bwd gemm du")));
+  if constexpr (!KN) {
+    // dW2 [d, f] = dout^T h: h^T [f, M] as the B operand, or the saved h
+    // [M, f] read as [K, N].
+    if (saved == nullptr)
+      CREDIT_TRY(launch_gemm<kEpiStore>(doutt, nullptr, ht, nullptr, dw2, nullptr, nullptr, D, F,
+                                        M, stream, "ffn bwd gemm dw2"));
+    else
+      CREDIT_TRY((launch_gemm<kEpiStore, true>(doutt, nullptr, saved->h, nullptr, dw2, nullptr,
+                                               nullptr, D, F, M, stream, "ffn bwd gemm dw2")));
+    // dW1 [f, d] = du^T a.
+    CREDIT_TRY(launch_gemm<kEpiStore>(dut, nullptr, at, nullptr, dw1, nullptr, nullptr, F, D, M,
+                                      stream, "ffn bwd gemm dw1"));
+  } else {
+    // dW2 [f, d] = h^T dout: h^T as A and dout [M, d] read as [K, N]; from
+    // the saved h, (dout^T h)^T with h read as [K, N] and the output stored
+    // transposed.
+    if (saved == nullptr)
+      CREDIT_TRY((launch_gemm<kEpiStore, true>(ht, nullptr, dout, nullptr, dw2, nullptr, nullptr,
+                                               F, D, M, stream, "ffn bwd gemm dw2")));
+    else
+      CREDIT_TRY((launch_gemm<kEpiStoreT, true>(doutt, nullptr, saved->h, nullptr, dw2, nullptr,
+                                                nullptr, D, F, M, stream, "ffn bwd gemm dw2")));
+    // dW1 [d, f] = a^T du: du [M, f] read as [K, N].
+    CREDIT_TRY((launch_gemm<kEpiStore, true>(at, nullptr, du, nullptr, dw1, nullptr, nullptr, D, F,
+                                             M, stream, "ffn bwd gemm dw1")));
+  }
+  // da [M, d] = du W1 (du W1^T for [in, out]), fp32, then dx = dout +
   // RMSNorm backward of da.
-  CREDIT_TRY((launch_gemm<kEpiStoreF32, true>(du, nullptr, w1, nullptr, nullptr, nullptr, da, M, D,
+  CREDIT_TRY((launch_gemm<kEpiStoreF32, !KN>(du, nullptr, w1, nullptr, nullptr, nullptr, da, M, D,
                                              F, stream, "ffn bwd gemm da")));
   ffn_dx_kernel<<<dim3(M), dim3(256), 0, stream>>>(x, rstd, da, dout, dx, D);
   return check_launch("ffn_dx_kernel");
@@ -1176,7 +1230,7 @@ extern "C" int credit_ffn_rmsnorm_gelu_bwd_bf16(const uint16_t* x, const uint16_
                                                 uint16_t* dx, uint16_t* dw1, uint16_t* dw2,
                                                 int64_t rows, int64_t d, int64_t f, float eps,
                                                 const credit_cfg* cfg) {
-  return ffn_backward(x, w1, w2, dout, nullptr, dx, dw1, dw2, rows, d, f, eps, cfg);
+  return ffn_backward<false>(x, w1, w2, dout, nullptr, dx, dw1, dw2, rows, d, f, eps, cfg);
 }
 
 extern "C" int credit_ffn_rmsnorm_gelu_bwd_saved_bf16(
@@ -1184,5 +1238,21 @@ extern "C" int credit_ffn_rmsnorm_gelu_bwd_saved_bf16(
     const float* rstd, const uint16_t* u, const uint16_t* h, uint16_t* dx, uint16_t* dw1,
     uint16_t* dw2, int64_t rows, int64_t d, int64_t f, const credit_cfg* cfg) {
   const FfnSaved saved{rstd, u, h};
-  return ffn_backward(x, w1, w2, dout, &saved, dx, dw1, dw2, rows, d, f, 0.0f, cfg);
+  return ffn_backward<false>(x, w1, w2, dout, &saved, dx, dw1, dw2, rows, d, f, 0.0f, cfg);
+}
+
+extern "C" int credit_ffn_rmsnorm_gelu_bwd_kn_bf16(const uint16_t* x, const uint16_t* w1,
+                                                   const uint16_t* w2, const uint16_t* dout,
+                                                   uint16_t* dx, uint16_t* dw1, uint16_t* dw2,
+                                                   int64_t rows, int64_t d, int64_t f, float eps,
+                                                   const credit_cfg* cfg) {
+  return ffn_backward<true>(x, w1, w2, dout, nullptr, dx, dw1, dw2, rows, d, f, eps, cfg);
+}
+
+extern "C" int credit_ffn_rmsnorm_gelu_bwd_saved_kn_bf16(
+    const uint16_t* x, const uint16_t* w1, const uint16_t* w2, const uint16_t* dout,
+    const float* rstd, const uint16_t* u, const uint16_t* h, uint16_t* dx, uint16_t* dw1,
+    uint16_t* dw2, int64_t rows, int64_t d, int64_t f, const credit_cfg* cfg) {
+  const FfnSaved saved{rstd, u, h};
+  return ffn_backward<true>(x, w1, w2, dout, &saved, dx, dw1, dw2, rows, d, f, 0.0f, cfg);
 }

@@ -223,6 +223,11 @@ extern "C" int credit_row_sum_max_f32(const float* x, float* sum, float* max,
   chunk = (chunk + 3) & ~3;
   split = static_cast<int>((cols + chunk - 1) / chunk);
   const SplitLayout l = split_layout(rows, split);
+  // The grid is not co-resident (no member waits), but its shape is what
+  // credit_last_split_shape reports for this call: plan it the same way.
+  int64_t resident_groups = 0;
+  CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(row_sum_max_split_kernel<kRowThreads>),
+                               kRowThreads, 0, split, &resident_groups));
   char* ws = nullptr;
   CREDIT_TRY(acquire_workspace(cfg, l.bytes, &ws));
   char* scratch = ws_scratch(ws);

@@ -135,6 +135,12 @@ SIGNATURES: dict[str, list] = {
                                                _CFG],
     "credit_ffn_rmsnorm_gelu_bwd_saved_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                                                _I64, _CFG],
+    "credit_ffn_rmsnorm_gelu_fwd_train_kn_bf16": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
+                                                  _F, _CFG],
+    "credit_ffn_rmsnorm_gelu_bwd_kn_bf16": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F,
+                                            _CFG],
+    "credit_ffn_rmsnorm_gelu_bwd_saved_kn_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                                                  _I64, _I64, _CFG],
     "credit_ffn_bwd_workspace_bytes": [_I64, _I64, _I64],
     "credit_layernorm_bwd_f32": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
     "credit_layernorm_bwd_bf16": [_P, _P, _P, _P, _I64, _I64, _F, _CFG],
@@ -620,77 +626,85 @@ def transpose(src: torch.Tensor, dst: torch.Tensor, cfg: CreditCfg | None = None
     )
 
 
+def _ffn_dims(x, w1, w2, what, kn):
+    """(rows, d, f) of an FFN call: w1 [f, d], w2 [d, f] (nn.Linear), or with
+    kn w1 [d, f], w2 [f, d] ([in, out])."""
+    rows, d = _rows_cols(x)
+    f = int(w1.shape[1] if kn else w1.shape[0])
+    want1, want2 = ((d, f), (f, d)) if kn else ((f, d), (d, f))
+    if tuple(w1.shape) != want1 or tuple(w2.shape) != want2:
+        raise ValueError(f"{what}: w1 must be {list(want1)} and w2 {list(want2)}; got "
+                         f"{tuple(w1.shape)}, {tuple(w2.shape)}")
+    return rows, d, f
+
+
 def ffn_backward(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, dout: torch.Tensor,
                  dx: torch.Tensor, dw1: torch.Tensor, dw2: torch.Tensor, eps: float,
-                 cfg: CreditCfg) -> None:
-    """Gradients of ffn(): dx [rows, d], dw1 [f, d], dw2 [d, f] (the
-    weights' own layouts), all bf16; w1 [f, d], w2 [d, f] as the forward."""
-    rows, d = _rows_cols(x)
-    f = int(w1.shape[0])
-    if tuple(w1.shape) != (f, d) or tuple(w2.shape) != (d, f):
-        raise ValueError(f"ffn_backward: w1 must be [f, d] and w2 [d, f]; got {tuple(w1.shape)}, "
-                         f"{tuple(w2.shape)} for d={d}")
+                 cfg: CreditCfg, kn: bool = False) -> None:
+    """Gradients of ffn(): dx [rows, d] and dw1, dw2 in the weights' own
+    layouts, all bf16.  w1 [f, d], w2 [d, f] as the forward, or with kn the
+    [in, out] weights w1 [d, f], w2 [f, d]."""
+    rows, d, f = _ffn_dims(x, w1, w2, "ffn_backward", kn)
     for name, t, shape in (("dout", dout, (rows, d)), ("dx", dx, (rows, d)),
-                           ("dw1", dw1, (f, d)), ("dw2", dw2, (d, f))):
+                           ("dw1", dw1, tuple(w1.shape)), ("dw2", dw2, tuple(w2.shape))):
         if tuple(t.shape) != shape:
             raise ValueError(f"ffn_backward: {name} must be {shape}, got {tuple(t.shape)}")
     bf = torch.bfloat16
+    fn = "credit_ffn_rmsnorm_gelu_bwd_kn_bf16" if kn else "credit_ffn_rmsnorm_gelu_bwd_bf16"
     check(
-        load_library().credit_ffn_rmsnorm_gelu_bwd_bf16(
+        getattr(load_library(), fn)(
             _ptr(x, "x", bf), _ptr(w1, "w1", bf), _ptr(w2, "w2", bf), _ptr(dout, "dout", bf),
             _ptr(dx, "dx", bf), _ptr(dw1, "dw1", bf), _ptr(dw2, "dw2", bf), rows, d, f,
             float(eps), ctypes.byref(cfg)),
-        "credit_ffn_rmsnorm_gelu_bwd_bf16",
+        fn,
     )
-
-
-def _ffn_linear_dims(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, who: str):
-    rows, d = _rows_cols(x)
-    f = int(w1.shape[0])
-    if tuple(w1.shape) != (f, d) or tuple(w2.shape) != (d, f):
-        raise ValueError(f"{who}: w1 must be [f, d] and w2 [d, f]; got {tuple(w1.shape)}, "
-                         f"{tuple(w2.shape)} for d={d}")
-    return rows, d, f
 
 
 def ffn_train_forward(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, out: torch.Tensor,
                       rstd: torch.Tensor, u: torch.Tensor, h: torch.Tensor, eps: float,
-                      cfg: CreditCfg) -> None:
-    """ffn() (nn.Linear weights) that also writes what its backward needs:
-    rstd [rows] fp32, u [rows, f] and h [rows, f] bf16."""
-    rows, d, f = _ffn_linear_dims(x, w1, w2, "ffn_train_forward")
+                      cfg: CreditCfg, kn: bool = False) -> None:
+    """ffn() (nn.Linear weights, or with kn the [in, out] ones) that also
+    writes what its backward needs: rstd [rows] fp32, u [rows, f] and h
+    [rows, f] bf16."""
+    rows, d, f = _ffn_dims(x, w1, w2, "ffn_train_forward", kn)
     for name, t, shape in (("out", out, (rows, d)), ("rstd", rstd, (rows,)),
                            ("u", u, (rows, f)), ("h", h, (rows, f))):
         if tuple(t.shape) != shape:
             raise ValueError(f"ffn_train_forward: {name} must be {shape}, got {tuple(t.shape)}")
     bf = torch.bfloat16
+    fn = ("credit_ffn_rmsnorm_gelu_fwd_train_kn_bf16" if kn
+          else "credit_ffn_rmsnorm_gelu_fwd_train_bf16")
     check(
-        load_library().credit_ffn_rmsnorm_gelu_fwd_train_bf16(
+        getattr(load_library(), fn)(
             _ptr(x, "x", bf), _ptr(w1, "w1", bf), _ptr(w2, "w2", bf), _ptr(out, "out", bf),
             _ptr(rstd, "rstd", torch.float32), _ptr(u, "u", bf), _ptr(h, "h", bf), rows, d, f,
             float(eps), ctypes.byref(cfg)),
-        "credit_ffn_rmsnorm_gelu_fwd_train_bf16",
+        fn,
     )
 
 
 def ffn_backward_saved(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, dout: torch.Tensor,
                        rstd: torch.Tensor, u: torch.Tensor, h: torch.Tensor, dx: torch.Tensor,
-                       dw1: torch.Tensor, dw2: torch.Tensor, cfg: CreditCfg) -> None:
-    """ffn_backward() from the saved rstd, u and h of ffn_train_forward()."""
-    rows, d, f = _ffn_linear_dims(x, w1, w2, "ffn_backward_saved")
+                       dw1: torch.Tensor, dw2: torch.Tensor, cfg: CreditCfg,
+                       kn: bool = False) -> None:
+    """ffn_backward() from the saved rstd, u and h of ffn_train_forward()
+    (the same weight layout, kn)."""
+    rows, d, f = _ffn_dims(x, w1, w2, "ffn_backward_saved", kn)
     for name, t, shape in (("dout", dout, (rows, d)), ("rstd", rstd, (rows,)),
                            ("u", u, (rows, f)), ("h", h, (rows, f)), ("dx", dx, (rows, d)),
-                           ("dw1", dw1, (f, d)), ("dw2", dw2, (d, f))):
+                           ("dw1", dw1, tuple(w1.shape)), ("dw2", dw2, tuple(w2.shape))):
         if tuple(t.shape) != shape:
             raise ValueError(f"ffn_backward_saved: {name} must be {shape}, got {tuple(t.shape)}")
     bf = torch.bfloat16
+    fn = ("credit_ffn_rmsnorm_gelu_bwd_saved_kn_bf16" if kn
+          else "credit_ffn_rmsnorm_gelu_bwd_saved_bf16")
     check(
-        load_library().credit_ffn_rmsnorm_gelu_bwd_saved_bf16(
+        getattr(load_library(), fn)(
             _ptr(x, "x", bf), _ptr(w1, "w1", bf), _ptr(w2, "w2", bf), _ptr(dout, "dout", bf),
             _ptr(rstd, "rstd", torch.float32), _ptr(u, "u", bf), _ptr(h, "h", bf),
             _ptr(dx, "dx", bf), _ptr(dw1, "dw1", bf), _ptr(dw2, "dw2", bf), rows, d, f,
             ctypes.byref(cfg)),
-        "credit_ffn_rmsnorm_gelu_bwd_saved_bf16",
+        fn,
     )
 
 
@@ -821,6 +835,16 @@ def launch_ffn_backward(inputs, outputs, config: LaunchConfig = LaunchConfig()) 
     ffn_backward(x, w1, w2, dout, dx, dw1, dw2, FFN_EPS, make_cfg(config.variant, config.split))
 
 
+def launch_ffn_backward_baseline_layout(inputs, outputs,
+                                        config: LaunchConfig = LaunchConfig()) -> None:
+    """inputs: (x, w1 [d, f], w2 [f, d], dout) in the BASELINE's [in, out]
+    layout; outputs: (dx, dw1 [d, f], dw2 [f, d])."""
+    x, w1, w2, dout = inputs
+    dx, dw1, dw2 = outputs
+    ffn_backward(x, w1, w2, dout, dx, dw1, dw2, FFN_EPS, make_cfg(config.variant, config.split),
+                 kn=True)
+
+
 def launch_ffn_backward_saved(inputs, outputs, config: LaunchConfig = LaunchConfig()) -> None:
     """inputs: (x, w1 [f, d], w2 [d, f], dout, rstd, u, h) -- the last three
     from ffn_train_forward; outputs: (dx, dw1, dw2)."""
@@ -840,6 +864,7 @@ HIP_LAUNCHERS: dict[str, Callable[..., None]] = {
     "ffn": launch_ffn,
     "ffn_baseline_layout": launch_ffn_baseline_layout,
     "ffn_backward": launch_ffn_backward,
+    "ffn_backward_baseline_layout": launch_ffn_backward_baseline_layout,
     "ffn_backward_saved": launch_ffn_backward_saved,
     "layernorm_backward": launch_layernorm_backward,
     "layernorm_backward_bf16": launch_layernorm_backward,
@@ -965,7 +990,7 @@ def allocate_outputs(name: str, inputs: tuple[torch.Tensor, ...]) -> tuple[torch
         return torch.empty_like(x), torch.empty(rows, **f32), torch.empty(rows, **f32)
     if name == "rowwise_quant":
         return torch.empty(x.shape, device=x.device, dtype=torch.int8), torch.empty(rows, **f32)
-    if name in ("ffn_backward", "ffn_backward_saved"):
+    if name in ("ffn_backward", "ffn_backward_saved", "ffn_backward_baseline_layout"):
         w1 = inputs[1]
         return torch.empty_like(x), torch.empty_like(w1), torch.empty_like(inputs[2])
     if name in ("lars_momentum", "pearson_backward"):

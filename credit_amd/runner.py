@@ -68,7 +68,7 @@ SWEEP_WORKLOADS = (
     "pearson_backward",
 )
 DEFAULT_N_VALUES = (4096, 8192, 16384, 32768, 65536, 131072, 262144)
-DEFAULT_SPLITS = (2, 4, 8, 16)
+DEFAULT_SPLITS = (2, 4, 8, 16, 32)
 # Rows per sweep point: as many as make one input tensor this large, so the
 # rotating buffer sets (3 x inputs + outputs) exceed the 256 MB MALL and
 # every point streams from HBM.

@@ -58,6 +58,13 @@ class WorkloadSpec:
     # mix of the stream ceiling the kernel's rate is compared with.  (0, 0)
     # for compute-bound work.
     stream_mix: tuple[int, int] = (0, 0)
+    # Row-steps by which this build's SPLIT kernel publishes a row's partial
+    # ahead of waiting for its total: 2 for the group pipelines (RMSNorm
+    # backward, softmax forward and backward: data waves publish row i+2 and
+    # finish row i while a communication wave polls), 0 for the
+    # barrier-synchronised slice kernels.  The cost model hides that much of
+    # the exchange behind the stream.
+    split_pipeline_depth: int = 0
 
     @property
     def barrier_count(self) -> int:
@@ -263,6 +270,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=4,
         reductions_per_stage=(1,),
         staged_max_cols=8192,
+        split_pipeline_depth=2,
         stream_mix=(2, 1),
     ),
     # C3's forward and backward in one call (credit_rmsnorm_fwd_bwd_bf16):
@@ -294,6 +302,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=4,
         reductions_per_stage=(2,),
         staged_max_cols=65536,
+        split_pipeline_depth=2,
         stream_mix=(1, 1),
     ),
     "softmax_bwd": WorkloadSpec(
@@ -311,6 +320,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=8,
         reductions_per_stage=(1,),
         staged_max_cols=32768,
+        split_pipeline_depth=2,
         stream_mix=(2, 1),
     ),
     "ffn": WorkloadSpec(
@@ -341,6 +351,20 @@ WORKLOADS: dict[str, WorkloadSpec] = {
     "ffn_backward": WorkloadSpec(
         name="ffn_backward",
         label="Norm-fused FFN backward (bf16 MFMA)",
+        category="gemm",
+        rows=4096,
+        cols=8192,
+        input_factory=make_ffn_backward_inputs,
+        output_names=("dx", "dw1", "dw2"),
+        algorithmic_bytes=lambda r, c: 2 * (3 * r * c + 4 * c * 28672),
+        tolerances=(BF16_TOL, BF16_TOL, BF16_TOL),
+    ),
+    # The same gradients for the BASELINE's own [in, out] weights (W1 [d, f],
+    # W2 [f, d]), read as they are; dW1 [d, f] and dW2 [f, d] come back in
+    # that layout.
+    "ffn_backward_baseline_layout": WorkloadSpec(
+        name="ffn_backward_baseline_layout",
+        label="Norm-fused FFN backward, [in, out] weights (bf16 MFMA)",
         category="gemm",
         rows=4096,
         cols=8192,

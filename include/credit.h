@@ -393,6 +393,15 @@ int credit_ffn_rmsnorm_gelu_fwd_train_bf16(const uint16_t* x, const uint16_t* w1
                                            const uint16_t* w2, uint16_t* out, float* rstd,
                                            uint16_t* u, uint16_t* h, int64_t rows, int64_t d,
                                            int64_t f, float eps, const credit_cfg* cfg);
+/* The same training forward on the [in, out] weights (w1 [d, f], w2 [f, d]),
+ * as credit_ffn_rmsnorm_gelu_kn_bf16 takes them: out, rstd, u and h
+ * bit-identical to the nn.Linear form on transposed weights.  Feeds
+ * credit_ffn_rmsnorm_gelu_bwd_saved_kn_bf16.  No counterpart in the
+ * reference. */
+int credit_ffn_rmsnorm_gelu_fwd_train_kn_bf16(const uint16_t* x, const uint16_t* w1,
+                                              const uint16_t* w2, uint16_t* out, float* rstd,
+                                              uint16_t* u, uint16_t* h, int64_t rows, int64_t d,
+                                              int64_t f, float eps, const credit_cfg* cfg);
 
 /* ----------------------------------- FFN backward (next row of C5) -------
  * The gradients of out = x + GELU_tanh(RMSNorm(x) @ W1^T) @ W2^T (unit
@@ -427,6 +436,25 @@ int credit_ffn_rmsnorm_gelu_bwd_saved_bf16(const uint16_t* x, const uint16_t* w1
                                            const uint16_t* h, uint16_t* dx, uint16_t* dw1,
                                            uint16_t* dw2, int64_t rows, int64_t d, int64_t f,
                                            const credit_cfg* cfg);
+/* Both backward forms on the [in, out] weights (w1 [d, f], w2 [f, d], BASELINE
+ * C5's own layout), returning the gradients in that layout too: dw1 [d, f],
+ * dw2 [f, d].  The weights, dout and the activations are read in place; the
+ * weight-gradient GEMMs take their operands the other way round (dw1 = a^T
+ * du with du read as [K, N], dw2 = h^T dout with dout read as [K, N]), so
+ * neither dout^T nor du^T is formed (the saved form's dw2, from h [rows, f],
+ * is (dout^T h)^T stored transposed).  The gradients are bit-identical to the
+ * nn.Linear entry points' on transposed weights, transposed.  Same shape,
+ * alignment and workspace rules.  No counterpart in the reference. */
+int credit_ffn_rmsnorm_gelu_bwd_kn_bf16(const uint16_t* x, const uint16_t* w1,
+                                        const uint16_t* w2, const uint16_t* dout, uint16_t* dx,
+                                        uint16_t* dw1, uint16_t* dw2, int64_t rows, int64_t d,
+                                        int64_t f, float eps, const credit_cfg* cfg);
+int credit_ffn_rmsnorm_gelu_bwd_saved_kn_bf16(const uint16_t* x, const uint16_t* w1,
+                                              const uint16_t* w2, const uint16_t* dout,
+                                              const float* rstd, const uint16_t* u,
+                                              const uint16_t* h, uint16_t* dx, uint16_t* dw1,
+                                              uint16_t* dw2, int64_t rows, int64_t d, int64_t f,
+                                              const credit_cfg* cfg);
 /* Workspace bytes the FFN backward (either form) needs at (rows, d, f); 0
  * for an empty shape.  Plumbing of this ABI, no counterpart in the
  * reference. */

@@ -155,6 +155,7 @@ FUNCTIONS = {
     "ffn": ffn,
     "ffn_baseline_layout": ffn,
     "ffn_backward": ffn_backward,
+    "ffn_backward_baseline_layout": ffn_backward,
     # Builds the graph and returns the backward-only call (bench.py times
     # that call).
     "ffn_backward_saved": ffn_backward_saved,

@@ -307,3 +307,61 @@ def test_ffn_backward_saved_rejects_bad_shapes(gpu):
             u.data_ptr(), hv.data_ptr(), dx.data_ptr(), dw1.data_ptr(), dw2.data_ptr(), 128, 128,
             256, ctypes.byref(hip_lib.make_cfg()))
         hip_lib.check(st, "credit_ffn_rmsnorm_gelu_bwd_saved_bf16")
+
+
+# ------------------------------------------------ [in, out] weight layout --
+
+
+@pytest.mark.parametrize("rows,d,f", [(128, 128, 256), (256, 128, 512), (384, 512, 256),
+                                      (512, 512, 1024), (1024, 512, 2048), (4096, 8192, 28672)])
+def test_ffn_backward_in_out_layout_is_bit_identical(gpu, rows, d, f):
+    """The [in, out] entry points (w1 [d, f], w2 [f, d] read as they are,
+    gradients returned in that layout) against the nn.Linear ones on the
+    transposed weights: the training forward's out, rstd, u and h, and dx,
+    dW1^T and dW2^T of both backward forms, bit for bit.  The weight-gradient
+    GEMMs take their operands the other way round there (a^T du, h^T dout;
+    the saved form's dW2 stored transposed), which changes neither the
+    products nor their order.  Includes the full C5 shape."""
+    print(f"ffn_backward [in, out] rows={rows} d={d} f={f}", flush=True)
+    x, w1, w2, dout = make(rows, d, f, seed=5 * rows + d + f)
+    xs, ds = x.to(gpu), dout.to(gpu)
+    w1k, w2k = w1.to(gpu).contiguous(), w2.to(gpu).contiguous()   # [d, f], [f, d]
+    w1l, w2l = hip_lib.linear_layout(w1k), hip_lib.linear_layout(w2k)  # [f, d], [d, f]
+    cfg = hip_lib.make_cfg()
+
+    def train(wa, wb, kn):
+        out = torch.full_like(xs, float("nan"))
+        rstd = torch.full((rows,), float("nan"), device=gpu)
+        u = torch.full((rows, f), float("nan"), device=gpu, dtype=torch.bfloat16)
+        h = torch.full_like(u, float("nan"))
+        hip_lib.ffn_train_forward(xs, wa, wb, out, rstd, u, h, EPS, cfg, kn=kn)
+        return out, rstd, u, h
+
+    def backward(wa, wb, kn, saved):
+        dx = torch.full_like(xs, float("nan"))
+        dw1, dw2 = torch.full_like(wa, float("nan")), torch.full_like(wb, float("nan"))
+        if saved is None:
+            hip_lib.ffn_backward(xs, wa, wb, ds, dx, dw1, dw2, EPS, cfg, kn=kn)
+        else:
+            hip_lib.ffn_backward_saved(xs, wa, wb, ds, *saved[1:], dx, dw1, dw2, cfg, kn=kn)
+        return dx, dw1, dw2
+
+    def same(a, b, name):
+        assert not torch.isnan(a.float()).any(), name
+        assert torch.equal(a.contiguous().view(torch.int16), b.contiguous().view(torch.int16)), (
+            f"{name}: max |diff| {float((a.float() - b.float()).abs().max()):.3e}")
+
+    lin, kn = train(w1l, w2l, False), train(w1k, w2k, True)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("out", "rstd", "u", "h"), kn, lin):
+        same(a, b, f"train forward {name}")
+    for saved in (None, "saved"):
+        ref_g = backward(w1l, w2l, False, None if saved is None else lin)
+        got_g = backward(w1k, w2k, True, None if saved is None else kn)
+        torch.cuda.synchronize()
+        same(got_g[0], ref_g[0], f"{saved} dx")
+        same(got_g[1], ref_g[1].t(), f"{saved} dW1")
+        same(got_g[2], ref_g[2].t(), f"{saved} dW2")
+        del ref_g, got_g
+    del lin, kn
+    torch.cuda.empty_cache()

@@ -54,8 +54,27 @@ def test_estimate_delta_is_sum_of_terms():
     m = cost_model.estimate(spec, 262144, 4, 0.005, prof, baseline_ms=0.3, rows=512)
     assert m.predicted_delta_ms == pytest.approx(
         m.saved_reread_ms + m.fill_gain_ms - m.control_overhead_ms - m.lds_replay_ms
-        - m.l2_exchange_ms)
+        - m.l2_exchange_ms + m.hidden_sync_ms)
     assert m.predicted_profitable == (m.predicted_delta_ms > 0)
+
+
+def test_pipelined_split_hides_at_most_depth_stream_steps_of_sync():
+    """The group pipelines (split_pipeline_depth 2) hide control + exchange
+    up to twice the compulsory stream time; a barrier-synchronised slice
+    kernel (depth 0) hides none.  A control overhead beyond that is charged."""
+    prof = make_device_profile(PARSED)
+    piped = dataclasses.replace(WORKLOADS["softmax_fwd"], rows=512)
+    flat = dataclasses.replace(piped, split_pipeline_depth=0)
+    for ctl in (0.001, 0.05, 5.0):
+        a = cost_model.estimate(piped, 262144, 16, ctl, prof, baseline_ms=0.3, rows=512)
+        b = cost_model.estimate(flat, 262144, 16, ctl, prof, baseline_ms=0.3, rows=512)
+        sync = a.control_overhead_ms + a.l2_exchange_ms
+        remaining = 0.3 - a.saved_reread_ms
+        assert b.hidden_sync_ms == 0.0
+        assert a.hidden_sync_ms == pytest.approx(min(sync, 2 * remaining))
+        assert a.predicted_delta_ms - b.predicted_delta_ms == pytest.approx(a.hidden_sync_ms)
+    assert cost_model.estimate(piped, 262144, 16, 5.0, prof, baseline_ms=0.3,
+                               rows=512).predicted_profitable is False
 
 
 def test_rows_wider_than_staging_save_rereads():
