@@ -17,6 +17,8 @@
 // READ streams the row three times (stats; the two sums; the output), the
 // counterpart of block_bwd_read_kernel (:274-321).
 #include <initializer_list>
+#include <type_traits>
+#include <utility>
 
 #include "api_internal.hpp"
 #include "common.hpp"
@@ -198,6 +200,221 @@ __global__ __launch_bounds__(THREADS) void layernorm_bwd_slice_kernel(
   split_leave(sa);
 }
 
+// ------------------------------------------------ bf16 group pipeline ---
+// SPLIT for bf16 rows: the barrier-free row pipeline of the RMSNorm backward
+// group kernel (credit_amd/csrc/rmsnorm.hip, rmsnorm_group_body) with the
+// LayerNorm statistics in the same single exchange.  Each member publishes
+// four partials of a row, about the row's first element x0:
+//   S1 = sum(x - x0), S2 = sum((x - x0)^2), S3 = sum(g), S4 = sum(g (x - x0))
+// with g = dy * gamma.  From the group totals d = S1/N (= mean - x0),
+// var = S2/N - d^2, rstd, mean(g) = S3/N and
+// mean(g xhat) = rstd (S4 - d S3) / N, so one exchange per row carries what
+// the slice kernel exchanges in two stages.  The communication wave turns
+// the totals into (d, rstd, mean(g), mean(g xhat)); a data wave then writes
+// dx = (g - mean(g) - xhat mean(g xhat)) rstd with xhat = ((x - x0) - d) rstd.
+// The shifted product sum S4 - d S3 cancels where |mean - x0| |S3| is far
+// above |sum(g xhat)| / rstd; fp32 lane sums over 16 elements, fp64 beyond,
+// leave that well inside bf16 output precision (the fp32 variant keeps the
+// two-stage slice kernel).  THREADS data lanes hold VPT vectors of x and dy
+// per row in DEPTH + AHEAD + 1 rotating buffers, gamma's slice in registers,
+// one extra communication wave polls; rows are published DEPTH steps before
+// their totals are needed and loaded AHEAD steps before that.
+constexpr int kLnGroupRing = 16;  // device slot rows per group (> 2 DEPTH + 1)
+constexpr int kLnValues = 4;      // partials per member and row
+
+template <int THREADS, int VPT, int DEPTH, int AHEAD>
+__device__ __forceinline__ void layernorm_bwd_group_body(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ dx, int rows, int cols, int chunk,
+    int members, int rows_per_group, float eps, SplitArgs sa) {
+  constexpr int NW = THREADS / kWave;
+  constexpr int K = kLnValues;
+  constexpr int NB = DEPTH + AHEAD + 1;
+  constexpr int RING = DEPTH + 2 <= 4 ? 4 : 8;
+  static_assert(DEPTH >= 1 && AHEAD >= 1 && DEPTH + 2 <= 8, "pipeline depth");
+  static_assert(2 * DEPTH + 1 < kLnGroupRing, "device slot ring too short for DEPTH");
+  __shared__ double red[RING][K][NW];  // wave partials of row k at [k % RING]
+  __shared__ float ring[RING][4];      // (d, rstd, mean g, mean g xhat) of row k
+  __shared__ uint32_t arrivals[RING];
+  __shared__ uint32_t ready;           // rows 0 .. ready - 1 have totals
+  const int tid = threadIdx.x;
+  if (tid < RING) arrivals[tid] = 0;
+  if (tid == 0) ready = 0;
+  const SplitGroup g = split_join(sa, members, K);  // its barrier covers the stores above
+  // Rows dealt round-robin to the G groups that take rows (padding groups
+  // of the dispenser-multiple grid exit); i counts the group's rows.
+  const int G = (rows + rows_per_group - 1) / rows_per_group;
+  if (g.group >= G) return;
+  const int r1 = (rows - g.group + G - 1) / G;
+  auto row_of = [&](int i) { return g.group + i * G; };
+  const int nvec = cols >> 3;
+  const int v0 = g.member * chunk;
+  const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  const uint32_t slice_bytes = static_cast<uint32_t>(vlen) * 16u;
+  const double inv_n = 1.0 / cols;
+
+  if (__builtin_amdgcn_readfirstlane(tid) >= THREADS) {
+    // ---- communication wave: every row's totals, in row order ----
+    for (int k = 0; k < r1; ++k) {
+      const uint32_t bits = split_poll(g, k, K);
+      const double s1 = split_wave_sum(bits, members, 0);
+      const double s2 = split_wave_sum(bits, members, 1);
+      const double s3 = split_wave_sum(bits, members, 2);
+      const double s4 = split_wave_sum(bits, members, 3);
+      if (tid == THREADS) {
+        const double d = s1 * inv_n;
+        const double var = s2 * inv_n - d * d;
+        const double rs = 1.0 / __builtin_sqrt((var > 0.0 ? var : 0.0) + eps);
+        float* e = ring[k % RING];
+        e[0] = static_cast<float>(d);
+        e[1] = static_cast<float>(rs);
+        e[2] = static_cast<float>(s3 * inv_n);
+        e[3] = static_cast<float>(rs * (s4 - d * s3) * inv_n);
+        __hip_atomic_store(&ready, static_cast<uint32_t>(k + 1), __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+    return;
+  }
+
+  // ---- data waves ----
+  const int wid = tid / kWave;
+  const bool lead = (tid & (kWave - 1)) == 0;
+  const uint32_t lane_off = static_cast<uint32_t>(tid) * 16u;
+  constexpr uint32_t kStride = THREADS * 16u;
+  struct Row {
+    u32x4 x[VPT], d[VPT];
+    uint32_t x0;  // the row's first two bf16 (x0 in the low half), every lane
+  };
+  Row b[NB];
+  // Row r's slice and its first element, or zeros (no traffic) beyond the
+  // group: every load goes through a buffer resource, none under a branch.
+  auto load_row = [&](Row& b, int r) {
+    const bool live = r < r1;
+    const size_t row_off = static_cast<size_t>(row_of(live ? r : 0)) * cols;
+    const size_t off = row_off + 8 * static_cast<size_t>(v0);
+    const buffer_rsrc_t xs = make_rsrc(x + off, live ? slice_bytes : 0u);
+    const buffer_rsrc_t ds = make_rsrc(dy + off, live ? slice_bytes : 0u);
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      b.x[k] = buffer_load_nt(xs, lane_off + k * kStride);
+      b.d[k] = buffer_load_nt(ds, lane_off + k * kStride);
+    }
+    b.x0 = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(x + row_off, live ? 4u : 0u), 0, 0, 0);
+  };
+  const buffer_rsrc_t grs = make_rsrc(gamma + 8 * static_cast<size_t>(v0), slice_bytes);
+  u32x4 gk[VPT];
+#pragma unroll
+  for (int q = 0; q < VPT; ++q) gk[q] = buffer_load(grs, lane_off + q * kStride);
+  // Row k's four lane sums -> wave partials; the last wave in publishes the
+  // member's four partials (wave order, fp64).
+  auto publish_row = [&](const Row& b, int k) {
+    const float x0 = bf16_lo(b.x0);
+    float a[K] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) {
+      float p1 = 0.0f, p2 = 0.0f, p3 = 0.0f, p4 = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xc = Vec<uint16_t>::get(b.x[q], e) - x0;
+        const float gg = Vec<uint16_t>::get(b.d[q], e) * Vec<uint16_t>::get(gk[q], e);
+        p1 += xc;
+        p2 += xc * xc;
+        p3 += gg;
+        p4 += gg * xc;
+      }
+      // Beyond the slice x reads 0: its shifted value -x0 must add nothing
+      // (g is 0 there, since dy reads 0).
+      const bool in = lane_off + q * kStride < slice_bytes;
+      a[0] += in ? p1 : 0.0f;
+      a[1] += in ? p2 : 0.0f;
+      a[2] += p3;
+      a[3] += p4;
+    }
+    double v[K];
+#pragma unroll
+    for (int e = 0; e < K; ++e) v[e] = wave_reduce_sum_f64(static_cast<double>(a[e]));
+    const int slot = k % RING;
+    if (lead) {
+#pragma unroll
+      for (int e = 0; e < K; ++e) red[slot][e][wid] = v[e];
+      const uint32_t t = __hip_atomic_fetch_add(&arrivals[slot], 1u, __ATOMIC_ACQ_REL,
+                                                __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (t == NW - 1) {
+#pragma unroll
+        for (int e = 0; e < K; ++e) {
+          double s = red[slot][e][0];
+#pragma unroll
+          for (int q = 1; q < NW; ++q) s += red[slot][e][q];
+          split_publish_at(g, k, e, s);
+        }
+        arrivals[slot] = 0;
+      }
+    }
+  };
+  auto wait_total = [&](int i) {
+    const uint32_t need = static_cast<uint32_t>(i + 1);
+    while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < need)
+      __builtin_amdgcn_s_sleep(1);
+    return i % RING;
+  };
+  auto finish_row = [&](Row& b, int r, int slot) {
+    // The packed row stays in registers across the DEPTH steps; unpacked
+    // copies would double it (opaque: recompute from the packed values).
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) {
+      __asm__ volatile("" : "+v"(b.x[q]));
+      __asm__ volatile("" : "+v"(b.d[q]));
+    }
+    const float x0 = bf16_lo(b.x0);
+    const float d = ring[slot][0], rs = ring[slot][1], mg = ring[slot][2], mgx = ring[slot][3];
+    const size_t off = static_cast<size_t>(row_of(r)) * cols + 8 * static_cast<size_t>(v0);
+    const buffer_rsrc_t out = make_rsrc(dx + off, slice_bytes);
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xh = ((Vec<uint16_t>::get(b.x[q], e) - x0) - d) * rs;
+        const float gg = Vec<uint16_t>::get(b.d[q], e) * Vec<uint16_t>::get(gk[q], e);
+        o[e] = (gg - mg - xh * mgx) * rs;
+      }
+      buffer_store_nt(out, lane_off + q * kStride, Vec<uint16_t>::pack(o));
+    }
+  };
+  auto step = [&]<int S>(std::integral_constant<int, S>, int i) {
+    load_row(b[(S + DEPTH + AHEAD) % NB], i + DEPTH + AHEAD);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + DEPTH < r1) publish_row(b[(S + DEPTH) % NB], i + DEPTH);
+    finish_row(b[S], i, wait_total(i));
+  };
+  [&]<int... J>(std::integer_sequence<int, J...>) {
+    (load_row(b[J], J), ...);
+  }(std::make_integer_sequence<int, DEPTH + AHEAD>{});
+  [&]<int... J>(std::integer_sequence<int, J...>) {
+    ((J < r1 ? publish_row(b[J], J) : void()), ...);
+  }(std::make_integer_sequence<int, DEPTH>{});
+  int i = 0;
+  for (; i + NB - 1 < r1; i += NB)
+    [&]<int... S>(std::integer_sequence<int, S...>) {
+      (step(std::integral_constant<int, S>{}, i + S), ...);
+    }(std::make_integer_sequence<int, NB>{});
+  [&]<int... S>(std::integer_sequence<int, S...>) {
+    ((i + S < r1 ? step(std::integral_constant<int, S>{}, i + S) : void()), ...);
+  }(std::make_integer_sequence<int, NB - 1>{});
+}
+
+template <int THREADS, int VPT, int DEPTH, int AHEAD>
+__global__ __launch_bounds__(THREADS + kWave)
+__attribute__((amdgpu_waves_per_eu(3, 8))) void layernorm_bwd_group_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ dx, int rows, int cols, int chunk,
+    int members, int rows_per_group, float eps, SplitArgs sa) {
+  layernorm_bwd_group_body<THREADS, VPT, DEPTH, AHEAD>(x, dy, gamma, dx, rows, cols, chunk,
+                                                       members, rows_per_group, eps, sa);
+  split_leave(sa);
+}
+
 // Three streaming passes over the row (any width and alignment).
 template <class T, int THREADS>
 __global__ __launch_bounds__(THREADS) void layernorm_bwd_read_kernel(
@@ -323,6 +540,75 @@ int resolve(const credit_cfg* cfg, int64_t nvec, bool vec, int64_t kCapacity, Pl
   return CREDIT_OK;
 }
 
+// The bf16 group pipeline: members of at most kLnGroupCapacity vectors, at
+// most kMaxExchangeValues / 4 of them (four partials each per row).
+using LnGroupFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int,
+                           int, int, int, float, SplitArgs);
+struct LnGroupPick {
+  LnGroupFn fn;
+  int threads;   // data lanes (plus one communication wave)
+  int capacity;  // vectors per member
+};
+// One shape: 512 lanes x 2 vectors, one workgroup per CU.  A 256-lane form
+// (three workgroups per CU, 16 members of 512 vectors at 2048 x 65536) ran
+// at 2.7 TB/s against 5.0 for this one at 8 members; narrower slices leave
+// lanes of this shape idle instead.
+const LnGroupPick kLnGroup[] = {
+    {layernorm_bwd_group_kernel<512, 2, 3, 2>, 512, 1024},
+};
+constexpr int64_t kLnGroupCapacity = 1024;
+constexpr int kLnGroupMaxMembers = kMaxExchangeValues / kLnValues;
+
+// Members of the bf16 group pipeline for this call, or 0 when it does not
+// apply: AUTO on rows wider than the STAGED capacity (the fewest power-of-two
+// members whose slices fit), SPLIT with a split factor whose slices fit.
+int ln_group_members(const credit_cfg* cfg, int64_t nvec, bool vec) {
+  if (!vec) return 0;
+  const int variant = cfg_variant(cfg);
+  int p = 0;
+  if (variant == CREDIT_VARIANT_AUTO && nvec > Slices<uint16_t>::capacity) {
+    p = 2;
+    while (p * kLnGroupCapacity < nvec) p *= 2;
+  } else if (variant == CREDIT_VARIANT_SPLIT && cfg_split(cfg) > 1) {
+    p = cfg_split(cfg);
+  }
+  if (p < 2 || p > kLnGroupMaxMembers || p > nvec) return 0;
+  const int64_t chunk = (nvec + p - 1) / p;
+  if (chunk > kLnGroupCapacity || (nvec + chunk - 1) / chunk != p) return 0;
+  return p;
+}
+
+int layernorm_bwd_group(const uint16_t* x, const uint16_t* dy, const uint16_t* gamma,
+                        uint16_t* dx, int64_t rows, int64_t cols, float eps, int members,
+                        const credit_cfg* cfg) {
+  const int64_t nvec = cols / 8;
+  const int64_t chunk = (nvec + members - 1) / members;
+  const LnGroupPick* pk = &kLnGroup[0];
+  int64_t fit = 0;
+  int dispensers = 0;
+  CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(pk->fn), pk->threads + kWave, 0,
+                               members, &fit, &dispensers));
+  if (fit == 0)
+    return set_error(CREDIT_ERR_UNSUPPORTED,
+                     "layernorm_bwd: %d groups of %d members do not fit the device", kDispensers,
+                     members);
+  const int64_t g = fit < padded_groups(rows) ? fit : padded_groups(rows);
+  const int64_t rpg = (rows + g - 1) / g;
+  if (rpg > int64_t{credit::plan::kMaxLaunchStages})
+    return set_error(CREDIT_ERR_BAD_SHAPE, "layernorm_bwd: %lld rows per group",
+                     static_cast<long long>(rpg));
+  const int64_t groups = padded_groups((rows + rpg - 1) / rpg);
+  SplitWorkspace ws;
+  CREDIT_TRY(acquire_split_workspace(cfg, groups, members, kLnValues, kLnGroupRing, 0, &ws));
+  const uint32_t total = static_cast<uint32_t>(groups * members);
+  hipLaunchKernelGGL(pk->fn, dim3(total), dim3(pk->threads + kWave), 0, cfg_stream(cfg), x, dy,
+                     gamma, dx, static_cast<int>(rows), static_cast<int>(cols),
+                     static_cast<int>(chunk), members, static_cast<int>(rpg), eps,
+                     make_split_args(ws, total, static_cast<uint32_t>(rpg), kLnGroupRing,
+                                     dispensers));
+  return check_launch("layernorm_bwd_group_kernel");
+}
+
 template <class T>
 int layernorm_bwd(const T* x, const T* dy, const T* gamma, T* dx, int64_t rows, int64_t cols,
                   float eps, const credit_cfg* cfg) {
@@ -343,6 +629,10 @@ int layernorm_bwd(const T* x, const T* dy, const T* gamma, T* dx, int64_t rows, 
   for (const void* p : {static_cast<const void*>(x), static_cast<const void*>(dy),
                         static_cast<const void*>(gamma), static_cast<const void*>(dx)})
     vec = vec && reinterpret_cast<uintptr_t>(p) % 16 == 0;
+  if constexpr (std::is_same_v<T, uint16_t>) {
+    if (const int p = ln_group_members(cfg, cols / E, vec))
+      return layernorm_bwd_group(x, dy, gamma, dx, rows, cols, eps, p, cfg);
+  }
   Plan plan;
   CREDIT_TRY(resolve(cfg, cols / E, vec, Slices<T>::capacity, &plan));
   hipStream_t stream = cfg_stream(cfg);
@@ -390,6 +680,13 @@ size_t layernorm_bwd_workspace(int64_t rows, int64_t cols, int variant, int spli
   Plan p;
   const int64_t e = 16 / elem_bytes;
   const int64_t cap = elem_bytes == 4 ? Slices<float>::capacity : Slices<uint16_t>::capacity;
+  if (elem_bytes == 2) {
+    if (const int m = ln_group_members(&c, cols / e, cols % e == 0)) {
+      int64_t groups = coresident_groups_bound(m, cu_count);
+      if (groups > padded_groups(rows)) groups = padded_groups(rows);
+      return split_workspace_bytes(groups, m, kLnValues, kLnGroupRing, 0);
+    }
+  }
   if (resolve(&c, cols / e, cols % e == 0, cap, &p) != CREDIT_OK || p.members <= 1) return 0;
   int64_t groups = coresident_groups_bound(p.members, cu_count);
   if (groups > padded_groups(rows)) groups = padded_groups(rows);

@@ -491,6 +491,32 @@ int stream_ceiling(int reads, int writes, int64_t call_bytes, int trials, int it
 
 namespace {
 
+// The runtime's own device-to-device copy (hipMemcpyAsync on the null
+// stream) of `bytes` per call, over the stream ceiling's three rotating
+// buffer sets, settle phase and trial blocks: an independent 1:1 ceiling
+// beside the library's stream kernels.  results: [0] GB/s (read + write
+// bytes over the median call time), [1] ms per call.
+int bench_runtime_copy(int64_t bytes, int iters, double* results, int n) {
+  if (bytes < (int64_t{1} << 20)) bytes = int64_t{128} << 20;
+  if (iters <= 0) iters = 20;
+  constexpr int kSets = 3;
+  std::vector<DevBuf> src(kSets), dst(kSets);
+  for (int k = 0; k < kSets; ++k) {
+    CREDIT_TRY(src[k].alloc(static_cast<size_t>(bytes)));
+    CREDIT_TRY(dst[k].alloc(static_cast<size_t>(bytes)));
+  }
+  auto launch = [&](int i) -> int {
+    CREDIT_HIP(hipMemcpyAsync(dst[i % kSets].p, src[i % kSets].p, static_cast<size_t>(bytes),
+                              hipMemcpyDeviceToDevice, nullptr));
+    return CREDIT_OK;
+  };
+  double ms = 0.0;
+  CREDIT_TRY(settled_median_ms(launch, 20.0, 5, iters, &ms));
+  results[0] = 2.0 * static_cast<double>(bytes) / (ms * 1e-3) / 1e9;
+  if (n > 1) results[1] = ms;
+  return CREDIT_OK;
+}
+
 int bench_stream(int which, int64_t bytes, int iters, double* results, int n) {
   if (bytes < (int64_t{1} << 20)) bytes = int64_t{1} << 30;
   const int reads = which == CREDIT_MB_HBM_WRITE ? 0 : 1;
@@ -858,6 +884,8 @@ extern "C" int credit_microbench(int32_t which, int64_t bytes, int32_t iters, do
       return bench_mfma(iters, results, n_results);
     case CREDIT_MB_XCC_MAP:
       return bench_xcc_map(results, n_results);
+    case CREDIT_MB_RUNTIME_COPY:
+      return bench_runtime_copy(bytes, iters, results, n_results);
     default:
       return set_error(CREDIT_ERR_BAD_CONFIG, "unknown microbenchmark %d", which);
   }

@@ -286,6 +286,7 @@ MICROBENCH = {
     "exchange_throughput": 10,
     "mfma_bf16": 11,
     "xcc_map": 12,
+    "runtime_copy": 13,
 }
 
 

@@ -128,6 +128,14 @@ def ceiling_table(sizes: list[int], trials: int = 5, iters: int = 20) -> str:
                          f"{sh['workgroups_per_cu']}/CU{', nt' if sh['nontemporal_stores'] else ''})")
         lines.append(f"| {r}:{w} | " + " | ".join(cells) + " |")
         print(f"ceiling {r}:{w} done", file=sys.stderr, flush=True)
+    # The runtime's own copy (hipMemcpyAsync device to device) at the same
+    # 1:1 call sizes, settled and rotated the same way: an independent check
+    # of the 1:1 row.
+    cells = []
+    for s in sizes:
+        gbps, ms = hip_lib.microbench("runtime_copy", s // 2, iters, 2)
+        cells.append(f"{gbps:.0f} GB/s ({ms * 1e3:.1f} us per call)")
+    lines.append("| 1:1, runtime D2D copy | " + " | ".join(cells) + " |")
     return "\n".join(lines) + "\n"
 
 

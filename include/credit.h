@@ -528,6 +528,14 @@ int credit_transpose_bf16(const uint16_t* src, uint16_t* dst, int64_t rows, int6
  *                         split launches' ticket subsets assume.  No
  *                         counterpart in the reference (one die per GPU). */
 #define CREDIT_MB_XCC_MAP 12
+/*  RUNTIME_COPY           the runtime's device-to-device hipMemcpyAsync of
+ *                         `bytes` (default 128 MiB) per call, settled and
+ *                         timed as credit_stream_ceiling times its kernels
+ *                         (three rotating buffer sets): [0] GB/s counting
+ *                         read and write bytes, [1] ms per call.  An
+ *                         independent 1:1 ceiling; the DRAM copy of
+ *                         primitive_benchmark.cu:160-171 in the reference. */
+#define CREDIT_MB_RUNTIME_COPY 13
 int credit_microbench(int32_t which, int64_t bytes, int32_t iters, double* results,
                       int32_t n_results);
 

@@ -97,3 +97,35 @@ def test_layernorm_backward_full_reference_shape(gpu):
     e = expect(x, dy, gamma)
     for variant, split in [("auto", 0), ("split", 4), ("read", 0)]:
         np.testing.assert_allclose(run(x, dy, gamma, variant, split, gpu), e, **FP32)
+
+
+@pytest.mark.parametrize("variant,split,shape", [
+    ("auto", 0, (2048, 65536)),    # the reference shape: the group pipeline, 8 members
+    ("split", 16, (2048, 65536)),  # 16 members of 512 vectors (the 256-lane kernel)
+    ("split", 2, (2048, 65536)),   # slices too wide for the group pipeline: slice kernel
+    ("auto", 0, (40, 131072)),     # 16 members of 1024 vectors
+    ("split", 5, (64, 40960)),     # a non-power-of-two group
+    ("split", 4, (1, 32768)),      # one row: every group but one is padding
+])
+def test_layernorm_backward_bf16_group_pipeline(gpu, variant, split, shape):
+    """bf16 rows wider than one workgroup take the group pipeline (one
+    exchange of four shifted sums per row), against the float64 oracle."""
+    print(f"layernorm_backward bf16 {variant} P={split} shape={shape}", flush=True)
+    x, dy, gamma = WORKLOADS["layernorm_backward_bf16"].make_inputs(*shape, seed=17)
+    np.testing.assert_allclose(run(x, dy, gamma, variant, split, gpu), expect(x, dy, gamma), **BF16)
+
+
+@pytest.mark.parametrize("variant,split", [("auto", 0), ("split", 8), ("split", 3)])
+def test_layernorm_backward_bf16_offset_spike_and_constant_rows(gpu, variant, split):
+    """Rows the shifted sums must survive: a large common offset, a spike as
+    the row's first element x0 (the shift point far from the mean), a
+    constant row (variance 0), at 65536 columns."""
+    x, dy, gamma = WORKLOADS["layernorm_backward_bf16"].make_inputs(6, 65536, seed=23)
+    x = x.float()
+    x[0] += 1000.0
+    x[1, 0] = 300.0
+    x[2] = 0.25
+    x[3, 0] = -500.0
+    x[3, 1:] *= 4.0
+    x = x.to(torch.bfloat16)
+    np.testing.assert_allclose(run(x, dy, gamma, variant, split, gpu), expect(x, dy, gamma), **BF16)
