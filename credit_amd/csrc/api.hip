@@ -473,6 +473,13 @@ int credit_check_watchdog(const credit_cfg* cfg) {
   return CREDIT_OK;
 }
 
+int credit_host_watchdog_words(int32_t* count) {
+  CREDIT_TRY(check_ptr(count, "count"));
+  std::lock_guard<std::mutex> lock(g_host_flag_mu);
+  *count = static_cast<int32_t>(g_host_flags.size());
+  return CREDIT_OK;
+}
+
 int credit_last_split_shape(int32_t* threads, int32_t* lds_bytes, int32_t* per_cu,
                             int32_t* dispensers) {
   CREDIT_TRY(check_ptr(threads, "threads"));

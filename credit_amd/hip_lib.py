@@ -154,6 +154,7 @@ SIGNATURES: dict[str, list] = {
                                 ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],
     "credit_last_split_shape": [ctypes.POINTER(ctypes.c_int32)] * 4,
     "credit_set_clock_probe": [_P],
+    "credit_host_watchdog_words": [ctypes.POINTER(ctypes.c_int32)],
 }
 _RESTYPES = {
     "credit_version": ctypes.c_char_p,

@@ -582,6 +582,12 @@ int credit_control_overhead(int64_t rows, int32_t split, int32_t barriers, int32
  * launched meanwhile on any stream add to the same sums. */
 int credit_set_clock_probe(uint64_t* sums);
 
+/* Host-mapped watchdog words this process has allocated (at most one per
+ * device; the first allocating split call on a device makes it).  Lets a
+ * caller check that the allocation-free entry point allocated nothing.  No
+ * counterpart in the reference. */
+int credit_host_watchdog_words(int32_t* count);
+
 /* Shape of the last co-resident split launch this thread made: block size
  * (data lanes plus any communication wave), LDS per workgroup (static and
  * dynamic), workgroups resident per CU, and its ticket subsets.  What the

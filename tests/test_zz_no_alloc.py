@@ -4,6 +4,10 @@ device array) must give the allocating entry point's outputs, bit for bit
 (same kernels, deterministic dweight order), on two calls in a row, the
 second with a smaller input; shapes beyond the array are rejected."""
 import ctypes
+import os
+import subprocess
+import sys
+from pathlib import Path
 
 import pytest
 import torch
@@ -44,8 +48,9 @@ def test_noalloc_matches_the_allocating_entry_point(gpu, first, second):
     for shape, seed in ((first, 11), (second, 12)):
         print(f"rmsnorm_bwd noalloc shape={shape}", flush=True)
         ins = _inputs(*shape, seed, gpu)
-        # The allocation-free call first: in a fresh process no allocating
-        # split call has run yet, so it runs without a host-mapped watchdog word.
+        # In this suite's process earlier split calls have made the device's
+        # host-mapped watchdog word, which the allocation-free call then uses;
+        # test_noalloc_first_call_in_a_fresh_process covers the call without one.
         got = _run(lib.credit_rmsnorm_bwd_bf16_noalloc, *ins)
         ref = _run(lib.credit_rmsnorm_bwd_bf16, *ins)
         assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
@@ -101,3 +106,47 @@ def test_noalloc_expired_wait_is_reported(gpu):
     got = _run(lib.credit_rmsnorm_bwd_bf16_noalloc, *ins, "split", 8)
     assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
     hip_lib.check_watchdog()
+
+
+_FRESH = r"""
+import ctypes, sys, torch
+from credit_amd import hip_lib
+from credit_amd.workloads import WORKLOADS
+lib = hip_lib.load_library()
+dev = torch.device("cuda:0")
+x, w, dy = (t.to(dev) for t in WORKLOADS["rmsnorm_bwd"].make_inputs(64, 65536, seed=3))
+rstd = torch.rand(64, device=dev) + 0.5
+def run(fn):
+    dx, dw = torch.full_like(x, 7.0), torch.full((65536,), float("nan"), device=dev)
+    cfg = hip_lib.make_cfg("split", 8)
+    hip_lib.check(fn(x.data_ptr(), w.data_ptr(), dy.data_ptr(), rstd.data_ptr(), dx.data_ptr(),
+                     dw.data_ptr(), 64, 65536, ctypes.byref(cfg)), "rmsnorm_bwd")
+    torch.cuda.synchronize()
+    return dx.cpu(), dw.cpu()
+def words():
+    n = ctypes.c_int32()
+    hip_lib.check(lib.credit_host_watchdog_words(ctypes.byref(n)), "words")
+    return n.value
+assert words() == 0
+got = run(lib.credit_rmsnorm_bwd_bf16_noalloc)  # the first library call of the process
+assert words() == 0, "the allocation-free call allocated a host watchdog word"
+hip_lib.check_watchdog()
+ref = run(lib.credit_rmsnorm_bwd_bf16)
+assert words() == 1
+assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
+print("fresh-process allocation-free call: ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_in_a_fresh_process(gpu):
+    """In a child process whose first library call is the allocation-free
+    one (split 8, so it runs the exchange): no host-mapped watchdog word
+    exists yet and none is made; its outputs match the allocating entry
+    point's, which then makes the word."""
+    root = Path(__file__).resolve().parents[1]
+    env = dict(os.environ, PYTHONPATH=str(root) + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    print("allocation-free call in a child process", flush=True)
+    out = subprocess.run([sys.executable, "-c", _FRESH], capture_output=True, text=True,
+                         timeout=240, env=env, cwd=str(root))
+    assert out.returncode == 0, out.stdout[-2000:] + out.stderr[-4000:]
+    assert "fresh-process allocation-free call: ok" in out.stdout
