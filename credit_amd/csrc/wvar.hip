@@ -203,11 +203,19 @@ const Pick<WvarFn> kWvar[] = {
     {wvar_bwd_slice_kernel<256, 4>, 256, 1024},
     {wvar_bwd_slice_kernel<512, 4>, 512, 2048},
     {wvar_bwd_slice_kernel<1024, 4>, 1024, 4096},
+    {wvar_bwd_slice_kernel<512, 16>, 512, 8192},
 };
+// AUTO and STAGED hold at most 4096 vectors per workgroup; an explicit SPLIT
+// may take the 512-lane 16-vector shape (192 VGPRs of row data, one
+// workgroup per CU), which brings 262144 columns within 12 members (five
+// partials each fill at most 64 exchange slots per stage).
 constexpr int64_t kWvarCapacity = 4096;
+constexpr int64_t kWvarSplitCapacity = 8192;
 
 int wvar_plan(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
-  CREDIT_TRY(resolve(cfg, cols, vec, kWvarCapacity, "weighted_var_backward", plan));
+  const int64_t capacity =
+      cfg_variant(cfg) == CREDIT_VARIANT_SPLIT ? kWvarSplitCapacity : kWvarCapacity;
+  CREDIT_TRY(resolve(cfg, cols, vec, capacity, "weighted_var_backward", plan));
   if (plan->members * kWvarValues > kMaxExchangeValues) {
     if (cfg_variant(cfg) != CREDIT_VARIANT_AUTO)
       return set_error(CREDIT_ERR_UNSUPPORTED,

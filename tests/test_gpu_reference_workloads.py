@@ -28,6 +28,9 @@ def _gpu(ts, gpu):
 
 
 PARTIALS = {"lars_momentum": 2, "weighted_var_backward": 5, "pearson_backward": 5}
+# f32x4 one member holds under an explicit SPLIT where it exceeds the STAGED
+# width (the weighted-variance 512-lane 16-vector slice shape).
+SPLIT_CAP = {"weighted_var_backward": 8192}
 
 
 def supported(name, variant, split, cols):
@@ -45,7 +48,7 @@ def supported(name, variant, split, cols):
     p = min(split, nvec)
     chunk = -(-nvec // p)
     members = -(-nvec // chunk)
-    return chunk <= cap and members * PARTIALS[name] <= 64
+    return chunk <= SPLIT_CAP.get(name, cap) and members * PARTIALS[name] <= 64
 
 
 def run_or_reject(name, variant, split, cols, fn):
@@ -168,6 +171,24 @@ def test_weighted_var_wide_and_shifted_rows(gpu, variant, split):
     x[2] *= 1e-3
     np.testing.assert_allclose(wvar(x, w, dy, variant, split, gpu),
                                ref.weighted_var_backward(x, w, dy), **FP32)
+
+
+@pytest.mark.parametrize("variant,split", [("split", 8), ("split", 12), ("split", 6),
+                                           ("auto", 0)])
+def test_weighted_var_262144_columns(gpu, variant, split):
+    """The widest swept width: an explicit SPLIT of 8 or 12 members takes the
+    512-lane 16-vector slice shape (32768 and 21848 columns per member), 6
+    members are too few (43692 > 32768 columns each) and are refused, AUTO stays
+    on the 4096-vector shapes (16 members x 5 partials exceed one exchange:
+    the READ kernel).  Row 1 is shifted by 1000."""
+    print(f"weighted_var 262144 {variant} P={split}", flush=True)
+    x, w, dy = WORKLOADS["weighted_var_backward"].make_inputs(3, 262144, seed=85)
+    x[1] += 1000.0
+    got = run_or_reject("weighted_var_backward", variant, split, 262144,
+                        lambda: wvar(x, w, dy, variant, split, gpu))
+    assert (got is None) == (split == 6)
+    if got is not None:
+        np.testing.assert_allclose(got, ref.weighted_var_backward(x, w, dy), **FP32)
 
 
 def test_weighted_var_hash_inputs_and_rejects(gpu):
