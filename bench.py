@@ -68,7 +68,7 @@ CALL_KERNELS = {
     "row_sum_max": ("rowreduce.hip", ["row_sum_max_read_kernel<256>"]),
     "layernorm_fwd": ("layernorm.hip", ["layernorm_fwd_pipe_kernel<512, 8>"]),
     "rmsnorm_fwd": ("rmsnorm.hip", ["rmsnorm_fwd_slice_kernel<1024, 8>"]),
-    "rmsnorm_bwd": ("rmsnorm.hip", ["rmsnorm_bwd_group_kernel<512, 2, 3, 2>",
+    "rmsnorm_bwd": ("rmsnorm.hip", ["rmsnorm_bwd_group_kernel<512, 2, 4, 2>",
                                     "rmsnorm_dw_reduce_kernel"]),
     "rmsnorm_fwd_bwd": ("rmsnorm.hip", ["rmsnorm_fused_group_kernel<512, 2, 2, 2>",
                                         "rmsnorm_dw_reduce_kernel"]),
@@ -80,7 +80,7 @@ CALL_KERNELS = {
     "ffn_baseline_layout": ("ffn.hip", ["ffn_rstd_kernel", "ffn_gemm256_kernel<0, true>",
                                         "ffn_gemm256_kernel<1, true>"]),
     "layernorm_backward": ("lnbwd.hip", ["layernorm_bwd_slice_kernel<float, 1024, 8>"]),
-    "layernorm_backward_bf16": ("lnbwd.hip", ["layernorm_bwd_group_kernel<512, 2, 3, 2>"]),
+    "layernorm_backward_bf16": ("lnbwd.hip", ["layernorm_bwd_group_kernel<512, 2, 4, 2>"]),
     "rowwise_quant": ("quant.hip", ["rowwise_quant_slice_kernel<1024, 16>"]),
     "lars_momentum": ("lars.hip", ["lars_slice_kernel<512, 8>"]),
     "weighted_var_backward": ("wvar.hip", ["wvar_bwd_slice_kernel<1024, 4>"]),

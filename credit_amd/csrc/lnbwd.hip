@@ -553,8 +553,12 @@ struct LnGroupPick {
 // (three workgroups per CU, 16 members of 512 vectors at 2048 x 65536) ran
 // at 2.7 TB/s against 5.0 for this one at 8 members; narrower slices leave
 // lanes of this shape idle instead.
+// DEPTH 4 / AHEAD 2: seven row buffers (168 VGPRs, no spill).  At
+// 2048 x 65536, two GPU sessions of three alternating runs: 160.0 us at 3 / 2,
+// 157.6 at 4 / 1, 157.7 at 2 / 2, 153.9 at 3 / 1 and 3 / 3, 152.1 at 2 / 1,
+// 151.8 at 4 / 2 (5 / 1 spills).
 const LnGroupPick kLnGroup[] = {
-    {layernorm_bwd_group_kernel<512, 2, 3, 2>, 512, 1024},
+    {layernorm_bwd_group_kernel<512, 2, 4, 2>, 512, 1024},
 };
 constexpr int64_t kLnGroupCapacity = 1024;
 constexpr int kLnGroupMaxMembers = kMaxExchangeValues / kLnValues;

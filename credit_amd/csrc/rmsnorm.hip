@@ -354,7 +354,10 @@ __global__ __launch_bounds__(THREADS) void rmsnorm_bwd_slice_kernel(
 // (16 members of 1024 vectors), against DEPTH 2 / AHEAD 1 on the same box:
 // the backward at DEPTH 3 / AHEAD 2 160.3 -> 157.6 us on one box and
 // unchanged (161.0) on another, the fused forward + backward at 2 / 2
-// 227 -> 217 and 229.5 -> 221.3 us; DEPTH 1 is exchange-bound (225 us), and
+// 227 -> 217 and 229.5 -> 221.3 us; later, the backward at DEPTH 4 / AHEAD 2
+// (seven row buffers, 162 VGPRs) 148.7 -> 147.5 us against 3 / 2 (three
+// alternating runs, one box; 3 / 3 and 2 / 3 no better, AHEAD 1 spills);
+// DEPTH 1 is exchange-bound (225 us), and
 // a build whose communication wave does not wait at all is slower (169.5
 // us), so the exchange is not what bounds the kernel.  The LDS ring, partial and
 // counter slots of row k are reused by row k+RING only (RING >= DEPTH + 2):
@@ -721,7 +724,7 @@ const BwdGroupPick kBwdGroup[] = {
     {rmsnorm_bwd_group_kernel<192, 1>, 192, 192, 4},
     {rmsnorm_bwd_group_kernel<448, 1>, 448, 448, 2},
     {rmsnorm_bwd_group_kernel<960, 1>, 960, 960, 1},
-    {rmsnorm_bwd_group_kernel<512, 2, 3, 2>, 512, 1024, 1},
+    {rmsnorm_bwd_group_kernel<512, 2, 4, 2>, 512, 1024, 1},
 };
 // Fused forward + backward: the same shapes, the sum of squares riding in
 // the same exchange (two values per member, so at most 32 members).
