@@ -339,8 +339,10 @@ int credit_lars_momentum_f32(const float* weight, const float* grad, const float
  * src/workloads/weighted_var_backward.cu:303-506, launched per
  * dsmem_eval/runner.py:280-310).  x, weight, dy, dx fp32 [rows, cols]; eps
  * > 0 (the reference's torch function uses 1e-5).  One exchange of five
- * sums per row (SPLIT: at most 12 members); STAGED holds x, w and dy for
- * rows <= 16384 columns; READ streams the inputs twice, any width. */
+ * sums per row (SPLIT: at most 12 members of at most 32768 columns each);
+ * STAGED holds x, w and dy for rows <= 16384 columns; READ streams the
+ * inputs twice, any width.  AUTO splits into members of at most 16384
+ * columns and takes READ where that needs more than 12. */
 int credit_weighted_var_bwd_f32(const float* x, const float* weight, const float* dy,
                                 float* dx, int64_t rows, int64_t cols, float eps,
                                 const credit_cfg* cfg);
