@@ -67,7 +67,7 @@ TRAFFIC_SUMMARY = ROOT / "profiles" / "hbm_traffic_suite.json"
 CALL_KERNELS = {
     "row_sum_max": ("rowreduce.hip", ["row_sum_max_read_kernel<256>"]),
     "layernorm_fwd": ("layernorm.hip", ["layernorm_fwd_pipe_kernel<512, 8>"]),
-    "rmsnorm_fwd": ("rmsnorm.hip", ["rmsnorm_fwd_slice_kernel<1024, 8>"]),
+    "rmsnorm_fwd": ("rmsnorm.hip", ["rmsnorm_fwd_group_kernel<512, 4, 4, 1>"]),
     "rmsnorm_bwd": ("rmsnorm.hip", ["rmsnorm_bwd_group_kernel<512, 2, 4, 2>",
                                     "rmsnorm_dw_reduce_kernel"]),
     "rmsnorm_fwd_bwd": ("rmsnorm.hip", ["rmsnorm_fused_group_kernel<512, 2, 2, 2>",

@@ -589,6 +589,146 @@ __device__ __forceinline__ void rmsnorm_group_body(
                                                    dw_lds[(v * 8 + 2 * q + 1) * THREADS + tid]}));
 }
 
+// Forward group pipeline (SPLIT of at most 32 members of 1025-2048 vectors, and AUTO on
+// rows of 8193-16384 vectors: C3's 131072 columns run as 8 members): the
+// backward's pipeline on x alone -- VPT dwordx4 of x per lane and row in
+// DEPTH + AHEAD + 1 rotating buffers, the weight slice in registers, no
+// barrier in the row loop -- with one exchanged value per row (the member's
+// sum of squares), which the communication wave turns into rstd.  At C3,
+// three alternating runs against the two-member slice kernel (97.0 us):
+// DEPTH / AHEAD 4 / 1 95.1 us, 3 / 2 95.7, 3 / 1 99.0, 2 / 2 103.0, 2 / 1
+// 104.7; 16 members of 1024 vectors (VPT 2) 4 / 2 118.7, 2 / 1 110.8; 5 / 1
+// and 4 / 2 at VPT 4 exceed the 168 VGPRs of a 9-wave workgroup.
+template <int THREADS, int VPT, int DEPTH, int AHEAD>
+__device__ __forceinline__ void rmsnorm_fwd_group_body(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
+    float* __restrict__ rstd_out, int rows, int cols, int chunk, int members,
+    int rows_per_group, float eps, SplitArgs sa) {
+  constexpr int NW = THREADS / kWave;
+  constexpr int NB = DEPTH + AHEAD + 1;
+  constexpr int RING = DEPTH + 2 <= 4 ? 4 : 8;
+  static_assert(DEPTH >= 1 && AHEAD >= 1 && DEPTH + 2 <= 8, "pipeline depth");
+  static_assert(2 * DEPTH + 1 < kGroupSlotRing, "device slot ring too short for DEPTH");
+  __shared__ double red[RING][NW];
+  __shared__ float ring[RING];
+  __shared__ uint32_t arrivals[RING];
+  __shared__ uint32_t ready;
+  const int tid = threadIdx.x;
+  if (tid < RING) arrivals[tid] = 0;
+  if (tid == 0) ready = 0;
+  const SplitGroup g = split_join(sa, members, 1);
+  const int G = (rows + rows_per_group - 1) / rows_per_group;
+  if (g.group >= G) return;
+  const int r1 = (rows - g.group + G - 1) / G;
+  auto row_of = [&](int i) { return g.group + i * G; };
+  const int nvec = cols >> 3;
+  const int v0 = g.member * chunk;
+  const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
+  const uint32_t slice_bytes = static_cast<uint32_t>(vlen) * 16u;
+  if (__builtin_amdgcn_readfirstlane(tid) >= THREADS) {
+    for (int k = 0; k < r1; ++k) {
+      const uint32_t bits = split_poll(g, k, 1);
+      const double ssq = split_wave_sum(bits, members, 0);
+      if (tid == THREADS) {
+        ring[k % RING] = static_cast<float>(1.0 / __builtin_sqrt(ssq / cols + eps));
+        __hip_atomic_store(&ready, static_cast<uint32_t>(k + 1), __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+    return;
+  }
+  const int wid = tid / kWave;
+  const bool lead = (tid & (kWave - 1)) == 0;
+  const uint32_t lane_off = static_cast<uint32_t>(tid) * 16u;
+  constexpr uint32_t kStride = THREADS * 16u;
+  struct Row {
+    u32x4 x[VPT];
+  };
+  Row b[NB];
+  auto load_row = [&](Row& b, int r) {
+    const bool live = r < r1;
+    const size_t off =
+        static_cast<size_t>(row_of(live ? r : 0)) * cols + 8 * static_cast<size_t>(v0);
+    const buffer_rsrc_t xs = make_rsrc(x + off, live ? slice_bytes : 0u);
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) b.x[k] = buffer_load_nt(xs, lane_off + k * kStride);
+  };
+  const buffer_rsrc_t wrs = make_rsrc(w + 8 * static_cast<size_t>(v0), slice_bytes);
+  u32x4 wk[VPT];
+#pragma unroll
+  for (int q = 0; q < VPT; ++q) wk[q] = buffer_load(wrs, lane_off + q * kStride);
+  auto publish_row = [&](const Row& b, int k) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) ss += sumsq8(b.x[q]);
+    const double v = wave_reduce_sum_f64(static_cast<double>(ss));
+    const int slot = k % RING;
+    if (lead) {
+      red[slot][wid] = v;
+      const uint32_t t = __hip_atomic_fetch_add(&arrivals[slot], 1u, __ATOMIC_ACQ_REL,
+                                                __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (t == NW - 1) {
+        double s = red[slot][0];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) s += red[slot][q];
+        split_publish_at(g, k, 0, s);
+        arrivals[slot] = 0;
+      }
+    }
+  };
+  auto wait_total = [&](int i) {
+    const uint32_t need = static_cast<uint32_t>(i + 1);
+    while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < need)
+      __builtin_amdgcn_s_sleep(1);
+    return i % RING;
+  };
+  auto finish_row = [&](Row& b, int r, int slot) {
+#pragma unroll
+    for (int q = 0; q < VPT; ++q) __asm__ volatile("" : "+v"(b.x[q]));
+    const float rs = ring[slot];
+    const size_t off = static_cast<size_t>(row_of(r)) * cols + 8 * static_cast<size_t>(v0);
+    const buffer_rsrc_t out = make_rsrc(y + off, slice_bytes);
+#pragma unroll
+    for (int q = 0; q < VPT; ++q)
+      buffer_store_nt(out, lane_off + q * kStride, scale8(b.x[q], wk[q], rs));
+    // Lane 0 of member 0 writes rstd (a 4-byte resource; other lanes fall outside it).
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(rs),
+                                          make_rsrc(rstd_out + row_of(r), g.member == 0 ? 4u : 0u),
+                                          static_cast<uint32_t>(tid) * 4u, 0, 0);
+  };
+  auto step = [&]<int S>(std::integral_constant<int, S>, int i) {
+    load_row(b[(S + DEPTH + AHEAD) % NB], i + DEPTH + AHEAD);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + DEPTH < r1) publish_row(b[(S + DEPTH) % NB], i + DEPTH);
+    finish_row(b[S], i, wait_total(i));
+  };
+  [&]<int... J>(std::integer_sequence<int, J...>) {
+    (load_row(b[J], J), ...);
+  }(std::make_integer_sequence<int, DEPTH + AHEAD>{});
+  [&]<int... J>(std::integer_sequence<int, J...>) {
+    ((J < r1 ? publish_row(b[J], J) : void()), ...);
+  }(std::make_integer_sequence<int, DEPTH>{});
+  int i = 0;
+  for (; i + NB - 1 < r1; i += NB)
+    [&]<int... S>(std::integer_sequence<int, S...>) {
+      (step(std::integral_constant<int, S>{}, i + S), ...);
+    }(std::make_integer_sequence<int, NB>{});
+  [&]<int... S>(std::integer_sequence<int, S...>) {
+    ((i + S < r1 ? step(std::integral_constant<int, S>{}, i + S) : void()), ...);
+  }(std::make_integer_sequence<int, NB - 1>{});
+}
+
+template <int THREADS, int VPT, int DEPTH, int AHEAD>
+__global__ __launch_bounds__(THREADS + kWave)
+__attribute__((amdgpu_waves_per_eu(3, 8))) void rmsnorm_fwd_group_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
+    float* __restrict__ rstd_out, int rows, int cols, int chunk, int members,
+    int rows_per_group, float eps, SplitArgs sa) {
+  rmsnorm_fwd_group_body<THREADS, VPT, DEPTH, AHEAD>(x, w, y, rstd_out, rows, cols, chunk,
+                                                     members, rows_per_group, eps, sa);
+  split_leave(sa);
+}
+
 // Waves per SIMD a group kernel is compiled for: VPT 1 leaves room for two
 // 8-wave workgroups per CU; VPT 2 fills one 9-wave workgroup (512 data
 // lanes plus the communication wave).
@@ -747,6 +887,13 @@ const FusedGroupPick kFusedGroup[] = {
 };
 constexpr int kMaxFusedMembers = kMaxExchangeValues / 2;
 constexpr int kFwdMaxCapacity = 8192;
+// The forward group pipeline: 512 data lanes x 4 dwordx4; AUTO takes it for
+// rows that need at most 8 such members.
+constexpr int kFwdGroupThreads = 512;
+constexpr int kFwdGroupVpt = 4;
+constexpr int64_t kFwdGroupCapacity = kFwdGroupThreads * kFwdGroupVpt;
+constexpr int kFwdGroupAutoMembers = 8;
+
 constexpr int kBwdMaxCapacity = 1024;      // slice kernels (STAGED, READ tiles)
 constexpr int kBwdGroupCapacity = 1024;    // group kernel (SPLIT): largest member slice
 
@@ -771,6 +918,13 @@ struct Plan {
   int members;
   int64_t chunk;
 };
+
+// SPLIT plans of at most 32 members holding 1025-2048 vectors each run the
+// forward group pipeline; the others the slice kernel.
+bool fwd_takes_group(const Plan& p) {
+  return p.variant == CREDIT_VARIANT_SPLIT && p.members <= 32 &&
+         p.chunk > kFwdGroupCapacity / 2 && p.chunk <= kFwdGroupCapacity;
+}
 
 Plan plan_split(int64_t nvec, int members) {
   Plan p{CREDIT_VARIANT_SPLIT, members, (nvec + members - 1) / members};
@@ -797,7 +951,14 @@ int resolve_fwd(const credit_cfg* cfg, int64_t cols, bool vec, Plan* plan) {
     if (variant == CREDIT_VARIANT_STAGED)
       return set_error(CREDIT_ERR_UNSUPPORTED,
                        "rmsnorm_fwd staged variant holds at most %d columns", kFwdMaxCapacity * 8);
-    // AUTO on a row wider than one workgroup: split just enough.
+    // AUTO on a row wider than one workgroup: the group pipeline when at
+    // most kFwdGroupAutoMembers of its slices cover the row, else the slice
+    // kernel split just enough.
+    const int64_t pg = (nvec + kFwdGroupCapacity - 1) / kFwdGroupCapacity;
+    if (pg <= kFwdGroupAutoMembers) {
+      *plan = plan_split(nvec, static_cast<int>(pg));
+      return CREDIT_OK;
+    }
     *plan = plan_split(nvec, static_cast<int>((nvec + kFwdMaxCapacity - 1) / kFwdMaxCapacity));
     return CREDIT_OK;
   }
@@ -1096,6 +1257,32 @@ extern "C" int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uin
       rmsnorm_fwd_read_kernel<256, false>
           <<<dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream>>>(x, w, y, rstd, c, eps);
     return check_launch("rmsnorm_fwd_read_kernel");
+  }
+  if (fwd_takes_group(plan)) {
+    auto fn = rmsnorm_fwd_group_kernel<kFwdGroupThreads, kFwdGroupVpt, 4, 1>;
+    int64_t fit = 0;
+    int dispensers = 0;
+    CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(fn), kFwdGroupThreads + kWave, 0,
+                                 plan.members, &fit, &dispensers));
+    if (fit == 0)
+      return set_error(CREDIT_ERR_UNSUPPORTED,
+                       "rmsnorm_fwd: %d groups of %d members do not fit the device", kDispensers,
+                       plan.members);
+    const int64_t g = fit < padded_groups(rows) ? fit : padded_groups(rows);
+    const int64_t rows_per_group = (rows + g - 1) / g;
+    if (rows_per_group > int64_t{credit::plan::kMaxLaunchStages})
+      return set_error(CREDIT_ERR_BAD_SHAPE, "rmsnorm_fwd: %lld rows per group",
+                       static_cast<long long>(rows_per_group));
+    const int64_t grid_groups = padded_groups((rows + rows_per_group - 1) / rows_per_group);
+    SplitWorkspace ws;
+    CREDIT_TRY(acquire_split_workspace(cfg, grid_groups, plan.members, 1, kGroupSlotRing, 0, &ws));
+    const uint32_t total = static_cast<uint32_t>(grid_groups * plan.members);
+    hipLaunchKernelGGL(fn, dim3(total), dim3(kFwdGroupThreads + kWave), 0, stream, x, w, y, rstd,
+                       static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members,
+                       static_cast<int>(rows_per_group), eps,
+                       make_split_args(ws, total, static_cast<uint32_t>(rows_per_group),
+                                       kGroupSlotRing, dispensers));
+    return check_launch("rmsnorm_fwd_group_kernel");
   }
   const FwdPick* pick = pick_for(kFwd, plan.chunk);
   if (plan.variant == CREDIT_VARIANT_STAGED) {

@@ -222,10 +222,13 @@ int credit_layernorm_bwd_bf16(const uint16_t* x, const uint16_t* dy, const uint1
  * No RMSNorm exists in the reference; the row sum of squares is the LARS
  * norm of src/workloads/lars_momentum.cu:283-319 (dsmem_eval/workloads.py:
  * 139-140).  Variants: STAGED (row in one workgroup's VGPRs, cols <= 65536),
- * SPLIT (cfg->split workgroups per row exchanging one partial), READ (two
- * streaming passes; any shape).  AUTO: STAGED when the row fits, else the
- * smallest SPLIT that holds it; READ for cols % 8 != 0 or unaligned
- * buffers. */
+ * SPLIT (cfg->split workgroups per row exchanging one partial; at most 32
+ * members of 8193-16384 columns each run a barrier-free pipeline of rows,
+ * other splits a slice kernel of at most 65536 columns per member), READ
+ * (two streaming passes; any shape).  AUTO: STAGED when the row fits, else
+ * the pipeline when at most 8 members of <= 16384 columns cover the row
+ * (C3: 8 members), else the smallest slice SPLIT that holds it; READ for
+ * cols % 8 != 0 or unaligned buffers. */
 int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, float* rstd,
                             int64_t rows, int64_t cols, float eps, const credit_cfg* cfg);
 

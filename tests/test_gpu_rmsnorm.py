@@ -77,6 +77,43 @@ def test_rmsnorm_fwd_wide_rows(gpu, variant, split):
     check_fwd(x, w, *fwd(x, w, variant, split, gpu))
 
 
+@pytest.mark.parametrize("rows,cols,variant,split", [
+    (4, 131072, "auto", 0),    # 8 members of 2048 vectors
+    (5, 98304, "split", 6),    # 6 members of 2048
+    (5, 98304, "split", 7),    # members of 1756 vectors, the last 1752
+    (3, 81920, "auto", 0),     # 5 members of 2048
+    (7, 65544, "auto", 0),     # 8193 vectors: 5 members of 1639, the last 1637
+    (2, 262144, "split", 16),  # 16 members of 2048
+    (1, 131072, "auto", 0),
+    (300, 98304, "split", 6),  # many rows per group
+])
+def test_rmsnorm_fwd_group_pipeline(gpu, rows, cols, variant, split):
+    """Plans whose members hold 1025-2048 vectors run the forward group
+    pipeline (AUTO on rows of 8193-16384 vectors)."""
+    print(f"rmsnorm_fwd group {variant} P={split} shape=({rows}, {cols})", flush=True)
+    x, w, _ = SPEC.make_inputs(rows, cols, seed=rows + cols)
+    check_fwd(x, w, *fwd(x, w, variant, split, gpu))
+    assert hip_lib.last_split_shape()["threads"] == 512 + 64
+
+
+def test_rmsnorm_fwd_group_zero_constant_and_offset_rows(gpu):
+    x, w, _ = SPEC.make_inputs(4, 131072, seed=3)
+    x[0, :] = 0.0
+    x[1, :] = 2.0
+    x[2, :] += 100.0
+    y, rstd = fwd(x, w, "auto", 0, gpu)
+    np.testing.assert_allclose(rstd[0], 1.0 / np.sqrt(EPS), rtol=1e-6)
+    assert np.all(y[0] == 0.0)
+    np.testing.assert_allclose(rstd[1], 1.0 / np.sqrt(4.0 + EPS), rtol=1e-6)
+    check_fwd(x, w, y, rstd)
+
+
+def test_rmsnorm_fwd_group_repeats_and_shrinks(gpu):
+    for rows in [200, 200, 16, 1, 200]:
+        x, w, _ = SPEC.make_inputs(rows, 131072, seed=rows)
+        check_fwd(x, w, *fwd(x, w, "auto", 0, gpu))
+
+
 def test_rmsnorm_fwd_staged_rejects_wide_rows(gpu):
     x, w, _ = SPEC.make_inputs(2, 131072, seed=7)
     with pytest.raises(hip_lib.CreditError) as err:
@@ -191,7 +228,8 @@ def c3_case():
     return x, w, dy, ey, er, r32, edx, edw
 
 
-@pytest.mark.parametrize("variant,split", [("auto", 0), ("split", 4), ("read", 0)])
+@pytest.mark.parametrize("variant,split", [("auto", 0), ("split", 2), ("split", 4), ("split", 8),
+                                           ("read", 0)])
 def test_rmsnorm_fwd_full_config(gpu, c3_case, variant, split):
     x, w, dy, ey, er, *_ = c3_case
     y, rstd = fwd(x, w, variant, split, gpu)

@@ -96,6 +96,37 @@ def test_graph_replays_of_a_group_kernel_follow_their_inputs(gpu):
     del graph
 
 
+def test_graph_replays_of_the_forward_group_pipeline(gpu):
+    """rmsnorm_fwd AUTO at 64 x 131072: the forward group pipeline (8
+    members), captured once with a caller workspace, replayed with new x."""
+    rows, cols = 64, 131072
+    print(f"rmsnorm_fwd graph rows={rows} cols={cols}", flush=True)
+    x, w, _ = (t.to(gpu) for t in WORKLOADS["rmsnorm_fwd"].make_inputs(rows, cols, seed=13))
+    ws = _workspace("rmsnorm_fwd", rows, cols, gpu)
+    y, rstd = hip_lib.allocate_outputs("rmsnorm_fwd", (x, w))
+    hip_lib.rmsnorm_fwd(x, w, y, rstd, hip_lib.RMSNORM_EPS, hip_lib.make_cfg(workspace=ws))
+    torch.cuda.synchronize()
+    rpg, shape = _expected_rows_per_group(rows, 8)
+    assert shape["threads"] == 512 + 64
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):  # the config takes the capture stream
+        hip_lib.rmsnorm_fwd(x, w, y, rstd, hip_lib.RMSNORM_EPS, hip_lib.make_cfg(workspace=ws))
+    gen = torch.Generator().manual_seed(6)
+    for replay in range(4):
+        x.copy_(torch.randn(rows, cols, generator=gen) * (1 + replay))
+        before = _seq(ws)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (y.clone(), rstd.clone())
+        ry, rr = hip_lib.allocate_outputs("rmsnorm_fwd", (x, w))
+        hip_lib.rmsnorm_fwd(x, w, ry, rr, hip_lib.RMSNORM_EPS, hip_lib.make_cfg())
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], ry) and torch.equal(got[1], rr), f"replay {replay}"
+        assert _seq(ws) == before + rpg
+        hip_lib.check_watchdog(hip_lib.make_cfg(workspace=ws))
+    del graph
+
+
 def test_graph_replays_of_the_allocation_free_backward(gpu):
     """credit_rmsnorm_bwd_bf16_noalloc at 64 x 65536, split 8 (16 rows or
     fewer per group, inside the 16-row slot ring), captured once and
