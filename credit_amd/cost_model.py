@@ -38,7 +38,9 @@ L2-resident workspace.  The terms become:
   is measured with the exchanges back to back (credit_control_overhead, at
   the launch's own block size and LDS), so it is charged only beyond
   depth x the compulsory stream time.  0 for the barrier-synchronised slice
-  kernels.
+  kernels.  The depth is the one of the kernel the split runs (v3: per
+  split factor, from the workload's planner rules; v2 had one depth per
+  workload).
 
 ``estimate()`` keeps the reference's signature and result shape so the
 runner's summary logic (dsmem_eval/runner.py:444-620) carries over.
@@ -64,7 +66,7 @@ class WorkloadModelSpec(Protocol):
     barrier_count: int
 
 
-MODEL_VERSION = "cdna4-onchip-fill-exchange-v2"
+MODEL_VERSION = "cdna4-onchip-fill-exchange-v3"
 
 # Register staging budget of one 1024-lane workgroup: 64 VGPRs of data per
 # lane (the rest of the 512-entry file holds addresses and accumulators).
@@ -220,6 +222,8 @@ def estimate(
 
     control = max(control_overhead_ms, 0.0)
     depth = getattr(spec, "split_pipeline_depth", 0)
+    if callable(depth):
+        depth = depth(cols, split)
     hidden_sync_ms = min(control + l2_exchange_ms, depth * remaining_ms)
     delta = (saved_reread_ms + fill_gain_ms - (control + l2_exchange_ms - hidden_sync_ms)
              - lds_replay_ms)

@@ -59,12 +59,12 @@ class WorkloadSpec:
     # for compute-bound work.
     stream_mix: tuple[int, int] = (0, 0)
     # Row-steps by which this build's SPLIT kernel publishes a row's partial
-    # ahead of waiting for its total: 2 for the group pipelines (RMSNorm
-    # backward, softmax forward and backward: data waves publish row i+2 and
-    # finish row i while a communication wave polls), 0 for the
-    # barrier-synchronised slice kernels.  The cost model hides that much of
-    # the exchange behind the stream.
-    split_pipeline_depth: int = 0
+    # ahead of waiting for its total (the group pipelines' DEPTH: data waves
+    # publish row i+DEPTH and finish row i while a communication wave polls),
+    # 0 for the barrier-synchronised slice kernels; an int, or a function of
+    # (cols, split) where the split factor decides which kernel runs.  The
+    # cost model hides that much of the exchange behind the stream.
+    split_pipeline_depth: int | Callable[[int, int], int] = 0
 
     @property
     def barrier_count(self) -> int:
@@ -203,6 +203,41 @@ def make_pearson_inputs(rows, cols, g):
 FP32_TOL = (1.0e-6, 1.0e-5)
 BF16_TOL = (1.0e-2, 1.0e-2)
 
+def _member_vectors(cols: int, split: int, elems: int) -> int:
+    """Vectors (16 bytes, `elems` elements each) per member of a P-way
+    split, as the library's planners divide a row (ceil(nvec / P))."""
+    nvec = cols // elems
+    return -(-nvec // max(split, 1))
+
+
+def _rmsnorm_fwd_depth(cols: int, split: int) -> int:
+    """csrc/rmsnorm.hip fwd_takes_group: members of 1025-2048 vectors (at
+    most 32) run the forward group pipeline (DEPTH 4); others the slice
+    kernel."""
+    chunk = _member_vectors(cols, split, 8)
+    members = -(-(cols // 8) // chunk)
+    return 4 if 1024 < chunk <= 2048 and members <= 32 else 0
+
+
+def _softmax_fwd_depth(cols: int, split: int) -> int:
+    """csrc/softmax.hip kFwdGroup: the 512-lane 8-vector shape (members of
+    3841-4096 vectors) parks rows and publishes 4 steps ahead; the other
+    group shapes 2."""
+    return 4 if _member_vectors(cols, split, 4) > 3840 else 2
+
+
+def _softmax_bwd_depth(cols: int, split: int) -> int:
+    """csrc/softmax.hip kBwdGroup: the 512-lane 4-vector shape (members of
+    1025-2048 vectors) parks rows and publishes 4 steps ahead; the others 2."""
+    return 4 if _member_vectors(cols, split, 4) > 1024 else 2
+
+
+def _layernorm_bwd_bf16_depth(cols: int, split: int) -> int:
+    """csrc/lnbwd.hip: SPLIT of at most 16 members of at most 1024 vectors
+    runs the bf16 group pipeline (DEPTH 4); others the slice kernel."""
+    return 4 if split <= 16 and _member_vectors(cols, split, 8) <= 1024 else 0
+
+
 WORKLOADS: dict[str, WorkloadSpec] = {
     "row_sum_max": WorkloadSpec(
         name="row_sum_max",
@@ -254,6 +289,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         reductions_per_stage=(1,),
         staged_max_cols=65536,
         stream_mix=(1, 1),
+        split_pipeline_depth=_rmsnorm_fwd_depth,
     ),
     "rmsnorm_bwd": WorkloadSpec(
         name="rmsnorm_bwd",
@@ -270,7 +306,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=4,
         reductions_per_stage=(1,),
         staged_max_cols=8192,
-        split_pipeline_depth=2,
+        split_pipeline_depth=4,
         stream_mix=(2, 1),
     ),
     # C3's forward and backward in one call (credit_rmsnorm_fwd_bwd_bf16):
@@ -302,7 +338,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=4,
         reductions_per_stage=(2,),
         staged_max_cols=65536,
-        split_pipeline_depth=2,
+        split_pipeline_depth=_softmax_fwd_depth,
         stream_mix=(1, 1),
     ),
     "softmax_bwd": WorkloadSpec(
@@ -320,7 +356,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         staged_bytes_per_element=8,
         reductions_per_stage=(1,),
         staged_max_cols=32768,
-        split_pipeline_depth=2,
+        split_pipeline_depth=_softmax_bwd_depth,
         stream_mix=(2, 1),
     ),
     "ffn": WorkloadSpec(
@@ -422,6 +458,7 @@ WORKLOADS: dict[str, WorkloadSpec] = {
         reductions_per_stage=(2, 2),
         staged_max_cols=32768,
         stream_mix=(2, 1),
+        split_pipeline_depth=_layernorm_bwd_bf16_depth,
     ),
     "softmax_logits_backward": WorkloadSpec(
         name="softmax_logits_backward",

@@ -59,22 +59,44 @@ def test_estimate_delta_is_sum_of_terms():
 
 
 def test_pipelined_split_hides_at_most_depth_stream_steps_of_sync():
-    """The group pipelines (split_pipeline_depth 2) hide control + exchange
-    up to twice the compulsory stream time; a barrier-synchronised slice
+    """The group pipelines hide control + exchange up to DEPTH times the
+    compulsory stream time (the softmax forward's parked 512-lane shape at
+    C4: 16 members of 4096 vectors, DEPTH 4); a barrier-synchronised slice
     kernel (depth 0) hides none.  A control overhead beyond that is charged."""
     prof = make_device_profile(PARSED)
     piped = dataclasses.replace(WORKLOADS["softmax_fwd"], rows=512)
     flat = dataclasses.replace(piped, split_pipeline_depth=0)
+    assert piped.split_pipeline_depth(262144, 16) == 4
     for ctl in (0.001, 0.05, 5.0):
         a = cost_model.estimate(piped, 262144, 16, ctl, prof, baseline_ms=0.3, rows=512)
         b = cost_model.estimate(flat, 262144, 16, ctl, prof, baseline_ms=0.3, rows=512)
         sync = a.control_overhead_ms + a.l2_exchange_ms
         remaining = 0.3 - a.saved_reread_ms
         assert b.hidden_sync_ms == 0.0
-        assert a.hidden_sync_ms == pytest.approx(min(sync, 2 * remaining))
+        assert a.hidden_sync_ms == pytest.approx(min(sync, 4 * remaining))
         assert a.predicted_delta_ms - b.predicted_delta_ms == pytest.approx(a.hidden_sync_ms)
     assert cost_model.estimate(piped, 262144, 16, 5.0, prof, baseline_ms=0.3,
                                rows=512).predicted_profitable is False
+
+
+@pytest.mark.parametrize("name,cols,split,depth", [
+    ("rmsnorm_fwd", 131072, 8, 4),             # 2048 vectors per member: group pipeline
+    ("rmsnorm_fwd", 131072, 2, 0),             # 8192: slice kernel
+    ("rmsnorm_fwd", 131072, 16, 0),            # 1024: slice kernel
+    ("rmsnorm_fwd", 65544, 5, 4),              # 1639 (the last member 1637)
+    ("layernorm_backward_bf16", 65536, 8, 4),  # 1024 vectors, 8 members
+    ("layernorm_backward_bf16", 65536, 2, 0),  # 4096 vectors: slice kernel
+    ("layernorm_backward_bf16", 262144, 32, 0),  # more than 16 members
+    ("softmax_fwd", 262144, 16, 4),            # 4096 f32x4: the parked shape
+    ("softmax_fwd", 262144, 32, 2),
+    ("softmax_bwd", 262144, 32, 4),            # 2048 f32x4: the parked shape
+    ("softmax_bwd", 262144, 64, 2),
+    ("rmsnorm_bwd", 131072, 16, 4),
+    ("row_sum_max", 65536, 4, 0),
+])
+def test_pipeline_depth_follows_the_kernel_each_split_runs(name, cols, split, depth):
+    d = WORKLOADS[name].split_pipeline_depth
+    assert (d(cols, split) if callable(d) else d) == depth
 
 
 def test_rows_wider_than_staging_save_rereads():
