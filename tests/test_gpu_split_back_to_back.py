@@ -81,14 +81,31 @@ def test_layernorm_bwd_back_to_back(gpu, split):
     np.testing.assert_allclose(dx.cpu().numpy(), expect, **FP32)
 
 
-@pytest.mark.parametrize("split", [2, 8])
-def test_rmsnorm_fwd_back_to_back(gpu, split):
-    x, w, _ = WORKLOADS["rmsnorm_bwd"].make_inputs(2048, 16384, seed=7)
+def test_layernorm_bwd_bf16_group_back_to_back(gpu):
+    """The bf16 group pipeline (AUTO at 65536 columns: 8 members of 1024
+    vectors, rows published four steps ahead), 64 rows per group."""
+    x, dy, gamma = WORKLOADS["layernorm_backward_bf16"].make_inputs(2048, 65536, seed=6)
+    ins = [t.to(gpu) for t in (x, dy, gamma)]
+    dx = torch.empty_like(ins[0])
+    cfg = hip_lib.make_cfg()
+    print("layernorm_backward_bf16 auto (2048, 65536)", flush=True)
+    queue(lambda: hip_lib.layernorm_backward(*ins, dx, 1e-5, cfg))
+    expect = ref.layernorm_backward(x.float().numpy(), dy.float().numpy(),
+                                    gamma.float().numpy(), 1e-5)
+    np.testing.assert_allclose(dx.float().cpu().numpy(), expect, **BF16)
+
+
+@pytest.mark.parametrize("rows,cols,variant,split", [
+    (2048, 16384, "split", 2), (2048, 16384, "split", 8),
+    (512, 131072, "auto", 0),   # the forward group pipeline, 8 members
+])
+def test_rmsnorm_fwd_back_to_back(gpu, rows, cols, variant, split):
+    x, w, _ = WORKLOADS["rmsnorm_bwd"].make_inputs(rows, cols, seed=7)
     xs, ws_ = x.to(gpu), w.to(gpu)
     y = torch.empty_like(xs)
     rstd = torch.empty(x.shape[0], device=gpu)
-    cfg = hip_lib.make_cfg("split", split)
-    print(f"rmsnorm_fwd split {split}", flush=True)
+    cfg = hip_lib.make_cfg(variant, split)
+    print(f"rmsnorm_fwd {variant} {split} ({rows}, {cols})", flush=True)
     queue(lambda: hip_lib.rmsnorm_fwd(xs, ws_, y, rstd, 1e-6, cfg))
     ey, er = ref.rmsnorm_fwd(x.float().numpy(), w.float().numpy(), 1e-6)
     np.testing.assert_allclose(rstd.cpu().numpy(), er, **FP32)
