@@ -426,6 +426,12 @@ __device__ __forceinline__ void rmsnorm_group_body(
 
   if (__builtin_amdgcn_readfirstlane(tid) >= THREADS) {
     // ---- communication wave: poll every row's exchange in order ----
+    // The backward's communication wave runs at raised issue priority: 146.5
+    // -> 144.9 us at C3 (two sessions of three alternating runs).  The same
+    // raise slowed the fused forward + backward by 7.5%, the forward group
+    // pipeline by 5% and the softmax group kernels by 3-5%, which keep the
+    // default priority.
+    if constexpr (!FUSED) __builtin_amdgcn_s_setprio(3);
     for (int k = r0; k < r1; ++k) {
       const uint32_t bits = split_poll(g, k - r0, K);
       const double dot = split_wave_sum(bits, members, 0);
