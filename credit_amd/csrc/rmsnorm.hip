@@ -1265,7 +1265,8 @@ extern "C" int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uin
     return check_launch("rmsnorm_fwd_read_kernel");
   }
   if (fwd_takes_group(plan)) {
-    auto fn = rmsnorm_fwd_group_kernel<kFwdGroupThreads, kFwdGroupVpt, 4, 1>;
+    static_assert(kFwdGroupThreads == 512 && kFwdGroupVpt == 4, "the instance below");
+    auto fn = rmsnorm_fwd_group_kernel<512, 4, 4, 1>;
     int64_t fit = 0;
     int dispensers = 0;
     CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(fn), kFwdGroupThreads + kWave, 0,
