@@ -109,8 +109,11 @@ constexpr int kDispensers = plan::kMaxDispensers;  // ticket dispensers at most 
 constexpr int kDispenserStride = 16;     // one 64-byte line each
 constexpr int kGroupCounterBase = kDispensers * kDispenserStride;  // first group counter
 constexpr int kGroupCounterStride = 16;  // one 64-byte line per group counter
+// The counter area's last line holds the row-ticket counter of the queued
+// group pipelines (returned to zero by the launch that draws its last ticket).
+constexpr int kQueueWord = kCounterSlots - 16;
 constexpr int kMaxGroupsPerLaunch =
-    (kCounterSlots - kGroupCounterBase) / kGroupCounterStride / kDispensers * kDispensers;
+    (kQueueWord - kGroupCounterBase) / kGroupCounterStride / kDispensers * kDispensers;
 // Groups of a split launch are padded to a multiple of kDispensers (the
 // padding groups exit at once).
 inline int64_t padded_groups(int64_t groups) {

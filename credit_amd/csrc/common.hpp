@@ -227,6 +227,12 @@ __device__ __forceinline__ u32x4 buffer_load(buffer_rsrc_t r, uint32_t offset) {
 __device__ __forceinline__ void buffer_store_nt(buffer_rsrc_t r, uint32_t offset, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, offset, 0, kBufferNt);
 }
+// Atomic add through a buffer resource, returning the old value; lanes
+// whose offset falls outside the resource change nothing (and read 0).
+__device__ __forceinline__ uint32_t queue_add(buffer_rsrc_t q, uint32_t off, uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(static_cast<int>(v), q, off, 0, 0));
+}
 __device__ __forceinline__ void buffer_store(buffer_rsrc_t r, uint32_t offset, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, offset, 0, 0);
 }
@@ -539,6 +545,42 @@ __device__ __forceinline__ uint32_t split_poll(const SplitGroup& g, int stage, i
     __builtin_amdgcn_s_sleep(1);
   }
   return lane < n ? static_cast<uint32_t>(word) : 0u;
+}
+
+// Row tickets of a queued group pipeline travel as raw 32-bit words in
+// member 0's value-k slot of the row step they name (a ticket does not fit a
+// float).  One thread publishes; every member's communication wave reads the
+// word back with split_poll_word.
+__device__ __forceinline__ void split_publish_word(const SplitGroup& g, int stage, int k,
+                                                   uint32_t bits) {
+  const uint64_t word = (static_cast<uint64_t>(plan::stage_tag(g.epoch, stage)) << 32) | bits;
+  uint64_t* slot = g.slots + (static_cast<size_t>(stage % g.ring) * g.k_values + k) * g.members;
+  __hip_atomic_store(slot, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One whole wave: wait until member 0's value-k slot of `stage` carries the
+// stage's tag and return its payload (the same in every lane).  Bounded like
+// split_poll: on expiry it raises the watchdog and returns what it read.
+__device__ __forceinline__ uint32_t split_poll_word(const SplitGroup& g, int stage, int k) {
+  const uint64_t* slot =
+      g.slots + (static_cast<size_t>(stage % g.ring) * g.k_values + k) * g.members;
+  const uint32_t tag = plan::stage_tag(g.epoch, stage);
+  uint32_t spins = 0;
+  for (;;) {
+    const uint64_t word = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(word >> 32));
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(word));
+    if (hi == tag) return lo;
+    if (++spins > g.spin_limit) {
+      if ((threadIdx.x & (kWave - 1)) == 0) {
+        __hip_atomic_store(g.watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (g.host_flag != nullptr)
+          __hip_atomic_store(g.host_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+      return lo;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
 }
 
 // One whole wave, after split_poll: sum of partial k over the members in

@@ -605,36 +605,104 @@ __device__ __forceinline__ void rmsnorm_group_body(
 // DEPTH / AHEAD 4 / 1 95.1 us, 3 / 2 95.7, 3 / 1 99.0, 2 / 2 103.0, 2 / 1
 // 104.7; 16 members of 1024 vectors (VPT 2) 4 / 2 118.7, 2 / 1 110.8; 5 / 1
 // and 4 / 2 at VPT 4 exceed the 168 VGPRs of a 9-wave workgroup.
+//
+// Rows come from a launch-wide ticket queue, so that groups which run
+// faster take more rows (a group sits on one XCD, and with a fixed share
+// per group the XCDs' ends were 5-10 us apart at C3, the slowest XCD
+// changing from call to call).  Row step i < L takes the fixed row g + i G;
+// step i >= L takes row L G + t for a ticket t that member 0's ticket wave
+// (a tenth wave) draws from the counter once stage i - L - 1 is released,
+// waits for and publishes in member 0's value-1 slot of stage i; every
+// member's communication wave reads it at stage i - L + 2 and writes the
+// row id into an LDS ring (RR entries) before it releases that stage, which
+// is one stage before the data waves issue the row's loads (step i - DEPTH
+// - AHEAD).  The first ticket naming no row ends the group's steps.  One
+// ticket is drawn per row step processed, so a launch draws exactly `rows`
+// tickets and the wave that draws value rows - 1 returns the counter to
+// zero.  C3: 94.8-95.1 -> 93.8-94.1 us (three alternating runs).
 template <int THREADS, int VPT, int DEPTH, int AHEAD>
 __device__ __forceinline__ void rmsnorm_fwd_group_body(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
     float* __restrict__ rstd_out, int rows, int cols, int chunk, int members,
-    int rows_per_group, float eps, SplitArgs sa) {
+    int rows_per_group, float eps, SplitArgs sa, uint32_t* __restrict__ queue) {
   constexpr int NW = THREADS / kWave;
   constexpr int NB = DEPTH + AHEAD + 1;
   constexpr int RING = DEPTH + 2 <= 4 ? 4 : 8;
+  constexpr int L = DEPTH + AHEAD + 3;
+  constexpr int RR = 16;
   static_assert(DEPTH >= 1 && AHEAD >= 1 && DEPTH + 2 <= 8, "pipeline depth");
   static_assert(2 * DEPTH + 1 < kGroupSlotRing, "device slot ring too short for DEPTH");
+  static_assert(L + DEPTH < RR && L + DEPTH < kGroupSlotRing, "ticket rings");
   __shared__ double red[RING][NW];
   __shared__ float ring[RING];
   __shared__ uint32_t arrivals[RING];
   __shared__ uint32_t ready;
+  __shared__ int rowid[RR];
   const int tid = threadIdx.x;
   if (tid < RING) arrivals[tid] = 0;
   if (tid == 0) ready = 0;
-  const SplitGroup g = split_join(sa, members, 1);
+  const SplitGroup g = split_join(sa, members, 2);
   const int G = (rows + rows_per_group - 1) / rows_per_group;
   if (g.group >= G) return;
+  // The group's fixed rows g + i G, i < n_fixed (all L of them when rows >= L G).
   const int r1 = (rows - g.group + G - 1) / G;
-  auto row_of = [&](int i) { return g.group + i * G; };
+  const int n_fixed = r1 < L ? r1 : L;
+  const int64_t first = static_cast<int64_t>(L) * G;  // the row of ticket 0
+  auto row_of = [&](int i) {
+    return i < L ? (i < n_fixed ? g.group + i * G : rows) : rowid[i % RR];
+  };
+  // Step i has a row (the steps that do are a prefix).
+  auto live = [&](int i) { return row_of(i) < rows; };
   const int nvec = cols >> 3;
   const int v0 = g.member * chunk;
   const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
   const uint32_t slice_bytes = static_cast<uint32_t>(vlen) * 16u;
+  if (__builtin_amdgcn_readfirstlane(tid) >= THREADS + kWave) {
+    // ---- ticket wave (member 0) ----
+    if (g.member == 0) {
+      // A 4-byte resource that only lane 0 addresses.
+      const buffer_rsrc_t qrs = make_rsrc(queue, 4u);
+      const uint32_t qoff = static_cast<uint32_t>(tid - THREADS - kWave) * 4u;
+      int n = n_fixed < L ? n_fixed : INT32_MAX;  // the group's steps, once known
+      for (int k = 0; k < n; ++k) {
+        // Bounded like the exchange polls: the communication wave releases
+        // every stage of the group unless one of its own waits expired.
+        uint32_t spins = 0;
+        while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+               static_cast<uint32_t>(k)) {
+          if (++spins > g.spin_limit) {
+            if (tid == THREADS + kWave)
+              __hip_atomic_store(g.watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+        const uint32_t t = __builtin_amdgcn_readfirstlane(queue_add(qrs, qoff, 1u));
+        if (first + t >= rows && n == INT32_MAX) n = k + L;
+        if (tid == THREADS + kWave) split_publish_word(g, k + L, 1, t);
+        queue_add(qrs, t == static_cast<uint32_t>(rows - 1) ? qoff : 4u,
+                  0u - static_cast<uint32_t>(rows));
+      }
+    }
+    return;
+  }
   if (__builtin_amdgcn_readfirstlane(tid) >= THREADS) {
-    for (int k = 0; k < r1; ++k) {
+    // ---- communication wave: stage k's total into ring, the row of step
+    // k + L - 2 into rowid, then the release of stage k ----
+    int n = n_fixed < L ? n_fixed : INT32_MAX;
+    for (int k = 0; k < n; ++k) {
       const uint32_t bits = split_poll(g, k, 1);
       const double ssq = split_wave_sum(bits, members, 0);
+      const int j = k + L - 2;
+      if (j >= L) {
+        int row = rows;
+        if (n == INT32_MAX) {
+          const int64_t r = first + split_poll_word(g, j, 1);
+          if (r < rows) row = static_cast<int>(r);
+          else n = j;
+        }
+        if (tid == THREADS) rowid[j % RR] = row;
+      }
       if (tid == THREADS) {
         ring[k % RING] = static_cast<float>(1.0 / __builtin_sqrt(ssq / cols + eps));
         __hip_atomic_store(&ready, static_cast<uint32_t>(k + 1), __ATOMIC_RELEASE,
@@ -652,10 +720,10 @@ __device__ __forceinline__ void rmsnorm_fwd_group_body(
   };
   Row b[NB];
   auto load_row = [&](Row& b, int r) {
-    const bool live = r < r1;
+    const bool on = live(r);
     const size_t off =
-        static_cast<size_t>(row_of(live ? r : 0)) * cols + 8 * static_cast<size_t>(v0);
-    const buffer_rsrc_t xs = make_rsrc(x + off, live ? slice_bytes : 0u);
+        static_cast<size_t>(on ? row_of(r) : 0) * cols + 8 * static_cast<size_t>(v0);
+    const buffer_rsrc_t xs = make_rsrc(x + off, on ? slice_bytes : 0u);
 #pragma unroll
     for (int k = 0; k < VPT; ++k) b.x[k] = buffer_load_nt(xs, lane_off + k * kStride);
   };
@@ -692,46 +760,47 @@ __device__ __forceinline__ void rmsnorm_fwd_group_body(
 #pragma unroll
     for (int q = 0; q < VPT; ++q) __asm__ volatile("" : "+v"(b.x[q]));
     const float rs = ring[slot];
-    const size_t off = static_cast<size_t>(row_of(r)) * cols + 8 * static_cast<size_t>(v0);
+    const int row = row_of(r);
+    const size_t off = static_cast<size_t>(row) * cols + 8 * static_cast<size_t>(v0);
     const buffer_rsrc_t out = make_rsrc(y + off, slice_bytes);
 #pragma unroll
     for (int q = 0; q < VPT; ++q)
       buffer_store_nt(out, lane_off + q * kStride, scale8(b.x[q], wk[q], rs));
     // Lane 0 of member 0 writes rstd (a 4-byte resource; other lanes fall outside it).
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(rs),
-                                          make_rsrc(rstd_out + row_of(r), g.member == 0 ? 4u : 0u),
+                                          make_rsrc(rstd_out + row, g.member == 0 ? 4u : 0u),
                                           static_cast<uint32_t>(tid) * 4u, 0, 0);
   };
   auto step = [&]<int S>(std::integral_constant<int, S>, int i) {
     load_row(b[(S + DEPTH + AHEAD) % NB], i + DEPTH + AHEAD);
     __builtin_amdgcn_sched_barrier(0);
-    if (i + DEPTH < r1) publish_row(b[(S + DEPTH) % NB], i + DEPTH);
+    if (live(i + DEPTH)) publish_row(b[(S + DEPTH) % NB], i + DEPTH);
     finish_row(b[S], i, wait_total(i));
   };
   [&]<int... J>(std::integer_sequence<int, J...>) {
     (load_row(b[J], J), ...);
   }(std::make_integer_sequence<int, DEPTH + AHEAD>{});
   [&]<int... J>(std::integer_sequence<int, J...>) {
-    ((J < r1 ? publish_row(b[J], J) : void()), ...);
+    ((live(J) ? publish_row(b[J], J) : void()), ...);
   }(std::make_integer_sequence<int, DEPTH>{});
+  // The group's steps end at the first step without a row; step i's row is
+  // known once the data waves are past step i - DEPTH - AHEAD - 1.
   int i = 0;
-  for (; i + NB - 1 < r1; i += NB)
+  for (bool go = true; go; i += NB)
     [&]<int... S>(std::integer_sequence<int, S...>) {
-      (step(std::integral_constant<int, S>{}, i + S), ...);
+      (((go = go && live(i + S)) ? step(std::integral_constant<int, S>{}, i + S) : void()), ...);
     }(std::make_integer_sequence<int, NB>{});
-  [&]<int... S>(std::integer_sequence<int, S...>) {
-    ((i + S < r1 ? step(std::integral_constant<int, S>{}, i + S) : void()), ...);
-  }(std::make_integer_sequence<int, NB - 1>{});
 }
 
+// THREADS data lanes, the communication wave and the ticket wave.
 template <int THREADS, int VPT, int DEPTH, int AHEAD>
-__global__ __launch_bounds__(THREADS + kWave)
+__global__ __launch_bounds__(THREADS + 2 * kWave)
 __attribute__((amdgpu_waves_per_eu(3, 8))) void rmsnorm_fwd_group_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
     float* __restrict__ rstd_out, int rows, int cols, int chunk, int members,
-    int rows_per_group, float eps, SplitArgs sa) {
+    int rows_per_group, float eps, SplitArgs sa, uint32_t* __restrict__ queue) {
   rmsnorm_fwd_group_body<THREADS, VPT, DEPTH, AHEAD>(x, w, y, rstd_out, rows, cols, chunk,
-                                                     members, rows_per_group, eps, sa);
+                                                     members, rows_per_group, eps, sa, queue);
   split_leave(sa);
 }
 
@@ -1267,9 +1336,10 @@ extern "C" int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uin
   if (fwd_takes_group(plan)) {
     static_assert(kFwdGroupThreads == 512 && kFwdGroupVpt == 4, "the instance below");
     auto fn = rmsnorm_fwd_group_kernel<512, 4, 4, 1>;
+    const int threads = kFwdGroupThreads + 2 * kWave;
     int64_t fit = 0;
     int dispensers = 0;
-    CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(fn), kFwdGroupThreads + kWave, 0,
+    CREDIT_TRY(coresident_groups(reinterpret_cast<const void*>(fn), threads, 0,
                                  plan.members, &fit, &dispensers));
     if (fit == 0)
       return set_error(CREDIT_ERR_UNSUPPORTED,
@@ -1277,18 +1347,22 @@ extern "C" int credit_rmsnorm_fwd_bf16(const uint16_t* x, const uint16_t* w, uin
                        plan.members);
     const int64_t g = fit < padded_groups(rows) ? fit : padded_groups(rows);
     const int64_t rows_per_group = (rows + g - 1) / g;
-    if (rows_per_group > int64_t{credit::plan::kMaxLaunchStages})
-      return set_error(CREDIT_ERR_BAD_SHAPE, "rmsnorm_fwd: %lld rows per group",
-                       static_cast<long long>(rows_per_group));
     const int64_t grid_groups = padded_groups((rows + rows_per_group - 1) / rows_per_group);
+    // A group may take every row (the queue); its tags run L < 16 steps
+    // past its last.
+    const int64_t stages = rows + 16;
+    if (stages > int64_t{credit::plan::kMaxLaunchStages})
+      return set_error(CREDIT_ERR_BAD_SHAPE, "rmsnorm_fwd: %lld rows",
+                       static_cast<long long>(rows));
     SplitWorkspace ws;
-    CREDIT_TRY(acquire_split_workspace(cfg, grid_groups, plan.members, 1, kGroupSlotRing, 0, &ws));
+    CREDIT_TRY(acquire_split_workspace(cfg, grid_groups, plan.members, 2, kGroupSlotRing, 0, &ws));
     const uint32_t total = static_cast<uint32_t>(grid_groups * plan.members);
-    hipLaunchKernelGGL(fn, dim3(total), dim3(kFwdGroupThreads + kWave), 0, stream, x, w, y, rstd,
+    hipLaunchKernelGGL(fn, dim3(total), dim3(threads), 0, stream, x, w, y, rstd,
                        static_cast<int>(rows), c, static_cast<int>(plan.chunk), plan.members,
                        static_cast<int>(rows_per_group), eps,
-                       make_split_args(ws, total, static_cast<uint32_t>(rows_per_group),
-                                       kGroupSlotRing, dispensers));
+                       make_split_args(ws, total, static_cast<uint32_t>(stages), kGroupSlotRing,
+                                       dispensers),
+                       ws.counters + kQueueWord);
     return check_launch("rmsnorm_fwd_group_kernel");
   }
   const FwdPick* pick = pick_for(kFwd, plan.chunk);

@@ -224,7 +224,9 @@ int credit_layernorm_bwd_bf16(const uint16_t* x, const uint16_t* dy, const uint1
  * 139-140).  Variants: STAGED (row in one workgroup's VGPRs, cols <= 65536),
  * SPLIT (cfg->split workgroups per row exchanging one partial; at most 32
  * members of 8193-16384 columns each run a barrier-free pipeline of rows,
- * other splits a slice kernel of at most 65536 columns per member), READ
+ * whose row groups take rows from a launch-wide ticket counter in the
+ * workspace's counter area, so faster groups take more rows; other splits
+ * a slice kernel of at most 65536 columns per member), READ
  * (two streaming passes; any shape).  AUTO: STAGED when the row fits, else
  * the pipeline when at most 8 members of <= 16384 columns cover the row
  * (C3: 8 members), else the smallest slice SPLIT that holds it; READ for

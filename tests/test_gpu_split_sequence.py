@@ -24,6 +24,9 @@ from credit_amd.workloads import WORKLOADS
 pytestmark = pytest.mark.gpu
 
 SEQ_BYTE = 64           # header word of the tag sequence
+# The row-ticket counter of the queued forward group pipeline: the counter
+# area (256 bytes in, 262144 words) ends with its 64-byte line.
+QUEUE_BYTE = 256 + 4 * (262144 - 16)
 SLOT_OFFSET = 256 + (1 << 20)
 SLOT_BYTES = 4 << 20
 SEQ_LIMIT = 0xFFFFFFFF - (1 << 30)
@@ -31,6 +34,10 @@ SEQ_LIMIT = 0xFFFFFFFF - (1 << 30)
 
 def _seq(ws: torch.Tensor) -> int:
     return int(ws[SEQ_BYTE:SEQ_BYTE + 4].cpu().view(torch.int32).item()) & 0xFFFFFFFF
+
+
+def _queue(ws: torch.Tensor) -> int:
+    return int(ws[QUEUE_BYTE:QUEUE_BYTE + 4].cpu().view(torch.int32).item()) & 0xFFFFFFFF
 
 
 def _set_seq(ws: torch.Tensor, value: int) -> None:
@@ -106,8 +113,8 @@ def test_graph_replays_of_the_forward_group_pipeline(gpu):
     y, rstd = hip_lib.allocate_outputs("rmsnorm_fwd", (x, w))
     hip_lib.rmsnorm_fwd(x, w, y, rstd, hip_lib.RMSNORM_EPS, hip_lib.make_cfg(workspace=ws))
     torch.cuda.synchronize()
-    rpg, shape = _expected_rows_per_group(rows, 8)
-    assert shape["threads"] == 512 + 64
+    _, shape = _expected_rows_per_group(rows, 8)
+    assert shape["threads"] == 512 + 128  # data lanes, communication and ticket waves
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):  # the config takes the capture stream
         hip_lib.rmsnorm_fwd(x, w, y, rstd, hip_lib.RMSNORM_EPS, hip_lib.make_cfg(workspace=ws))
@@ -122,7 +129,8 @@ def test_graph_replays_of_the_forward_group_pipeline(gpu):
         hip_lib.rmsnorm_fwd(x, w, ry, rr, hip_lib.RMSNORM_EPS, hip_lib.make_cfg())
         torch.cuda.synchronize()
         assert torch.equal(got[0], ry) and torch.equal(got[1], rr), f"replay {replay}"
-        assert _seq(ws) == before + rpg
+        assert _seq(ws) == before + rows + 16  # a queued group may take every row
+        assert _queue(ws) == 0, f"replay {replay}"
         hip_lib.check_watchdog(hip_lib.make_cfg(workspace=ws))
     del graph
 
@@ -277,3 +285,39 @@ def test_control_overhead_takes_the_split_launchs_shape(gpu):
                                             threads=shape["threads"])
     assert 0 < plain < 1 and 0 < split < 5
     hip_lib.check_watchdog()
+
+
+@pytest.mark.parametrize("rows", [1, 7, 64, 255, 256, 257, 300, 1024, 1500])
+def test_forward_row_queue_returns_to_zero(gpu, rows):
+    """rmsnorm_fwd AUTO at 131072 columns takes rows from a launch-wide
+    ticket counter (one draw per row processed; the drawer of the last
+    ticket resets it).  After every launch the counter reads zero, every row
+    matches the oracle, and repeated launches give identical outputs
+    whichever group took which row.  Row counts below, at and above the
+    groups' fixed share (8 steps per group)."""
+    from oracle import reference as ref
+
+    cols = 131072
+    print(f"rmsnorm_fwd queue rows={rows}", flush=True)
+    xc, wc, _ = WORKLOADS["rmsnorm_fwd"].make_inputs(rows, cols, seed=rows)
+    x, w = xc.to(gpu), wc.to(gpu)
+    ws = _workspace("rmsnorm_fwd", rows, cols, gpu)
+    y, rstd = hip_lib.allocate_outputs("rmsnorm_fwd", (x, w))
+    first = None
+    for call in range(3):
+        y.fill_(float("nan"))
+        rstd.fill_(float("nan"))
+        hip_lib.rmsnorm_fwd(x, w, y, rstd, hip_lib.RMSNORM_EPS, hip_lib.make_cfg(workspace=ws))
+        torch.cuda.synchronize()
+        assert hip_lib.last_split_shape()["threads"] == 512 + 128
+        assert _queue(ws) == 0, f"call {call}"
+        got = (y.clone(), rstd.clone())
+        if first is None:
+            first = got
+            ey, er = ref.rmsnorm_fwd(xc.float().numpy(), wc.float().numpy(),
+                                     hip_lib.RMSNORM_EPS)
+            np.testing.assert_allclose(got[1].cpu().numpy(), er, rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(got[0].float().cpu().numpy(), ey, rtol=1e-2, atol=1e-2)
+        else:
+            assert torch.equal(got[0], first[0]) and torch.equal(got[1], first[1]), call
+    hip_lib.check_watchdog(hip_lib.make_cfg(workspace=ws))
