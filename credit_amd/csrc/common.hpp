@@ -583,6 +583,62 @@ __device__ __forceinline__ uint32_t split_poll_word(const SplitGroup& g, int sta
   }
 }
 
+// ---- Row-ticket queue of the group pipelines ----
+// Row step i < L of group g takes the fixed row g + i G; step i >= L takes
+// row first + t (first = L G), t a ticket drawn from a launch-wide counter.
+// Member 0's ticket wave (queue_ticket_wave) draws step k + L's ticket once
+// the communication wave has released stage k - 1 and publishes it in
+// member 0's value-vk slot of stage k + L; every member's communication
+// wave takes it at stage k (queue_take_row, for step k + L - 2) and hands
+// the row id to its data waves through LDS before releasing the stage.  The
+// first ticket naming no row ends the group's steps.  One ticket is drawn
+// per row step processed, so a launch draws exactly `rows` tickets and the
+// wave that draws value rows - 1 (its group's last draw) returns the counter
+// to zero for the next launch.
+
+// One whole wave (member 0's ticket wave).  n_fixed: the group's fixed
+// steps (fewer than L: it has no other).  *ready: the communication wave's
+// released-stage count.  Bounded like the exchange polls.
+__device__ __forceinline__ void queue_ticket_wave(const SplitGroup& g, uint32_t* queue,
+                                                  const uint32_t* ready, int n_fixed, int L,
+                                                  int64_t first, int rows, int vk) {
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  const buffer_rsrc_t qrs = make_rsrc(queue, 4u);  // lane 0 alone addresses it
+  const uint32_t qoff = lane * 4u;
+  int n = n_fixed < L ? n_fixed : INT32_MAX;  // the group's steps, once known
+  for (int k = 0; k < n; ++k) {
+    uint32_t spins = 0;
+    while (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+           static_cast<uint32_t>(k)) {
+      if (++spins > g.spin_limit) {
+        if (lane == 0) __hip_atomic_store(g.watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    const uint32_t t = __builtin_amdgcn_readfirstlane(queue_add(qrs, qoff, 1u));
+    if (first + t >= rows && n == INT32_MAX) n = k + L;
+    if (lane == 0) split_publish_word(g, k + L, vk, t);
+    queue_add(qrs, t == static_cast<uint32_t>(rows - 1) ? qoff : 4u,
+              0u - static_cast<uint32_t>(rows));
+  }
+}
+
+// One whole wave (a communication wave at stage k): the row of step
+// k + L - 2, or rows when that step has none, or -1 when it is a fixed step
+// (k < 2).  *n: the group's step count, INT32_MAX while open; set here at
+// the first ticket that names no row.
+__device__ __forceinline__ int queue_take_row(const SplitGroup& g, int k, int L, int64_t first,
+                                              int rows, int vk, int* n) {
+  const int j = k + L - 2;
+  if (j < L) return -1;
+  if (*n != INT32_MAX) return rows;
+  const int64_t r = first + split_poll_word(g, j, vk);
+  if (r < rows) return static_cast<int>(r);
+  *n = j;
+  return rows;
+}
+
 // One whole wave, after split_poll: sum of partial k over the members in
 // member order (fp64), the same value in every lane.
 __device__ __forceinline__ double split_wave_sum(uint32_t bits, int members, int k) {

@@ -658,32 +658,7 @@ __device__ __forceinline__ void rmsnorm_fwd_group_body(
   const int vlen = nvec - v0 < chunk ? nvec - v0 : chunk;
   const uint32_t slice_bytes = static_cast<uint32_t>(vlen) * 16u;
   if (__builtin_amdgcn_readfirstlane(tid) >= THREADS + kWave) {
-    // ---- ticket wave (member 0) ----
-    if (g.member == 0) {
-      // A 4-byte resource that only lane 0 addresses.
-      const buffer_rsrc_t qrs = make_rsrc(queue, 4u);
-      const uint32_t qoff = static_cast<uint32_t>(tid - THREADS - kWave) * 4u;
-      int n = n_fixed < L ? n_fixed : INT32_MAX;  // the group's steps, once known
-      for (int k = 0; k < n; ++k) {
-        // Bounded like the exchange polls: the communication wave releases
-        // every stage of the group unless one of its own waits expired.
-        uint32_t spins = 0;
-        while (__hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
-               static_cast<uint32_t>(k)) {
-          if (++spins > g.spin_limit) {
-            if (tid == THREADS + kWave)
-              __hip_atomic_store(g.watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return;
-          }
-          __builtin_amdgcn_s_sleep(1);
-        }
-        const uint32_t t = __builtin_amdgcn_readfirstlane(queue_add(qrs, qoff, 1u));
-        if (first + t >= rows && n == INT32_MAX) n = k + L;
-        if (tid == THREADS + kWave) split_publish_word(g, k + L, 1, t);
-        queue_add(qrs, t == static_cast<uint32_t>(rows - 1) ? qoff : 4u,
-                  0u - static_cast<uint32_t>(rows));
-      }
-    }
+    if (g.member == 0) queue_ticket_wave(g, queue, &ready, n_fixed, L, first, rows, 1);
     return;
   }
   if (__builtin_amdgcn_readfirstlane(tid) >= THREADS) {
@@ -693,17 +668,9 @@ __device__ __forceinline__ void rmsnorm_fwd_group_body(
     for (int k = 0; k < n; ++k) {
       const uint32_t bits = split_poll(g, k, 1);
       const double ssq = split_wave_sum(bits, members, 0);
-      const int j = k + L - 2;
-      if (j >= L) {
-        int row = rows;
-        if (n == INT32_MAX) {
-          const int64_t r = first + split_poll_word(g, j, 1);
-          if (r < rows) row = static_cast<int>(r);
-          else n = j;
-        }
-        if (tid == THREADS) rowid[j % RR] = row;
-      }
+      const int row = queue_take_row(g, k, L, first, rows, 1, &n);
       if (tid == THREADS) {
+        if (row >= 0) rowid[(k + L - 2) % RR] = row;
         ring[k % RING] = static_cast<float>(1.0 / __builtin_sqrt(ssq / cols + eps));
         __hip_atomic_store(&ready, static_cast<uint32_t>(k + 1), __ATOMIC_RELEASE,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
