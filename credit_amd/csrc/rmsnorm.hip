@@ -619,7 +619,8 @@ __device__ __forceinline__ void rmsnorm_group_body(
 // - AHEAD).  The first ticket naming no row ends the group's steps.  One
 // ticket is drawn per row step processed, so a launch draws exactly `rows`
 // tickets and the wave that draws value rows - 1 returns the counter to
-// zero.  C3: 94.8-95.1 -> 93.8-94.1 us (three alternating runs).
+// zero.  C3: 94.8-95.1 -> 93.8-94.1 us and 94.7-94.9 -> 94.3-94.5 us
+// (alternating runs on two boxes).
 template <int THREADS, int VPT, int DEPTH, int AHEAD>
 __device__ __forceinline__ void rmsnorm_fwd_group_body(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
