@@ -611,7 +611,11 @@ __device__ __forceinline__ void queue_ticket_wave(const SplitGroup& g, uint32_t*
     while (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
            static_cast<uint32_t>(k)) {
       if (++spins > g.spin_limit) {
-        if (lane == 0) __hip_atomic_store(g.watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) {
+          __hip_atomic_store(g.watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (g.host_flag != nullptr)
+            __hip_atomic_store(g.host_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
         return;
       }
       __builtin_amdgcn_s_sleep(1);
